@@ -1,0 +1,232 @@
+/*
+ * prana_hip.h — C ABI of libprana_hip, the MI355X (gfx950) backend for the
+ * inference hot path of pariharshyamu/Prana.
+ *
+ * The reference exposes this path as a Rust crate API (prana-kernels
+ * src/lib.rs:35-54, re-exported by prana-model). Each entry point below
+ * replaces one of those functions (cited per declaration) on device-resident
+ * buffers; the model-level entry points replace prana-model's Model / KvCache /
+ * forward / prefill / forward_batch / generate / generate_speculative.
+ *
+ * Conventions (the reference's own C-ABI idiom, prana-cactus sys.rs:5-9):
+ *   - every function returns int: 0 = success, negative = failure;
+ *   - prana_last_error() returns a thread-local message for the last failure;
+ *   - shape/layout violations (assert! panics in the reference, e.g.
+ *     matmul.rs:31-39, kquant.rs:166-169, attention.rs:138-143) come back as
+ *     PRANA_ERR_INVALID instead of aborting; nothing throws across the ABI;
+ *   - kernel entry points take DEVICE pointers and a stream (NULL = the
+ *     library's stream) and are asynchronous; model entry points take host
+ *     buffers and synchronise before returning.
+ *
+ * Numerics: results are bit-identical to the reference's scalar tier
+ * (integer block dots exact, f32 folds in the reference's order); the only
+ * entry point with a different order is prana_attention_decode_splitk.
+ */
+#ifndef PRANA_HIP_H
+#define PRANA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRANA_OK 0
+#define PRANA_ERR_INVALID (-1)
+#define PRANA_ERR_HIP (-2)
+#define PRANA_ERR_NOMEM (-3)
+#define PRANA_ERR_UNSUPPORTED (-4)
+
+typedef void *prana_stream_t; /* hipStream_t */
+
+/* ---------------------------------------------------------------- runtime */
+/* Thread-local message of the last failure (prana-cactus sys.rs:210
+ * cactus_get_last_error idiom). Never NULL. */
+const char *prana_last_error(void);
+/* Select the device and initialise tables (idempotent). */
+int prana_init(int device);
+/* Minimal device-memory helpers so any FFI (ctypes, cgo, JNI) can drive the
+ * kernel entry points without a HIP binding of its own. */
+int prana_device_alloc(size_t bytes, void **out);
+int prana_device_free(void *p);
+int prana_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int prana_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int prana_memset_d(void *dst, int value, size_t bytes);
+int prana_synchronize(void);
+
+/* ---------------------------------------------------------------- matrices */
+/* ggml tensor type ids, as the reference's GGUF loader uses them
+ * (gguf.rs:33-38). PRANA_Q8_F32 is QuantMatrix with f32 block scales
+ * (matmul.rs:21-28, produced by quantize_q8 / QuantMatrix::from_parts). */
+enum prana_ggml_type {
+  PRANA_F32 = 0,
+  PRANA_F16 = 1,
+  PRANA_Q4_0 = 2,
+  PRANA_Q8_0 = 8,
+  PRANA_Q4_K = 12,
+  PRANA_Q6_K = 14,
+};
+
+typedef struct prana_mat *prana_mat_t;
+
+/* Upload a rows x cols matrix from GGUF tensor bytes (ggml block layout).
+ * Replaces Gguf::linear (gguf.rs:271-305) -> QuantMatrix::from_parts
+ * (matmul.rs:34-39) / KQuantMatrix::from_raw (kquant.rs:166-183) / Linear::F32.
+ * Q8_0/Q4_0 need cols % 32 == 0, Q4_K/Q6_K cols % 256 == 0. F16 tensors become
+ * dense f32 (the reference dequantizes them, gguf.rs:217-221). */
+int prana_mat_create(int ggml_type, size_t rows, size_t cols, const void *host_bytes, size_t nbytes,
+                     prana_mat_t *out);
+/* QuantMatrix::from_parts with f32 scales (matmul.rs:34-39). */
+int prana_mat_create_q8(size_t rows, size_t cols, const int8_t *q, const float *scales, prana_mat_t *out);
+int prana_mat_destroy(prana_mat_t m);
+/* rows, cols, device storage kind and the bytes a GEMV streams. */
+int prana_mat_info(prana_mat_t m, size_t *rows, size_t *cols, int *kind, size_t *stream_bytes);
+
+/* ---------------------------------------------------------------- kernels */
+/* quantize_acts (matmul.rs:105-127) for n_rows rows of k (k % 32 == 0):
+ * q[n_rows*k] i8, scales/sums[n_rows*k/32]. */
+int prana_quantize_acts(const float *x, size_t n_rows, size_t k, int8_t *q, float *scales, int32_t *sums,
+                        prana_stream_t stream);
+/* Linear::apply for n_tokens rows (checkpoint.rs:94-100): matmul_f32
+ * (matmul.rs:150-157) / matmul_q8_f32 (162-178) / matmul_kquant_f32
+ * (kquant.rs:323-333). x[n_tokens*cols] -> out[n_tokens*rows]. Quantizes the
+ * activations itself; scratch comes from the library. */
+int prana_matmul(prana_mat_t w, const float *x, size_t n_tokens, float *out, prana_stream_t stream);
+/* Linear::apply_prefill (checkpoint.rs:140-146): matmul_q8_prefill
+ * (matmul.rs:185-187) / matmul_kquant_prefill (kquant.rs:368-370) over
+ * already-quantized rows; x is read only for F32 matrices. */
+int prana_matmul_prefill(prana_mat_t w, const float *x, const int8_t *q, const float *scales, const int32_t *sums,
+                         size_t n_tokens, float *out, prana_stream_t stream);
+/* The exact i32 block dots behind every term (Q4_0: s - 8*sum_a; Q4_K: the
+ * nibble dot per 32-group; Q6_K: per 16-element sub-block). isums is
+ * [n_tokens][rows][terms], terms = cols/32 (cols/16 for Q6_K). */
+int prana_matmul_block_sums(prana_mat_t w, const int8_t *q, const int32_t *sums, size_t n_tokens, int32_t *isums,
+                            prana_stream_t stream);
+/* Embedding::row (checkpoint.rs:169-174) for n tokens (device ids), times
+ * scale when scale != 1 (infer.rs:155-159). out[n*cols]. */
+int prana_embed_rows(prana_mat_t table, const uint32_t *tokens, size_t n, float scale, float *out,
+                     prana_stream_t stream);
+/* rmsnorm (norms.rs:9-23), rows x dim. */
+int prana_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float eps, float *out,
+                  prana_stream_t stream);
+/* silu in place (norms.rs:27-31); gelu_tanh in place (norms.rs:35-41). */
+int prana_silu(float *x, size_t n, prana_stream_t stream);
+int prana_gelu_tanh(float *x, size_t n, prana_stream_t stream);
+/* softmax (norms.rs:44-56) over each of `rows` rows of n. */
+int prana_softmax(const float *in, size_t rows, size_t n, float *out, prana_stream_t stream);
+/* rope_interleaved (attention.rs:90-101) / rope_neox (107-121) in place on
+ * n_rows rows of row_len at positions pos0 + i; rope (attention.rs:59-80) is
+ * rope_neox with pos0 = 0 over [seq, n_heads*head_dim]. */
+int prana_rope_interleaved(float *x, size_t n_rows, size_t row_len, size_t pos0, size_t head_dim, float theta,
+                           prana_stream_t stream);
+int prana_rope_neox(float *x, size_t n_rows, size_t row_len, size_t pos0, size_t head_dim, float theta,
+                    prana_stream_t stream);
+/* f16_kv_write (attention.rs:47-52). */
+int prana_kv_write_f16(uint16_t *cache, size_t first_row, size_t kv_stride, const float *src, size_t n,
+                       prana_stream_t stream);
+/* attention_decode (attention.rs:129-160) over the f16 cache rows 0..=pos. */
+int prana_attention_decode(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t pos,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, float *out, prana_stream_t stream);
+/* attention_verify (attention.rs:296-333): seq rows at pos0.. over the cache. */
+int prana_attention_verify(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t pos0,
+                           size_t seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, float *out,
+                           prana_stream_t stream);
+/* attention (prefill, attention.rs:236-284): causal over f32 K/V. */
+int prana_attention_prefill(const float *q, const float *k, const float *v, size_t seq, size_t n_heads,
+                            size_t n_kv_heads, size_t head_dim, float *out, prana_stream_t stream);
+/* Greedy argmax (infer.rs:560-568 / sampler.rs:40-48) of each row. */
+int prana_argmax(const float *logits, size_t rows, size_t n, uint32_t *out_idx, prana_stream_t stream);
+/* f32_to_f16 / f16_to_f32 (lib.rs:57-113) elementwise. */
+int prana_f32_to_f16(const float *in, size_t n, uint16_t *out, prana_stream_t stream);
+int prana_f16_to_f32(const uint16_t *in, size_t n, float *out, prana_stream_t stream);
+/* The device expf behind silu/softmax (f32::exp, norms.rs:29,49). */
+int prana_expf(const float *in, size_t n, float *out, prana_stream_t stream);
+
+/* ---------------------------------------------------------------- model */
+/* Config (checkpoint.rs:32-56). rope_neox: 0 interleaved / 1 NeoX;
+ * act: 0 silu / 1 gelu_tanh. */
+typedef struct prana_config {
+  size_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len, head_dim;
+  float rope_theta, norm_eps, emb_scale;
+  int rope_neox;
+  int act;
+} prana_config;
+
+typedef struct prana_model *prana_model_t;
+typedef struct prana_cache *prana_cache_t;
+
+int prana_model_create(const prana_config *cfg, prana_model_t *out);
+int prana_model_destroy(prana_model_t m);
+/* Attach one tensor by its GGUF name (gguf.rs:381-437): token_embd.weight,
+ * output_norm.weight, output.weight, blk.N.{attn_norm,attn_q,attn_k,attn_v,
+ * attn_output,ffn_norm,ffn_gate,ffn_down,ffn_up}.weight, blk.N.attn_{q,k,v}.bias.
+ * dims follow ggml order (dims[0] = cols). */
+int prana_model_set_tensor(prana_model_t m, const char *name, int ggml_type, const uint64_t *dims, int n_dims,
+                           const void *bytes, size_t nbytes);
+/* Validate that every required tensor is present and shapes agree. */
+int prana_model_finalize(prana_model_t m);
+/* Total bytes of projection + head weights streamed per decoded token. */
+int prana_model_stream_bytes(prana_model_t m, size_t *bytes);
+
+/* KvCache::with_len (infer.rs:37-44): f16 K/V per layer, min(positions, seq_len) rows. */
+int prana_cache_create(prana_model_t m, size_t positions, prana_cache_t *out);
+int prana_cache_destroy(prana_cache_t c);
+/* Copy layer `layer`'s K or V (which = 0/1) rows [0, rows) to the host. */
+int prana_cache_read(prana_cache_t c, size_t layer, int which, size_t rows, uint16_t *host_out);
+
+/* forward / forward_impl (infer.rs:134-211): one token at pos; logits
+ * (host, vocab floats) written when need_logits. */
+int prana_forward(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, int need_logits,
+                  float *logits_host);
+/* prefill (infer.rs:220-286): tokens at positions 0..n. */
+int prana_prefill(prana_model_t m, prana_cache_t c, const uint32_t *tokens, size_t n);
+/* forward_batch (infer.rs:296-374): n tokens at pos0..; logits [n][vocab]. */
+int prana_forward_batch(prana_model_t m, prana_cache_t c, const uint32_t *tokens, size_t n, size_t pos0,
+                        float *logits_host);
+
+/* Greedy decode of n_steps tokens over an existing cache: feed `token` at pos,
+ * then each argmax at the next position — the sampled part of generate's loop
+ * (infer.rs:729-763) with the ids kept on the device; out[n_steps] gets the
+ * sampled ids at the end. No stop ids. */
+int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, size_t n_steps, uint32_t *out);
+
+/* GEMV launch profiling for roofline accounting: while on, every model GEMV is
+ * bracketed by HIP events on its stream; read returns launches, summed kernel
+ * seconds and summed algorithmic weight bytes since the last reset.
+ * No counterpart in the reference (its timing is PRANA_TIMING, infer.rs:81-130). */
+int prana_gemv_profile(int on);
+int prana_gemv_profile_read(size_t *launches, double *seconds, double *bytes, int reset);
+
+typedef struct prana_gen_stats {
+  size_t prompt_tokens, generated_tokens, proposed, accepted;
+  double seconds, prefill_seconds, decode_seconds;
+} prana_gen_stats;
+
+/* generate (infer.rs:696-771) with the greedy sampler; stops = ids for which
+ * Tokenize::is_stop holds (tokenizer.rs:174-176). out has room for `steps`. */
+int prana_generate(prana_model_t m, const uint32_t *prompt, size_t p, size_t steps, const uint32_t *stops,
+                   size_t n_stops, uint32_t *out, size_t *n_out, prana_gen_stats *stats);
+/* generate_speculative (infer.rs:581-690), greedy, draft length k. */
+int prana_generate_speculative(prana_model_t target, prana_model_t draft, const uint32_t *prompt, size_t p,
+                               size_t steps, size_t k, const uint32_t *stops, size_t n_stops, uint32_t *out,
+                               size_t *n_out, prana_gen_stats *stats);
+
+/* ---------------------------------------------------------------- synthetic weights */
+/* Block encoders for synthetic models (the reference has no Q8_0/Q4_0 encoder;
+ * Q4_K/Q6_K follow scripts/convert-to-gguf.py:29-89). src is rows x cols f32;
+ * out receives ggml bytes. */
+int prana_quantize_tensor(int ggml_type, const float *src, size_t rows, size_t cols, void *out, size_t nbytes);
+/* Seeded N(0, sigma) values (xorshift64* streams + Box-Muller), n floats. */
+int prana_synth_normal(uint64_t seed, float sigma, float *out, size_t n);
+/* prana_synth_normal values for a rows x cols tensor, encoded straight into
+ * ggml bytes (no f32 copy of the whole tensor is materialised). */
+int prana_synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, void *out,
+                       size_t nbytes);
+/* Bytes of a ggml tensor of the given type and element count. */
+size_t prana_ggml_nbytes(int ggml_type, size_t n_elems);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PRANA_HIP_H */

@@ -1,0 +1,392 @@
+"""prana_amd — MI355X (gfx950) backend for the inference hot path of
+pariharshyamu/Prana.
+
+Host-side mirror of the reference's interface (prana-kernels / prana-model) over
+the C ABI of libprana_hip (include/prana_hip.h): Matrix ~ Linear, Model ~
+prana_model::Model, Cache ~ KvCache, and forward / prefill / forward_batch /
+generate / generate_speculative with the reference's argument meanings.
+
+All compute runs in the HIP library; there is no CPU fallback in this package.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import GenStats, PranaConfig, PranaError, check, load
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+GGML_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+
+def _ptr(a):
+    return C.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def init():
+    check(load().prana_init(0))
+
+
+class DeviceArray:
+    """A device buffer holding one numpy-typed array (test/bench plumbing)."""
+
+    def __init__(self, shape, dtype):
+        init()
+        self.shape = tuple(shape) if isinstance(shape, (tuple, list)) else (shape,)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = C.c_void_p()
+        check(load().prana_device_alloc(self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    @classmethod
+    def from_host(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        if d.nbytes:
+            check(load().prana_memcpy_h2d(d.ptr, _ptr(a), d.nbytes))
+        return d
+
+    def to_host(self):
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            check(load().prana_memcpy_d2h(_ptr(out), self.ptr, self.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr is not None and self.ptr.value:
+            load().prana_device_free(self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def ggml_nbytes(ggml_type, n_elems):
+    return int(load().prana_ggml_nbytes(ggml_type, n_elems))
+
+
+def quantize_tensor(ggml_type, x):
+    """Encode an f32 [rows, cols] array into ggml block bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    out = np.zeros(ggml_nbytes(ggml_type, rows * cols), np.uint8)
+    check(load().prana_quantize_tensor(ggml_type, _ptr(x), rows, cols, _ptr(out), out.nbytes))
+    return out
+
+
+def synth_normal(seed, sigma, n):
+    out = np.empty(n, np.float32)
+    check(load().prana_synth_normal(seed, sigma, _ptr(out), n))
+    return out
+
+
+def synth_tensor(ggml_type, rows, cols, seed, sigma):
+    out = np.empty(ggml_nbytes(ggml_type, rows * cols), np.uint8)
+    check(load().prana_synth_tensor(ggml_type, rows, cols, seed, sigma, _ptr(out), out.nbytes))
+    return out
+
+
+class Matrix:
+    """A device-resident weight matrix (Linear / QuantMatrix / KQuantMatrix)."""
+
+    def __init__(self, ggml_type, rows, cols, raw):
+        init()
+        raw = np.ascontiguousarray(raw)
+        h = C.c_void_p()
+        check(load().prana_mat_create(ggml_type, rows, cols, _ptr(raw), raw.nbytes, C.byref(h)))
+        self.h, self.rows, self.cols, self.ggml_type = h, rows, cols, ggml_type
+
+    @classmethod
+    def q8_parts(cls, q, scales):
+        """QuantMatrix::from_parts (matmul.rs:34-39)."""
+        self = cls.__new__(cls)
+        init()
+        q = np.ascontiguousarray(q, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        rows, cols = q.shape
+        h = C.c_void_p()
+        check(load().prana_mat_create_q8(rows, cols, _ptr(q), _ptr(scales), C.byref(h)))
+        self.h, self.rows, self.cols, self.ggml_type = h, rows, cols, None
+        return self
+
+    def info(self):
+        r, c, k, b = C.c_size_t(), C.c_size_t(), C.c_int(), C.c_size_t()
+        check(load().prana_mat_info(self.h, C.byref(r), C.byref(c), C.byref(k), C.byref(b)))
+        return {"rows": r.value, "cols": c.value, "kind": k.value, "stream_bytes": b.value}
+
+    def apply(self, x):
+        """Linear::apply over n token rows: x [n, cols] f32 -> [n, rows]."""
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        n = x.shape[0]
+        dx = DeviceArray.from_host(x)
+        dout = DeviceArray((n, self.rows), np.float32)
+        check(load().prana_matmul(self.h, dx.ptr, n, dout.ptr, None))
+        return dout.to_host()
+
+    def apply_prefill(self, q, sa, sums, x=None):
+        """Linear::apply_prefill over already-quantized rows."""
+        n = q.shape[0]
+        dq, ds, dm = DeviceArray.from_host(q), DeviceArray.from_host(sa), DeviceArray.from_host(sums)
+        dx = DeviceArray.from_host(x) if x is not None else None
+        dout = DeviceArray((n, self.rows), np.float32)
+        check(load().prana_matmul_prefill(self.h, dx.ptr if dx else None, dq.ptr, ds.ptr, dm.ptr, n, dout.ptr, None))
+        return dout.to_host()
+
+    def block_sums(self, q, sums):
+        n = q.shape[0]
+        terms = self.cols // 16 if self.ggml_type == Q6_K else self.cols // 32
+        dq, dm = DeviceArray.from_host(q), DeviceArray.from_host(sums)
+        dout = DeviceArray((n, self.rows, terms), np.int32)
+        check(load().prana_matmul_block_sums(self.h, dq.ptr, dm.ptr, n, dout.ptr, None))
+        return dout.to_host()
+
+    def embed_rows(self, tokens, scale=1.0):
+        t = DeviceArray.from_host(np.asarray(tokens, np.uint32))
+        dout = DeviceArray((len(tokens), self.cols), np.float32)
+        check(load().prana_embed_rows(self.h, t.ptr, len(tokens), scale, dout.ptr, None))
+        return dout.to_host()
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_mat_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- kernels
+def quantize_acts(x):
+    """quantize_acts (matmul.rs:105-127) of each row of x."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    n, k = x.shape
+    dx = DeviceArray.from_host(x)
+    q, s, m = DeviceArray((n, k), np.int8), DeviceArray((n, k // 32), np.float32), DeviceArray((n, k // 32), np.int32)
+    check(load().prana_quantize_acts(dx.ptr, n, k, q.ptr, s.ptr, m.ptr, None))
+    return q.to_host(), s.to_host(), m.to_host()
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    rows, dim = x.shape
+    dx, dw, do = DeviceArray.from_host(x), DeviceArray.from_host(np.asarray(w, np.float32)), DeviceArray(x.shape,
+                                                                                                     np.float32)
+    check(load().prana_rmsnorm(dx.ptr, dw.ptr, rows, dim, eps, do.ptr, None))
+    return do.to_host()
+
+
+def _inplace(fn, x):
+    x = np.ascontiguousarray(x, np.float32)
+    d = DeviceArray.from_host(x)
+    check(fn(d.ptr, x.size, None))
+    return d.to_host()
+
+
+def silu(x):
+    return _inplace(load().prana_silu, x)
+
+
+def gelu_tanh(x):
+    return _inplace(load().prana_gelu_tanh, x)
+
+
+def softmax(x):
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    d, o = DeviceArray.from_host(x), DeviceArray(x.shape, np.float32)
+    check(load().prana_softmax(d.ptr, x.shape[0], x.shape[1], o.ptr, None))
+    return o.to_host()
+
+
+def expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    d, o = DeviceArray.from_host(x), DeviceArray(x.shape, np.float32)
+    check(load().prana_expf(d.ptr, x.size, o.ptr, None))
+    return o.to_host()
+
+
+def rope(x, pos0, head_dim, theta, neox):
+    """rope_interleaved / rope_neox on each row of x at positions pos0 + i."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    d = DeviceArray.from_host(x)
+    fn = load().prana_rope_neox if neox else load().prana_rope_interleaved
+    check(fn(d.ptr, x.shape[0], x.shape[1], pos0, head_dim, theta, None))
+    return d.to_host()
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    d, o = DeviceArray.from_host(x), DeviceArray(x.shape, np.uint16)
+    check(load().prana_f32_to_f16(d.ptr, x.size, o.ptr, None))
+    return o.to_host()
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    d, o = DeviceArray.from_host(h), DeviceArray(h.shape, np.float32)
+    check(load().prana_f16_to_f32(d.ptr, h.size, o.ptr, None))
+    return o.to_host()
+
+
+def kv_write_f16(cache, first_row, kv_stride, src):
+    """f16_kv_write on a host copy of the cache; returns the updated cache."""
+    dc = DeviceArray.from_host(np.asarray(cache, np.uint16))
+    ds = DeviceArray.from_host(np.asarray(src, np.float32))
+    check(load().prana_kv_write_f16(dc.ptr, first_row, kv_stride, ds.ptr, ds.shape[0] if ds.shape else 0, None))
+    return dc.to_host()
+
+
+def attention_decode(q, kc, vc, pos, n_heads, n_kv_heads, head_dim):
+    dq, dk, dv = (DeviceArray.from_host(np.asarray(q, np.float32)), DeviceArray.from_host(np.asarray(kc, np.uint16)),
+                  DeviceArray.from_host(np.asarray(vc, np.uint16)))
+    do = DeviceArray((n_heads * head_dim,), np.float32)
+    check(load().prana_attention_decode(dq.ptr, dk.ptr, dv.ptr, pos, n_heads, n_kv_heads, head_dim, do.ptr, None))
+    return do.to_host()
+
+
+def attention_verify(q, kc, vc, pos0, seq, n_heads, n_kv_heads, head_dim):
+    dq, dk, dv = (DeviceArray.from_host(np.asarray(q, np.float32)), DeviceArray.from_host(np.asarray(kc, np.uint16)),
+                  DeviceArray.from_host(np.asarray(vc, np.uint16)))
+    do = DeviceArray((seq, n_heads * head_dim), np.float32)
+    check(load().prana_attention_verify(dq.ptr, dk.ptr, dv.ptr, pos0, seq, n_heads, n_kv_heads, head_dim, do.ptr,
+                                        None))
+    return do.to_host()
+
+
+def attention_prefill(q, k, v, seq, n_heads, n_kv_heads, head_dim):
+    dq, dk, dv = (DeviceArray.from_host(np.asarray(q, np.float32)), DeviceArray.from_host(np.asarray(k, np.float32)),
+                  DeviceArray.from_host(np.asarray(v, np.float32)))
+    do = DeviceArray((seq, n_heads * head_dim), np.float32)
+    check(load().prana_attention_prefill(dq.ptr, dk.ptr, dv.ptr, seq, n_heads, n_kv_heads, head_dim, do.ptr, None))
+    return do.to_host()
+
+
+def argmax(logits):
+    x = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
+    d, o = DeviceArray.from_host(x), DeviceArray((x.shape[0],), np.uint32)
+    check(load().prana_argmax(d.ptr, x.shape[0], x.shape[1], o.ptr, None))
+    return o.to_host()
+
+
+# ---------------------------------------------------------------- model
+class Model:
+    """prana_model::Model over device buffers; tensors attached by GGUF name."""
+
+    def __init__(self, config, tensors=None):
+        init()
+        self.config = config
+        self.cfg = PranaConfig(**config)
+        h = C.c_void_p()
+        check(load().prana_model_create(C.byref(self.cfg), C.byref(h)))
+        self.h = h
+        if tensors:
+            for name, (ty, dims, raw) in tensors.items():
+                self.set_tensor(name, ty, dims, raw)
+            self.finalize()
+
+    def set_tensor(self, name, ggml_type, dims, raw):
+        raw = np.ascontiguousarray(raw)
+        d = (C.c_uint64 * len(dims))(*dims)
+        check(load().prana_model_set_tensor(self.h, name.encode(), ggml_type, d, len(dims), _ptr(raw), raw.nbytes))
+
+    def finalize(self):
+        check(load().prana_model_finalize(self.h))
+
+    def stream_bytes(self):
+        b = C.c_size_t()
+        check(load().prana_model_stream_bytes(self.h, C.byref(b)))
+        return b.value
+
+    def cache(self, positions):
+        return Cache(self, positions)
+
+    def generate(self, prompt, steps, stops=()):
+        prompt = np.asarray(prompt, np.uint32)
+        stops = np.asarray(stops, np.uint32)
+        out = np.zeros(max(steps, 1), np.uint32)
+        n = C.c_size_t()
+        st = GenStats()
+        check(load().prana_generate(self.h, _ptr(prompt), len(prompt), steps, _ptr(stops) if len(stops) else None,
+                                    len(stops), _ptr(out), C.byref(n), C.byref(st)))
+        return out[: n.value].copy(), st
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_model_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def gemv_profile(on):
+    check(load().prana_gemv_profile(1 if on else 0))
+
+
+def gemv_profile_read(reset=True):
+    n, s, b = C.c_size_t(), C.c_double(), C.c_double()
+    check(load().prana_gemv_profile_read(C.byref(n), C.byref(s), C.byref(b), 1 if reset else 0))
+    return n.value, s.value, b.value
+
+
+def generate_speculative(target, draft, prompt, steps, k, stops=()):
+    prompt = np.asarray(prompt, np.uint32)
+    stops = np.asarray(stops, np.uint32)
+    out = np.zeros(max(steps, 1), np.uint32)
+    n = C.c_size_t()
+    st = GenStats()
+    check(load().prana_generate_speculative(target.h, draft.h, _ptr(prompt), len(prompt), steps, k,
+                                            _ptr(stops) if len(stops) else None, len(stops), _ptr(out), C.byref(n),
+                                            C.byref(st)))
+    return out[: n.value].copy(), st
+
+
+class Cache:
+    """KvCache::with_len (infer.rs:37-44)."""
+
+    def __init__(self, model, positions):
+        self.model = model
+        h = C.c_void_p()
+        check(load().prana_cache_create(model.h, positions, C.byref(h)))
+        self.h = h
+        self.len = min(positions, model.config["seq_len"])
+
+    def forward(self, token, pos, need_logits=True):
+        v = self.model.config["vocab_size"]
+        logits = np.zeros(v, np.float32)
+        check(load().prana_forward(self.model.h, self.h, int(token), pos, 1 if need_logits else 0, _ptr(logits)))
+        return logits if need_logits else None
+
+    def prefill(self, tokens):
+        t = np.asarray(tokens, np.uint32)
+        check(load().prana_prefill(self.model.h, self.h, _ptr(t), len(t)))
+
+    def forward_batch(self, tokens, pos0):
+        t = np.asarray(tokens, np.uint32)
+        v = self.model.config["vocab_size"]
+        logits = np.zeros((len(t), v), np.float32)
+        check(load().prana_forward_batch(self.model.h, self.h, _ptr(t), len(t), pos0, _ptr(logits)))
+        return logits
+
+    def decode(self, token, pos, n_steps):
+        """Greedy decode n_steps tokens feeding `token` at `pos` (ids stay on device)."""
+        out = np.zeros(max(n_steps, 1), np.uint32)
+        check(load().prana_decode(self.model.h, self.h, int(token), pos, n_steps, _ptr(out)))
+        return out[:n_steps]
+
+    def read(self, layer, which, rows):
+        kv = self.model.config["n_kv_heads"] * self.model.config["head_dim"]
+        out = np.zeros((rows, kv), np.uint16)
+        check(load().prana_cache_read(self.h, layer, which, rows, _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_cache_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass

@@ -1,0 +1,131 @@
+"""ctypes binding of libprana_hip (include/prana_hip.h).
+
+The library is loaded from prana_amd/_build/libprana_hip.so (built in-tree by
+prana_amd/build.py). There is no fallback: if the library is missing or no GPU
+is visible, calls fail with PranaError.
+"""
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libprana_hip.so")
+
+c_size = C.c_size_t
+c_int = C.c_int
+c_void_p = C.c_void_p
+c_float = C.c_float
+c_u64 = C.c_uint64
+c_u32p = C.POINTER(C.c_uint32)
+c_u64p = C.POINTER(C.c_uint64)
+
+
+class PranaConfig(C.Structure):
+    """prana_config (checkpoint.rs:32-56)."""
+
+    _fields_ = [
+        ("dim", c_size), ("hidden_dim", c_size), ("n_layers", c_size), ("n_heads", c_size),
+        ("n_kv_heads", c_size), ("vocab_size", c_size), ("seq_len", c_size), ("head_dim", c_size),
+        ("rope_theta", c_float), ("norm_eps", c_float), ("emb_scale", c_float),
+        ("rope_neox", c_int), ("act", c_int),
+    ]
+
+
+class GenStats(C.Structure):
+    _fields_ = [
+        ("prompt_tokens", c_size), ("generated_tokens", c_size), ("proposed", c_size), ("accepted", c_size),
+        ("seconds", C.c_double), ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double),
+    ]
+
+
+class PranaError(RuntimeError):
+    pass
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "prana_last_error": (C.c_char_p, []),
+    "prana_init": (c_int, [c_int]),
+    "prana_device_alloc": (c_int, [c_size, C.POINTER(c_void_p)]),
+    "prana_device_free": (c_int, [c_void_p]),
+    "prana_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size]),
+    "prana_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size]),
+    "prana_memset_d": (c_int, [c_void_p, c_int, c_size]),
+    "prana_synchronize": (c_int, []),
+    "prana_mat_create": (c_int, [c_int, c_size, c_size, c_void_p, c_size, C.POINTER(c_void_p)]),
+    "prana_mat_create_q8": (c_int, [c_size, c_size, c_void_p, c_void_p, C.POINTER(c_void_p)]),
+    "prana_mat_destroy": (c_int, [c_void_p]),
+    "prana_mat_info": (c_int, [c_void_p, C.POINTER(c_size), C.POINTER(c_size), C.POINTER(c_int), C.POINTER(c_size)]),
+    "prana_quantize_acts": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "prana_matmul": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_matmul_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_matmul_block_sums": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_embed_rows": (c_int, [c_void_p, c_void_p, c_size, c_float, c_void_p, c_void_p]),
+    "prana_rmsnorm": (c_int, [c_void_p, c_void_p, c_size, c_size, c_float, c_void_p, c_void_p]),
+    "prana_silu": (c_int, [c_void_p, c_size, c_void_p]),
+    "prana_gelu_tanh": (c_int, [c_void_p, c_size, c_void_p]),
+    "prana_softmax": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p]),
+    "prana_rope_interleaved": (c_int, [c_void_p, c_size, c_size, c_size, c_size, c_float, c_void_p]),
+    "prana_rope_neox": (c_int, [c_void_p, c_size, c_size, c_size, c_size, c_float, c_void_p]),
+    "prana_kv_write_f16": (c_int, [c_void_p, c_size, c_size, c_void_p, c_size, c_void_p]),
+    "prana_attention_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p, c_void_p]),
+    "prana_attention_verify": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_size, c_void_p,
+                                       c_void_p]),
+    "prana_attention_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p,
+                                        c_void_p]),
+    "prana_argmax": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p]),
+    "prana_f32_to_f16": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_f16_to_f32": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_expf": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_model_create": (c_int, [C.POINTER(PranaConfig), C.POINTER(c_void_p)]),
+    "prana_model_destroy": (c_int, [c_void_p]),
+    "prana_model_set_tensor": (c_int, [c_void_p, C.c_char_p, c_int, c_u64p, c_int, c_void_p, c_size]),
+    "prana_model_finalize": (c_int, [c_void_p]),
+    "prana_model_stream_bytes": (c_int, [c_void_p, C.POINTER(c_size)]),
+    "prana_cache_create": (c_int, [c_void_p, c_size, C.POINTER(c_void_p)]),
+    "prana_cache_destroy": (c_int, [c_void_p]),
+    "prana_cache_read": (c_int, [c_void_p, c_size, c_int, c_size, c_void_p]),
+    "prana_forward": (c_int, [c_void_p, c_void_p, C.c_uint32, c_size, c_int, c_void_p]),
+    "prana_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "prana_forward_batch": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_void_p]),
+    "prana_decode": (c_int, [c_void_p, c_void_p, C.c_uint32, c_size, c_size, c_void_p]),
+    "prana_gemv_profile": (c_int, [c_int]),
+    "prana_gemv_profile_read": (c_int, [C.POINTER(c_size), C.POINTER(C.c_double), C.POINTER(C.c_double), c_int]),
+    "prana_generate": (c_int, [c_void_p, c_void_p, c_size, c_size, c_void_p, c_size, c_void_p, C.POINTER(c_size),
+                               C.POINTER(GenStats)]),
+    "prana_generate_speculative": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_void_p, c_size,
+                                           c_void_p, C.POINTER(c_size), C.POINTER(GenStats)]),
+    "prana_quantize_tensor": (c_int, [c_int, c_void_p, c_size, c_size, c_void_p, c_size]),
+    "prana_synth_normal": (c_int, [c_u64, c_float, c_void_p, c_size]),
+    "prana_synth_tensor": (c_int, [c_int, c_size, c_size, c_u64, c_float, c_void_p, c_size]),
+    "prana_ggml_nbytes": (c_size, [c_int, c_size]),
+}
+
+_lib = None
+
+
+def load():
+    """Load the in-tree library once and bind every symbol."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise PranaError(f"{LIB_PATH} is missing: build it with `python prana_amd/build.py` "
+                         "(or __graft_entry__.build())")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def check(rc):
+    if rc != 0:
+        msg = load().prana_last_error().decode(errors="replace")
+        raise PranaError(f"prana error {rc}: {msg}")
+    return rc

@@ -1,0 +1,574 @@
+// extern "C" entry points of libprana_hip (declared in include/prana_hip.h).
+// Nothing throws across this boundary: every entry point catches and turns
+// failures into status codes with a thread-local message.
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <vector>
+#include <new>
+#include <string>
+
+#include "model.h"
+
+namespace prana {
+const char* last_error_cstr();
+}
+
+using namespace prana;
+
+namespace {
+
+// Library-owned scratch for the kernel-level entry points that need
+// intermediate buffers (quantized activations, attention scores).
+struct Scratch {
+  std::mutex mu;
+  DevBuf qa, sa, sums, att;
+};
+Scratch& scratch() {
+  static Scratch s;
+  return s;
+}
+
+template <class F>
+int guard(F&& f) {
+  try {
+    return f();
+  } catch (const std::bad_alloc&) {
+    return fail(kErrNoMem, "host allocation failed");
+  } catch (const std::exception& e) {
+    return fail(kErrInvalid, std::string("internal error: ") + e.what());
+  } catch (...) {
+    return fail(kErrInvalid, "internal error");
+  }
+}
+
+#define INIT_OR_RETURN()          \
+  do {                            \
+    int rc_ = ensure_init();      \
+    if (rc_) return rc_;          \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+const char* prana_last_error(void) { return last_error_cstr(); }
+
+int prana_init(int device) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    if (device != 0) return fail(kErrUnsupported, "only device 0 is driven by this build (one GPU per process)");
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_device_alloc(size_t bytes, void** out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(out, "null out pointer");
+    *out = nullptr;
+    if (bytes == 0) return static_cast<int>(kOk);
+    PRANA_HIP(hipMalloc(out, bytes));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_device_free(void* p) {
+  return guard([&] {
+    if (p) PRANA_HIP(hipFree(p));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    if (bytes) PRANA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_HIP(hipStreamSynchronize(ctx().stream));
+    if (bytes) PRANA_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_memset_d(void* dst, int value, size_t bytes) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    if (bytes) PRANA_HIP(hipMemsetAsync(dst, value, bytes, ctx().stream));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_synchronize(void) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_HIP(hipStreamSynchronize(ctx().stream));
+    PRANA_HIP(hipDeviceSynchronize());
+    return static_cast<int>(kOk);
+  });
+}
+
+// ------------------------------------------------------------------ matrices
+int prana_mat_create(int ggml_type, size_t rows, size_t cols, const void* host_bytes, size_t nbytes,
+                     prana_mat_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(out && (host_bytes || rows * cols == 0), "null argument");
+    auto* m = new prana_mat();
+    int rc = mat_from_ggml(ggml_type, rows, cols, host_bytes, nbytes, m->m);
+    if (rc) {
+      delete m;
+      return rc;
+    }
+    *out = m;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_mat_create_q8(size_t rows, size_t cols, const int8_t* q, const float* scales, prana_mat_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(out && q && scales, "null argument");
+    auto* m = new prana_mat();
+    int rc = mat_from_q8_parts(rows, cols, q, scales, m->m);
+    if (rc) {
+      delete m;
+      return rc;
+    }
+    *out = m;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_mat_destroy(prana_mat_t m) {
+  return guard([&] {
+    delete m;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_mat_info(prana_mat_t m, size_t* rows, size_t* cols, int* kind, size_t* stream_bytes) {
+  return guard([&] {
+    PRANA_CHECK(m, "null matrix");
+    if (rows) *rows = m->m.d.rows;
+    if (cols) *cols = m->m.d.cols;
+    if (kind) *kind = m->m.d.kind;
+    if (stream_bytes) *stream_bytes = m->m.stream_bytes;
+    return static_cast<int>(kOk);
+  });
+}
+
+// ------------------------------------------------------------------ kernels
+int prana_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, float* scales, int32_t* sums,
+                        prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(k % 32 == 0, "quantize_acts: k must be a multiple of 32 (matmul.rs:106)");
+    return launch_quantize_acts(x, n_rows, k, q, scales, sums, pick_stream(stream));
+  });
+}
+
+int prana_matmul(prana_mat_t w, const float* x, size_t n_tokens, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(w, "null matrix");
+    const DevMat& d = w->m.d;
+    hipStream_t s = pick_stream(stream);
+    GemvOut o{out, d.rows, nullptr, 0};
+    if (d.kind == kKindF32) return launch_gemv(d, x, nullptr, nullptr, nullptr, n_tokens, o, s);
+    Scratch& sc = scratch();
+    std::lock_guard<std::mutex> lk(sc.mu);
+    size_t n = n_tokens * d.cols;
+    int rc;
+    if ((rc = sc.qa.ensure(n)) || (rc = sc.sa.ensure(n / 32 * 4)) || (rc = sc.sums.ensure(n / 32 * 4))) return rc;
+    if ((rc = launch_quantize_acts(x, n_tokens, d.cols, sc.qa.as<int8_t>(), sc.sa.as<float>(), sc.sums.as<int>(),
+                                   s)))
+      return rc;
+    rc = launch_gemv(d, x, sc.qa.as<int8_t>(), sc.sa.as<float>(), sc.sums.as<int>(), n_tokens, o, s);
+    if (rc) return rc;
+    // The scratch is shared: finish before another call may reuse it.
+    PRANA_HIP(hipStreamSynchronize(s));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_matmul_prefill(prana_mat_t w, const float* x, const int8_t* q, const float* scales, const int32_t* sums,
+                         size_t n_tokens, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(w, "null matrix");
+    const DevMat& d = w->m.d;
+    GemvOut o{out, d.rows, nullptr, 0};
+    return launch_gemv(d, x, q, scales, sums, n_tokens, o, pick_stream(stream));
+  });
+}
+
+int prana_matmul_block_sums(prana_mat_t w, const int8_t* q, const int32_t* sums, size_t n_tokens, int32_t* isums,
+                            prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(w, "null matrix");
+    return launch_block_isums(w->m.d, q, sums, n_tokens, isums, pick_stream(stream));
+  });
+}
+
+int prana_embed_rows(prana_mat_t table, const uint32_t* tokens, size_t n, float scale, float* out,
+                     prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(table, "null table");
+    return launch_embed(table->m.d, tokens, n, scale, out, pick_stream(stream));
+  });
+}
+
+int prana_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, float eps, float* out,
+                  prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_rmsnorm(x, w, rows, dim, eps, out, nullptr, nullptr, nullptr, pick_stream(stream));
+  });
+}
+
+int prana_silu(float* x, size_t n, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_act_mul(x, nullptr, n, 0, nullptr, nullptr, nullptr, pick_stream(stream));
+  });
+}
+
+int prana_gelu_tanh(float* x, size_t n, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_act_mul(x, nullptr, n, 1, nullptr, nullptr, nullptr, pick_stream(stream));
+  });
+}
+
+int prana_softmax(const float* in, size_t rows, size_t n, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_softmax(in, rows, n, out, pick_stream(stream));
+  });
+}
+
+namespace {
+int rope_entry(float* x, size_t n_rows, size_t row_len, size_t pos0, size_t hd, float theta, int neox, void* stream) {
+  INIT_OR_RETURN();
+  PRANA_CHECK(hd % 2 == 0 && hd > 0, "RoPE: head_dim must be even (attention.rs:91)");
+  PRANA_CHECK(row_len % hd == 0, "RoPE: row must be a whole number of heads (attention.rs:92)");
+  size_t half = hd / 2, npos = pos0 + n_rows;
+  std::vector<float> tab(npos * half * 2);
+  for (size_t m = 0; m < half; m++) {
+    float freq = std::pow(theta, -(2.0f * static_cast<float>(m)) / static_cast<float>(hd));
+    for (size_t p = pos0; p < npos; p++) {
+      float ang = static_cast<float>(p) * freq;
+      tab[(p * half + m) * 2] = std::cos(ang);
+      tab[(p * half + m) * 2 + 1] = std::sin(ang);
+    }
+  }
+  hipStream_t s = pick_stream(stream);
+  DevBuf t;
+  int rc = t.alloc(tab.size() * 4);
+  if (rc) return rc;
+  PRANA_HIP(hipMemcpyAsync(t.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s));
+  rc = launch_rope(x, n_rows, row_len, row_len, hd, t.as<float2>(), pos0, neox, s);
+  if (rc) return rc;
+  PRANA_HIP(hipStreamSynchronize(s));  // the table dies with this scope
+  return static_cast<int>(kOk);
+}
+}  // namespace
+
+int prana_rope_interleaved(float* x, size_t n_rows, size_t row_len, size_t pos0, size_t head_dim, float theta,
+                           prana_stream_t stream) {
+  return guard([&] { return rope_entry(x, n_rows, row_len, pos0, head_dim, theta, 0, stream); });
+}
+
+int prana_rope_neox(float* x, size_t n_rows, size_t row_len, size_t pos0, size_t head_dim, float theta,
+                    prana_stream_t stream) {
+  return guard([&] { return rope_entry(x, n_rows, row_len, pos0, head_dim, theta, 1, stream); });
+}
+
+int prana_kv_write_f16(uint16_t* cache, size_t first_row, size_t kv_stride, const float* src, size_t n,
+                       prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_kv_write(cache, first_row, kv_stride, src, n, pick_stream(stream));
+  });
+}
+
+namespace {
+int attn_entry(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t seq, size_t nh, size_t nkv,
+               size_t hd, float* out, void* stream) {
+  INIT_OR_RETURN();
+  Scratch& sc = scratch();
+  std::lock_guard<std::mutex> lk(sc.mu);
+  size_t cap = pos0 + seq;
+  int rc = sc.att.ensure(seq * nh * cap * 4);
+  if (rc) return rc;
+  hipStream_t s = pick_stream(stream);
+  rc = launch_attention_cache(q, kc, vc, pos0, seq, nh, nkv, hd, out, sc.att.as<float>(), cap, nullptr, s);
+  if (rc) return rc;
+  PRANA_HIP(hipStreamSynchronize(s));
+  return static_cast<int>(kOk);
+}
+}  // namespace
+
+int prana_attention_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, size_t pos,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, float* out, prana_stream_t stream) {
+  return guard([&] { return attn_entry(q, k_cache, v_cache, pos, 1, n_heads, n_kv_heads, head_dim, out, stream); });
+}
+
+int prana_attention_verify(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, size_t pos0,
+                           size_t seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, float* out,
+                           prana_stream_t stream) {
+  return guard(
+      [&] { return attn_entry(q, k_cache, v_cache, pos0, seq, n_heads, n_kv_heads, head_dim, out, stream); });
+}
+
+int prana_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
+                            size_t n_kv_heads, size_t head_dim, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    Scratch& sc = scratch();
+    std::lock_guard<std::mutex> lk(sc.mu);
+    int rc = sc.att.ensure(n_heads * seq * seq * 4);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream);
+    rc = launch_attention_prefill(q, k, v, seq, n_heads, n_kv_heads, head_dim, out, sc.att.as<float>(), s);
+    if (rc) return rc;
+    PRANA_HIP(hipStreamSynchronize(s));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_argmax(const float* logits, size_t rows, size_t n, uint32_t* out_idx, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_argmax(logits, rows, n, out_idx, pick_stream(stream));
+  });
+}
+
+int prana_f32_to_f16(const float* in, size_t n, uint16_t* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_f32_to_f16(in, n, out, pick_stream(stream));
+  });
+}
+
+int prana_f16_to_f32(const uint16_t* in, size_t n, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_f16_to_f32(in, n, out, pick_stream(stream));
+  });
+}
+
+int prana_expf(const float* in, size_t n, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_expf(in, n, out, pick_stream(stream));
+  });
+}
+
+// ------------------------------------------------------------------ model
+int prana_model_create(const prana_config* cfg, prana_model_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(cfg && out, "null argument");
+    const prana_config& c = *cfg;
+    PRANA_CHECK(c.dim > 0 && c.n_layers > 0 && c.n_heads > 0 && c.vocab_size > 0 && c.seq_len > 0,
+                "config: zero-sized dimension");
+    PRANA_CHECK(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "config: n_heads % n_kv_heads != 0");
+    PRANA_CHECK(c.head_dim % 2 == 0 && c.head_dim <= 256, "config: head_dim must be even and <= 256");
+    PRANA_CHECK(c.dim % 32 == 0 && c.hidden_dim % 32 == 0 && (c.n_heads * c.head_dim) % 32 == 0,
+                "config: dim, hidden_dim and n_heads*head_dim must be multiples of 32");
+    auto* m = new prana_model();
+    m->m.c = c;
+    m->m.layers.resize(c.n_layers);
+    *out = m;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_model_destroy(prana_model_t m) {
+  return guard([&] {
+    delete m;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_model_set_tensor(prana_model_t m, const char* name, int ggml_type, const uint64_t* dims, int n_dims,
+                           const void* bytes, size_t nbytes) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && name && dims && bytes, "null argument");
+    PRANA_CHECK(n_dims == 1 || n_dims == 2, "tensor must be 1-D or 2-D");
+    m->m.finalized = false;
+    return m->m.set_tensor(name, ggml_type, dims, n_dims, bytes, nbytes);
+  });
+}
+
+int prana_model_finalize(prana_model_t m) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m, "null model");
+    return m->m.finalize();
+  });
+}
+
+int prana_model_stream_bytes(prana_model_t m, size_t* bytes) {
+  return guard([&] {
+    PRANA_CHECK(m && bytes && m->m.finalized, "model not finalized");
+    *bytes = m->m.stream_bytes();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_cache_create(prana_model_t m, size_t positions, prana_cache_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && out, "null argument");
+    auto* c = new prana_cache();
+    c->owner = m;
+    int rc = c->c.create(m->m, positions);
+    if (rc) {
+      delete c;
+      return rc;
+    }
+    *out = c;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_cache_destroy(prana_cache_t c) {
+  return guard([&] {
+    delete c;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_cache_read(prana_cache_t c, size_t layer, int which, size_t rows, uint16_t* host_out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(c && host_out, "null argument");
+    PRANA_CHECK(layer < c->c.n_layers && rows <= c->c.len, "cache_read: out of range");
+    PRANA_HIP(hipStreamSynchronize(ctx().stream));
+    const uint16_t* src = which ? c->c.v(layer) : c->c.k(layer);
+    PRANA_HIP(hipMemcpy(host_out, src, rows * c->c.kv_dim * 2, hipMemcpyDeviceToHost));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_forward(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, int need_logits, float* logits_host) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && c && c->owner == m, "cache does not belong to this model");
+    return m->m.forward(c->c, token, pos, need_logits != 0, logits_host);
+  });
+}
+
+int prana_prefill(prana_model_t m, prana_cache_t c, const uint32_t* tokens, size_t n) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && c && c->owner == m && (tokens || n == 0), "bad argument");
+    return m->m.prefill(c->c, tokens, n);
+  });
+}
+
+int prana_forward_batch(prana_model_t m, prana_cache_t c, const uint32_t* tokens, size_t n, size_t pos0,
+                        float* logits_host) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && c && c->owner == m && tokens, "bad argument");
+    return m->m.forward_batch(c->c, tokens, n, pos0, logits_host);
+  });
+}
+
+int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, size_t n_steps, uint32_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && c && c->owner == m, "cache does not belong to this model");
+    PRANA_CHECK(token < m->m.c.vocab_size, "token id out of vocabulary");
+    return m->m.decode(c->c, token, pos, n_steps, out);
+  });
+}
+
+int prana_gemv_profile(int on) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    GemvProfile& gp = gemv_profile();
+    int rc = gp.collect();
+    gp.on = on != 0;
+    return rc;
+  });
+}
+
+int prana_gemv_profile_read(size_t* launches, double* seconds, double* bytes, int reset) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    GemvProfile& gp = gemv_profile();
+    int rc = gp.collect();
+    if (rc) return rc;
+    if (launches) *launches = gp.launches;
+    if (seconds) *seconds = gp.seconds;
+    if (bytes) *bytes = gp.bytes;
+    if (reset) {
+      gp.launches = 0;
+      gp.seconds = gp.bytes = 0.0;
+    }
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_generate(prana_model_t m, const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops,
+                   size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* stats) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && prompt && (out || steps == 0), "bad argument");
+    PRANA_CHECK(m->m.finalized, "model not finalized");
+    return m->m.generate(prompt, p, steps, stops, n_stops, out, n_out, stats);
+  });
+}
+
+int prana_generate_speculative(prana_model_t target, prana_model_t draft, const uint32_t* prompt, size_t p,
+                               size_t steps, size_t k, const uint32_t* stops, size_t n_stops, uint32_t* out,
+                               size_t* n_out, prana_gen_stats* stats) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(target && draft && prompt && (out || steps == 0), "bad argument");
+    PRANA_CHECK(target->m.finalized && draft->m.finalized, "model not finalized");
+    return generate_speculative(target->m, draft->m, prompt, p, steps, k, stops, n_stops, out, n_out, stats);
+  });
+}
+
+// ------------------------------------------------------------------ synthetic weights
+int prana_quantize_tensor(int ggml_type, const float* src, size_t rows, size_t cols, void* out, size_t nbytes) {
+  return guard([&] {
+    PRANA_CHECK(src && out, "null argument");
+    return quantize_tensor(ggml_type, src, rows, cols, static_cast<uint8_t*>(out), nbytes);
+  });
+}
+
+int prana_synth_normal(uint64_t seed, float sigma, float* out, size_t n) {
+  return guard([&] {
+    PRANA_CHECK(out || n == 0, "null argument");
+    synth_normal(seed, sigma, out, n);
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, void* out,
+                       size_t nbytes) {
+  return guard([&] {
+    PRANA_CHECK(out, "null argument");
+    return synth_tensor(ggml_type, rows, cols, seed, sigma, static_cast<uint8_t*>(out), nbytes);
+  });
+}
+
+size_t prana_ggml_nbytes(int ggml_type, size_t n_elems) { return ggml_nbytes(ggml_type, n_elems); }
+
+}  // extern "C"

@@ -1,0 +1,168 @@
+// Shared device helpers and host error plumbing for libprana_hip.
+//
+// Numerics contract: every f32 expression that feeds an output is evaluated
+// in the same order as the reference scalar tier (no FMA contraction — the
+// library is built with -ffp-contract=off — IEEE division and square root,
+// round-half-away-from-zero), so results are bit-identical to the CPU path.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace prana {
+
+// ---------------------------------------------------------------- errors
+// Status codes of the C ABI (see include/prana_hip.h).
+enum Status : int {
+  kOk = 0,
+  kErrInvalid = -1,
+  kErrHip = -2,
+  kErrNoMem = -3,
+  kErrUnsupported = -4,
+};
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define PRANA_HIP(expr)                                   \
+  do {                                                    \
+    hipError_t e_ = (expr);                               \
+    if (e_ != hipSuccess) return ::prana::hip_fail(e_, #expr); \
+  } while (0)
+
+#define PRANA_CHECK(cond, msg)                                 \
+  do {                                                         \
+    if (!(cond)) return ::prana::fail(::prana::kErrInvalid, msg); \
+  } while (0)
+
+#define PRANA_LAUNCH_CHECK()                                   \
+  do {                                                         \
+    hipError_t e_ = hipGetLastError();                         \
+    if (e_ != hipSuccess) return ::prana::hip_fail(e_, "kernel launch"); \
+  } while (0)
+
+// ---------------------------------------------------------------- f16
+// f16 bits -> f32 exactly as prana-kernels lib.rs:57-73. The hardware
+// conversion agrees with the reference on every non-NaN input (checked
+// exhaustively on gfx950); NaNs keep their payload unquieted, as the
+// reference does.
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  float hw = __half2float(__ushort_as_half(h));
+  bool nan = ((h & 0x7c00u) == 0x7c00u) && (h & 0x03ffu);
+  uint32_t nb = (static_cast<uint32_t>(h & 0x8000u) << 16) | 0x7f800000u |
+                (static_cast<uint32_t>(h & 0x03ffu) << 13);
+  return nan ? __uint_as_float(nb) : hw;
+}
+
+// f32 -> f16 bits, round-to-nearest-even, exactly as lib.rs:78-113 (NaN ->
+// sign | 0x7e00; hardware RNE matches every other input exhaustively).
+__device__ __forceinline__ uint16_t f32_to_f16(float x) {
+  uint32_t u = __float_as_uint(x);
+  bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  uint16_t hw = __half_as_ushort(__float2half_rn(x));
+  return nan ? static_cast<uint16_t>(((u >> 16) & 0x8000u) | 0x7e00u) : hw;
+}
+
+// ---------------------------------------------------------------- expf
+// The reference reaches expf through Rust's f32::exp -> glibc expf. glibc
+// (2.28+) computes it with the ARM optimized-routines algorithm: a 32-entry
+// table of 2^(i/32) and a cubic in double precision; on x86_64 hosts with FMA
+// the multiarch build contracts four products into FMAs. This restatement
+// reproduces that evaluation exactly; it equals the host glibc expf on all
+// 2^32 inputs (exhaustive check in the GPU test suite).
+// kExp2Tab[i] = asuint64(double(2^(i/32))) - (i << 47); regenerated and
+// compared by tests/test_device_numerics.py.
+static __constant__ const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__device__ __forceinline__ float dev_expf(float x) {
+  uint32_t ux = __float_as_uint(x);
+  uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {                       // |x| >= 88 or x is NaN/inf
+    if (ux == 0xff800000u) return 0.0f;         // exp(-inf)
+    if (abstop >= 0x7f8u) return x + x;         // +inf or NaN
+    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;                          // underflow
+  }
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  const double kShift = 0x1.8p+52;
+  const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  double xd = static_cast<double>(x);
+  double kd = __fma_rn(kInvLn2N, xd, kShift);
+  uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
+  kd -= kShift;
+  double r = __fma_rn(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  double s = __longlong_as_double(static_cast<long long>(t));
+  double z = __fma_rn(c0, r, c1);
+  double r2 = r * r;
+  double y = __fma_rn(c2, r, 1.0);
+  y = __fma_rn(z, r2, y);
+  y = y * s;
+  return static_cast<float>(y);
+}
+
+// ---------------------------------------------------------------- rounding
+// Rust `(x).round().clamp(-127.0, 127.0) as i32` (matmul.rs:123): half away
+// from zero, saturate, NaN -> 0.
+__device__ __forceinline__ int round_clamp127(float v) {
+  float r = roundf(v);
+  if (r != r) return 0;
+  r = r < -127.0f ? -127.0f : r;
+  r = r > 127.0f ? 127.0f : r;
+  return static_cast<int>(r);
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ float wave_max_f32(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Reductions over aligned groups of 32 lanes (one quantization block).
+__device__ __forceinline__ float half_wave_max_f32(float v) {
+  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int half_wave_sum_i32(int v) {
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Quantize one 32-element activation block held one value per lane of an
+// aligned 32-lane group (quantize_acts, matmul.rs:111-125). Returns the i8
+// value of this lane; the group's scale and integer sum come back by pointer
+// (valid in every lane of the group).
+__device__ __forceinline__ int quantize_lane(float x, float* scale_out, int* sum_out) {
+  float amax = half_wave_max_f32(fabsf(x));   // max is exact in any order
+  float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+  float inv = 1.0f / scale;
+  int v = round_clamp127(x * inv);
+  *scale_out = scale;
+  *sum_out = half_wave_sum_i32(v);            // integer sum: order-free
+  return v;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace prana

@@ -1,0 +1,467 @@
+// Elementwise, normalisation, RoPE, KV-cache, embedding and argmax kernels.
+//
+// Every reduction that the reference performs as a sequential f32 fold
+// (rmsnorm's sum of squares, softmax's sum) is performed here in exactly that
+// order by a single lane; order-free parts (max, integer sums, elementwise
+// products) run in parallel.
+#include "common.h"
+#include "kernels.h"
+
+namespace prana {
+
+// ---------------------------------------------------------------- quantize_acts
+// matmul.rs:105-127. One 32-lane group per 32-element block.
+__global__ __launch_bounds__(256) void quantize_acts_kernel(const float* __restrict__ x, size_t n_blocks,
+                                                            int8_t* __restrict__ q, float* __restrict__ sa,
+                                                            int* __restrict__ sums) {
+  size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  size_t blk = gid >> 5;
+  bool live = blk < n_blocks;
+  float v = live ? x[gid] : 0.0f;
+  float scale;
+  int sum;
+  int qi = quantize_lane(v, &scale, &sum);
+  if (live) {
+    q[gid] = static_cast<int8_t>(qi);
+    if ((threadIdx.x & 31) == 0) {
+      sa[blk] = scale;
+      sums[blk] = sum;
+    }
+  }
+}
+
+int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, float* sa, int* sums,
+                         hipStream_t s) {
+  size_t n = n_rows * k;
+  if (n == 0) return kOk;
+  size_t grid = (n + 255) / 256;
+  hipLaunchKernelGGL(quantize_acts_kernel, dim3(grid), dim3(256), 0, s, x, n / 32, q, sa, sums);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- rmsnorm
+// norms.rs:9-23: ms = (sum_seq x*x)/dim; inv = 1/sqrt(ms+eps); y = (x*inv)*w.
+// One workgroup per row. The sum is the reference's left-to-right fold from
+// -0.0 (single lane); the normalise + optional quantize is parallel.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      int dim, float eps, float* __restrict__ out,
+                                                      int8_t* __restrict__ q, float* __restrict__ sa,
+                                                      int* __restrict__ sums) {
+  __shared__ float s_inv;
+  const float* row = x + (size_t)blockIdx.x * dim;
+  if (threadIdx.x == 0) {
+    float ss = -0.0f;
+    for (int i = 0; i < dim; i++) ss += row[i] * row[i];
+    float mean_sq = ss / static_cast<float>(dim);
+    s_inv = 1.0f / sqrtf(mean_sq + eps);
+  }
+  __syncthreads();
+  float inv = s_inv;
+  // dim is a multiple of 32 whenever q != nullptr; round the loop up to a
+  // whole number of 32-lane groups so every group reduces together.
+  int span = q ? ((dim + 255) / 256) * 256 : dim;
+  for (int i = threadIdx.x; i < span; i += 256) {
+    bool live = i < dim;
+    float y = live ? row[i] * inv * w[i] : 0.0f;
+    if (live && out) out[(size_t)blockIdx.x * dim + i] = y;
+    if (q) {
+      float scale;
+      int sum;
+      int qi = quantize_lane(y, &scale, &sum);
+      if (live) {
+        size_t gi = (size_t)blockIdx.x * dim + i;
+        q[gi] = static_cast<int8_t>(qi);
+        if ((i & 31) == 0) {
+          sa[gi >> 5] = scale;
+          sums[gi >> 5] = sum;
+        }
+      }
+    }
+  }
+}
+
+int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, float eps, float* out, int8_t* q,
+                   float* sa, int* sums, hipStream_t s) {
+  if (rows == 0) return kOk;
+  PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, w, (int)dim, eps, out, q, sa, sums);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- activations
+// silu (norms.rs:27-31) then `g *= u` (infer.rs:197-199), optionally
+// quantizing the product for the down projection.
+__global__ __launch_bounds__(256) void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u,
+                                                       size_t n, int8_t* __restrict__ q, float* __restrict__ sa,
+                                                       int* __restrict__ sums, int gelu) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  bool live = i < n;
+  float v = live ? g[i] : 0.0f;
+  if (gelu) {
+    const float kS = 0.7978846f;  // norms.rs:36
+    float x3 = v * v * v;
+    v = 0.5f * v * (1.0f + tanhf(kS * (v + 0.044715f * x3)));
+  } else {
+    v = v * (1.0f / (1.0f + dev_expf(-v)));
+  }
+  if (u) v = v * (live ? u[i] : 0.0f);
+  if (live) g[i] = v;
+  if (q) {
+    float scale;
+    int sum;
+    int qi = quantize_lane(v, &scale, &sum);
+    if (live) {
+      q[i] = static_cast<int8_t>(qi);
+      if ((i & 31) == 0) {
+        sa[i >> 5] = scale;
+        sums[i >> 5] = sum;
+      }
+    }
+  }
+}
+
+int launch_act_mul(float* g, const float* u, size_t n, int gelu, int8_t* q, float* sa, int* sums, hipStream_t s) {
+  if (n == 0) return kOk;
+  PRANA_CHECK(!q || n % 32 == 0, "act: fused quantize needs n % 32 == 0");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, n, q, sa, sums, gelu);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- softmax
+// norms.rs:44-56, one workgroup per row; the sum is a single-lane fold.
+__global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ in, int n, float* __restrict__ out) {
+  __shared__ float s_red[4];
+  __shared__ float s_inv;
+  const float* row = in + (size_t)blockIdx.x * n;
+  float* dst = out + (size_t)blockIdx.x * n;
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, row[i]);
+  mx = wave_max_f32(mx);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  for (int i = threadIdx.x; i < n; i += 256) dst[i] = dev_expf(row[i] - mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = -0.0f;
+    for (int i = 0; i < n; i++) sum += dst[i];
+    s_inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  }
+  __syncthreads();
+  float inv = s_inv;
+  for (int i = threadIdx.x; i < n; i += 256) dst[i] = dst[i] * inv;
+}
+
+int launch_softmax(const float* in, size_t rows, size_t n, float* out, hipStream_t s) {
+  if (rows == 0 || n == 0) return kOk;
+  hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(256), 0, s, in, (int)n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- add
+__global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n, size_t period) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] + y[period ? i % period : i];
+}
+
+int launch_add(float* x, const float* y, size_t n, size_t period, hipStream_t s) {
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(add_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, y, n, period);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- RoPE
+// Pair rotation with host-computed (cos, sin) = glibc (cosf, sinf) of
+// (pos as f32) * powf(theta, -(2m)/hd) — the exact values the reference
+// computes inline (attention.rs:93-100, 111-119). table: [pos][hd/2] float2.
+__device__ __forceinline__ void rotate(float& a, float& b, float2 cs) {
+  float x0 = a, x1 = b;
+  a = x0 * cs.x - x1 * cs.y;
+  b = x0 * cs.y + x1 * cs.x;
+}
+
+// x: n_rows rows of row_len floats (row_stride apart); row t is at position
+// pos0 + t. neox: pairs (j, j + hd/2) per head; else adjacent pairs.
+__global__ void rope_kernel(float* __restrict__ x, int n_rows, int row_len, size_t row_stride, int hd,
+                            const float2* __restrict__ table, int pos0, int neox) {
+  int pairs = row_len / 2;
+  size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (gid >= (size_t)n_rows * pairs) return;
+  int t = static_cast<int>(gid / pairs);
+  int p = static_cast<int>(gid % pairs);
+  int half = hd / 2;
+  float* row = x + t * row_stride;
+  const float2* tab = table + (size_t)(pos0 + t) * half;
+  int i0, i1, m;
+  if (neox) {
+    int h = p / half, j = p % half;
+    i0 = h * hd + j;
+    i1 = i0 + half;
+    m = j;
+  } else {
+    i0 = 2 * p;
+    i1 = i0 + 1;
+    m = (i0 % hd) / 2;
+  }
+  rotate(row[i0], row[i1], tab[m]);
+}
+
+int launch_rope(float* x, size_t n_rows, size_t row_len, size_t row_stride, size_t hd, const float2* table,
+                size_t pos0, int neox, hipStream_t s) {
+  size_t n = n_rows * (row_len / 2);
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, (int)n_rows, (int)row_len, row_stride,
+                     (int)hd, table, (int)pos0, neox);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// f16_kv_write (attention.rs:47-52): cache[first_row*kv_stride + i] = f16(src[i]).
+__global__ void kv_write_kernel(uint16_t* __restrict__ cache, const float* __restrict__ src, size_t n) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) cache[i] = f32_to_f16(src[i]);
+}
+
+int launch_kv_write(uint16_t* cache, size_t first_row, size_t kv_stride, const float* src, size_t n,
+                    hipStream_t s) {
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(kv_write_kernel, dim3((n + 255) / 256), dim3(256), 0, s, cache + first_row * kv_stride, src,
+                     n);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// Decode glue after the Q/K/V projections (infer.rs:169-178): rope q and k
+// in place at `pos`, then write k and v to the f16 cache row `pos`.
+__global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+                               int q_dim, int kv_dim, int hd, const float2* __restrict__ table, int neox,
+                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ pos_dev,
+                               int pos_host) {
+  int pos = pos_dev ? *pos_dev : pos_host;
+  int half = hd / 2;
+  const float2* tab = table + (size_t)pos * half;
+  int qp = q_dim / 2, kp = kv_dim / 2;
+  int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid < qp + kp) {
+    float* row = gid < qp ? q : k;
+    int p = gid < qp ? gid : gid - qp;
+    int i0, i1, m;
+    if (neox) {
+      int h = p / half, j = p % half;
+      i0 = h * hd + j;
+      i1 = i0 + half;
+      m = j;
+    } else {
+      i0 = 2 * p;
+      i1 = i0 + 1;
+      m = (i0 % hd) / 2;
+    }
+    float a = row[i0], b = row[i1];
+    rotate(a, b, tab[m]);
+    row[i0] = a;
+    row[i1] = b;
+    if (gid >= qp) {
+      kc[(size_t)pos * kv_dim + i0] = f32_to_f16(a);
+      kc[(size_t)pos * kv_dim + i1] = f32_to_f16(b);
+    }
+  } else if (gid < qp + kp + kv_dim) {
+    int i = gid - qp - kp;
+    vc[(size_t)pos * kv_dim + i] = f32_to_f16(v[i]);
+  }
+}
+
+int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
+                   int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s) {
+  size_t n = q_dim / 2 + kv_dim / 2 + kv_dim;
+  hipLaunchKernelGGL(rope_kv_kernel, dim3((n + 255) / 256), dim3(256), 0, s, q, k, v, (int)q_dim, (int)kv_dim,
+                     (int)hd, table, neox, kc, vc, pos_dev, (int)pos_host);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- f16 conversions
+__global__ void f32_to_f16_kernel(const float* __restrict__ in, size_t n, uint16_t* __restrict__ out) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f32_to_f16(in[i]);
+}
+__global__ void f16_to_f32_kernel(const uint16_t* __restrict__ in, size_t n, float* __restrict__ out) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f16_to_f32(in[i]);
+}
+__global__ void expf_kernel(const float* __restrict__ in, size_t n, float* __restrict__ out) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = dev_expf(in[i]);
+}
+// exp over a contiguous range of f32 bit patterns [base, base + n).
+__global__ void expf_bits_kernel(uint32_t base, uint32_t n, float* __restrict__ out) {
+  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = dev_expf(__uint_as_float(base + i));
+}
+
+int launch_f32_to_f16(const float* in, size_t n, uint16_t* out, hipStream_t s) {
+  if (!n) return kOk;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((n + 255) / 256), dim3(256), 0, s, in, n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+int launch_f16_to_f32(const uint16_t* in, size_t n, float* out, hipStream_t s) {
+  if (!n) return kOk;
+  hipLaunchKernelGGL(f16_to_f32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, in, n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+int launch_expf(const float* in, size_t n, float* out, hipStream_t s) {
+  if (!n) return kOk;
+  hipLaunchKernelGGL(expf_kernel, dim3((n + 255) / 256), dim3(256), 0, s, in, n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s) {
+  if (!n) return kOk;
+  hipLaunchKernelGGL(expf_bits_kernel, dim3((n + 255) / 256), dim3(256), 0, s, base, n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- argmax
+// infer.rs:560-568: strict `>` scan, first max wins. A NaN at index 0 pins the
+// result to 0; later NaNs never win. Parallel form: per-lane strided scans
+// (increasing index, strict >), then a (value, lowest index) reduction.
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ v, int n, uint32_t* __restrict__ out) {
+  __shared__ float s_v[256];
+  __shared__ int s_i[256];
+  const float* row = v + (size_t)blockIdx.x * n;
+  float best = -INFINITY;
+  int bi = n;  // none
+  for (int i = threadIdx.x; i < n; i += 256) {
+    float x = row[i];
+    if (x > best) {
+      best = x;
+      bi = i;
+    }
+  }
+  s_v[threadIdx.x] = best;
+  s_i[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      float bv = s_v[threadIdx.x + o];
+      int bj = s_i[threadIdx.x + o];
+      float av = s_v[threadIdx.x];
+      int aj = s_i[threadIdx.x];
+      if (bj < n && (aj >= n || bv > av || (bv == av && bj < aj))) {
+        s_v[threadIdx.x] = bv;
+        s_i[threadIdx.x] = bj;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    int r = s_i[0];
+    if (r >= n || row[0] != row[0]) r = 0;  // all -inf / NaN at index 0
+    out[blockIdx.x] = static_cast<uint32_t>(r);
+  }
+}
+
+int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStream_t s) {
+  if (rows == 0) return kOk;
+  PRANA_CHECK(n > 0, "argmax: empty row");
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, v, (int)n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// ---------------------------------------------------------------- embedding
+// Embedding::row (checkpoint.rs:169-174): dense copy, or one row of a packed
+// table dequantized (kquant.rs:39-112; Q8_0 tables are f32 rows q*d as
+// gguf.rs:234-245 produces), then `x *= emb_scale` when it is not 1
+// (infer.rs:155-159).
+__device__ float dequant_elem(const DevMat& m, size_t r, int c) {
+  switch (m.kind) {
+    case kKindF32:
+      return reinterpret_cast<const float*>(m.qs)[r * m.cols + c];
+    case kKindQ8F: {
+      const int8_t* q = reinterpret_cast<const int8_t*>(m.qs);
+      const float* sc = reinterpret_cast<const float*>(m.sc);
+      return static_cast<float>(q[r * m.cols + c]) * sc[r * (m.cols / 32) + c / 32];
+    }
+    case kKindQ8_0: {
+      const int8_t* q = reinterpret_cast<const int8_t*>(m.qs);
+      const uint16_t* sc = reinterpret_cast<const uint16_t*>(m.sc);
+      return static_cast<float>(q[r * m.cols + c]) * f16_to_f32(sc[r * (m.cols / 32) + c / 32]);
+    }
+    case kKindQ4_0: {
+      size_t G = m.cols / 32;
+      size_t b = c / 32;
+      int j = c % 32;
+      const uint8_t* blk = m.qs + (r * G + b) * 16;
+      float d = f16_to_f32(reinterpret_cast<const uint16_t*>(m.sc)[r * G + b]);
+      int nib = j < 16 ? (blk[j] & 0xF) : (blk[j - 16] >> 4);
+      return d * (static_cast<float>(nib) - 8.0f);
+    }
+    case kKindQ4_K: {
+      size_t nb = m.cols / 256;
+      const uint8_t* b = m.qs + (r * nb + c / 256) * 144;
+      int e = c % 256;
+      int pair = e / 64, hi = (e % 64) / 32, l = e % 32;
+      float d = f16_to_f32(static_cast<uint16_t>(b[0] | (b[1] << 8)));
+      float dmin = f16_to_f32(static_cast<uint16_t>(b[2] | (b[3] << 8)));
+      const uint8_t* s = b + 4;
+      int j = pair * 2 + hi;
+      float sc, mn;
+      if (j < 4) {
+        sc = static_cast<float>(s[j] & 63);
+        mn = static_cast<float>(s[j + 4] & 63);
+      } else {
+        sc = static_cast<float>((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        mn = static_cast<float>((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+      }
+      uint8_t byte = b[16 + pair * 32 + l];
+      int nib = hi ? (byte >> 4) : (byte & 0xF);
+      float d1 = d * sc, m1 = dmin * mn;
+      return d1 * static_cast<float>(nib) - m1;
+    }
+    case kKindQ6_K: {
+      size_t nb = m.cols / 256;
+      const uint8_t* b = m.qs + (r * nb + c / 256) * 208;
+      float d = f16_to_f32(reinterpret_cast<const uint16_t*>(m.sc)[r * nb + c / 256]);
+      int e = c % 256;
+      int half = e / 128, rem = e % 128, g = rem / 32, l = rem % 32;
+      const uint8_t* ql = b + half * 64;
+      const uint8_t* qh = b + 128 + half * 32;
+      const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192);
+      int qlb = ql[l + (g & 1) * 32];
+      int nib = g < 2 ? (qlb & 0xF) : (qlb >> 4);
+      int hb = (qh[l] >> (2 * g)) & 3;
+      int qv = static_cast<int>(static_cast<int8_t>(nib | (hb << 4))) - 32;
+      int is = half * 8 + l / 16 + 2 * g;
+      return d * static_cast<float>(sc[is]) * static_cast<float>(qv);
+    }
+  }
+  return 0.0f;
+}
+
+__global__ void embed_kernel(DevMat m, const uint32_t* __restrict__ tokens, float scale, float* __restrict__ out) {
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  int t = blockIdx.y;
+  if (c >= (int)m.cols) return;
+  size_t r = tokens[t];
+  if (r >= m.rows) r = 0;  // out-of-vocabulary ids are rejected on the host
+  float v = dequant_elem(m, r, c);
+  if (scale != 1.0f) v = v * scale;
+  out[(size_t)t * m.cols + c] = v;
+}
+
+int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale, float* out, hipStream_t s) {
+  if (n == 0) return kOk;
+  hipLaunchKernelGGL(embed_kernel, dim3((m.cols + 255) / 256, n), dim3(256), 0, s, m, tokens, scale, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+}  // namespace prana

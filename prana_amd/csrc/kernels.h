@@ -1,0 +1,81 @@
+// Device-side matrix descriptor and the host launch functions of every kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace prana {
+
+// Device storage kinds. Byte layouts (all rows contiguous, row-major):
+//   F32  : float [rows][cols]
+//   Q8F  : int8 [rows][cols] + float scale [rows][cols/32]      (QuantMatrix, f32 scales)
+//   Q8_0 : int8 [rows][cols] + f16 d [rows][cols/32]            (GGUF Q8_0, 34 B / 32)
+//   Q4_0 : u8 [rows][cols/32][16] + f16 d [rows][cols/32]       (GGUF Q4_0, 18 B / 32)
+//   Q4_K : u8 [rows][cols/256][144]                            (GGUF block, unchanged)
+//   Q6_K : u8 [rows][cols/256][208] (ql|qh|scales) + f16 d [rows][cols/256]  (210 B / 256)
+// The split keeps every quant run 16-byte aligned for 128-bit loads; the
+// byte count per block is the GGUF one, so roofline bytes are unchanged.
+enum Kind : int { kKindF32 = 0, kKindQ8F = 1, kKindQ8_0 = 2, kKindQ4_0 = 3, kKindQ4_K = 4, kKindQ6_K = 5 };
+
+struct DevMat {
+  int kind;
+  size_t rows, cols;
+  const uint8_t* qs;  // quants (or f32 weights)
+  const void* sc;     // per-block scales (nullptr for Q4_K)
+};
+
+// Algorithmic bytes of a weight matrix (what a GEMV must stream).
+size_t devmat_bytes(const DevMat& m);
+
+// ---- elementwise.hip
+int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, float* sa, int* sums, hipStream_t s);
+int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, float eps, float* out, int8_t* q,
+                   float* sa, int* sums, hipStream_t s);
+int launch_act_mul(float* g, const float* u, size_t n, int gelu, int8_t* q, float* sa, int* sums, hipStream_t s);
+int launch_softmax(const float* in, size_t rows, size_t n, float* out, hipStream_t s);
+int launch_add(float* x, const float* y, size_t n, size_t period, hipStream_t s);
+int launch_rope(float* x, size_t n_rows, size_t row_len, size_t row_stride, size_t hd, const float2* table,
+                size_t pos0, int neox, hipStream_t s);
+int launch_kv_write(uint16_t* cache, size_t first_row, size_t kv_stride, const float* src, size_t n, hipStream_t s);
+int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
+                   int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s);
+int launch_f32_to_f16(const float* in, size_t n, uint16_t* out, hipStream_t s);
+int launch_f16_to_f32(const uint16_t* in, size_t n, float* out, hipStream_t s);
+int launch_expf(const float* in, size_t n, float* out, hipStream_t s);
+int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s);
+int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStream_t s);
+int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale, float* out, hipStream_t s);
+
+// ---- gemv.hip
+// out[t*ldo + r] (mode): 0 = store, 1 = store + bias[r], 2 = out += result
+// (the residual add x += o of infer.rs:186-188, 201-203).
+struct GemvOut {
+  float* out;
+  size_t ldo;
+  const float* bias;
+  int residual;
+};
+// Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
+int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                const GemvOut& o, hipStream_t s);
+// The exact i32 part of every term (debug / bit-exactness entry point):
+// isums[t][r][term] with T terms per row (cols/32, or cols/16 for Q6_K).
+int launch_block_isums(const DevMat& m, const int8_t* q, const int* sums, size_t n_tok, int* isums, hipStream_t s);
+size_t terms_per_row(const DevMat& m);
+
+// ---- attention.hip
+// attention_decode / attention_verify (attention.rs:129-160, 296-333) over the
+// f16 cache: n_q query rows at positions pos0 + i (pos0 read from pos_dev when
+// non-null). scratch >= n_q*n_heads*ctx_cap floats, ctx_cap >= pos0+n_q
+// (0 = exactly pos0+n_q).
+int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
+                           size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
+                           const int* pos_dev, hipStream_t s);
+// attention (prefill, attention.rs:236-284) over f32 K/V of the window.
+// scratch >= n_heads*seq*seq floats.
+int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
+                             size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s);
+
+}  // namespace prana

@@ -1,0 +1,552 @@
+// Device-resident model, KV cache and the forward passes (prana-model
+// checkpoint.rs / infer.rs), driving the kernels of kernels.h in the order the
+// reference runs its scalar kernels, so logits and token streams are
+// bit-identical to the CPU path.
+#include "model.h"
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace prana {
+
+namespace {
+
+double now_s() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+bool parse_layer(const std::string& name, size_t& layer, std::string& rest) {
+  if (name.rfind("blk.", 0) != 0) return false;
+  size_t dot = name.find('.', 4);
+  if (dot == std::string::npos) return false;
+  layer = std::strtoull(name.substr(4, dot - 4).c_str(), nullptr, 10);
+  rest = name.substr(dot + 1);
+  return true;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ tensors
+int Model::set_tensor(const std::string& name, int t, const uint64_t* dims, int n_dims, const void* bytes,
+                      size_t nbytes) {
+  const prana_config& k = c;
+  size_t q_dim = k.n_heads * k.head_dim, kv_dim = k.n_kv_heads * k.head_dim;
+  size_t n = 1;
+  for (int i = 0; i < n_dims; i++) n *= dims[i];
+  auto want2 = [&](size_t cols, size_t rows) -> int {
+    if (n_dims != 2 || dims[0] != cols || dims[1] != rows)
+      return fail(kErrInvalid, "tensor '" + name + "': expected shape [" + std::to_string(cols) + ", " +
+                                   std::to_string(rows) + "]");
+    return kOk;
+  };
+  auto vec_of = [&](size_t len, DevBuf& dst, bool& flag) -> int {
+    if (n_dims != 1 || dims[0] != len)
+      return fail(kErrInvalid, "tensor '" + name + "': expected length " + std::to_string(len));
+    std::vector<float> f(len);
+    if (t == 0) {
+      PRANA_CHECK(nbytes >= len * 4, "vector tensor: short buffer");
+      std::memcpy(f.data(), bytes, len * 4);
+    } else if (t == 1) {
+      PRANA_CHECK(nbytes >= len * 2, "vector tensor: short buffer");
+      const uint8_t* b = static_cast<const uint8_t*>(bytes);
+      for (size_t i = 0; i < len; i++) f[i] = host_f16_to_f32(static_cast<uint16_t>(b[2 * i] | (b[2 * i + 1] << 8)));
+    } else {
+      return fail(kErrUnsupported, "tensor '" + name + "': norm/bias vectors must be F32 or F16");
+    }
+    int rc = dst.alloc(len * 4);
+    if (rc) return rc;
+    PRANA_HIP(hipMemcpy(dst.p, f.data(), len * 4, hipMemcpyHostToDevice));
+    flag = true;
+    return kOk;
+  };
+  auto mat_of = [&](size_t cols, size_t rows, std::unique_ptr<Mat>& dst) -> int {
+    int rc = want2(cols, rows);
+    if (rc) return rc;
+    auto m = std::make_unique<Mat>();
+    rc = mat_from_ggml(t, rows, cols, bytes, nbytes, *m);
+    if (rc) return rc;
+    dst = std::move(m);
+    return kOk;
+  };
+
+  if (name == "token_embd.weight") {
+    int rc = want2(k.dim, k.vocab_size);
+    if (rc) return rc;
+    // gguf.rs:309-326: Q4_0/Q4_K/Q6_K tables stay packed; anything else
+    // becomes a dense f32 table (also what a tied classifier then reads).
+    bool packed = (t == 2 && k.dim % 32 == 0) || ((t == 12 || t == 14) && k.dim % 256 == 0);
+    auto m = std::make_unique<Mat>();
+    if (packed) {
+      rc = mat_from_ggml(t, k.vocab_size, k.dim, bytes, nbytes, *m);
+    } else {
+      PRANA_CHECK(t == 0 || t == 1 || t == 2 || t == 8, "token_embd.weight: unsupported type for a dense table");
+      // force a dense table: F32/F16 already are; Q8_0/Q4_0 with odd dims are densified.
+      if (t == 8 || t == 2) {
+        // dequantize on the host through a dense upload path
+        Mat tmp;
+        std::vector<float> f(k.vocab_size * k.dim);
+        const uint8_t* raw = static_cast<const uint8_t*>(bytes);
+        auto f16 = [&](const uint8_t* p) { return host_f16_to_f32(static_cast<uint16_t>(p[0] | (p[1] << 8))); };
+        size_t nn = f.size();
+        if (t == 8) {
+          for (size_t b = 0; b < nn / 32; b++) {
+            float s = f16(raw + b * 34);
+            for (int j = 0; j < 32; j++) f[b * 32 + j] = static_cast<float>(static_cast<int8_t>(raw[b * 34 + 2 + j])) * s;
+          }
+        } else {
+          for (size_t b = 0; b < nn / 32; b++) {
+            const uint8_t* p = raw + b * 18;
+            float d = f16(p);
+            for (int j = 0; j < 16; j++) f[b * 32 + j] = d * (static_cast<float>(p[2 + j] & 0xF) - 8.0f);
+            for (int j = 0; j < 16; j++) f[b * 32 + 16 + j] = d * (static_cast<float>(p[2 + j] >> 4) - 8.0f);
+          }
+        }
+        rc = mat_from_ggml(0, k.vocab_size, k.dim, f.data(), f.size() * 4, *m);
+      } else {
+        rc = mat_from_ggml(t, k.vocab_size, k.dim, bytes, nbytes, *m);
+      }
+    }
+    if (rc) return rc;
+    emb = std::move(m);
+    return kOk;
+  }
+  if (name == "output.weight") return mat_of(k.dim, k.vocab_size, wcls);
+  if (name == "output_norm.weight") return vec_of(k.dim, rms_final, has_rms_final);
+
+  size_t l;
+  std::string rest;
+  if (!parse_layer(name, l, rest) || l >= layers.size()) return fail(kErrInvalid, "unknown tensor '" + name + "'");
+  Layer& L = layers[l];
+  if (rest == "attn_norm.weight") return vec_of(k.dim, L.vec[kRmsAtt], L.has[kRmsAtt]);
+  if (rest == "ffn_norm.weight") return vec_of(k.dim, L.vec[kRmsFfn], L.has[kRmsFfn]);
+  if (rest == "attn_q.bias") return vec_of(q_dim, L.vec[kBq], L.has[kBq]);
+  if (rest == "attn_k.bias") return vec_of(kv_dim, L.vec[kBk], L.has[kBk]);
+  if (rest == "attn_v.bias") return vec_of(kv_dim, L.vec[kBv], L.has[kBv]);
+  if (rest == "attn_q.weight") return mat_of(k.dim, q_dim, L.w[kWq]);
+  if (rest == "attn_k.weight") return mat_of(k.dim, kv_dim, L.w[kWk]);
+  if (rest == "attn_v.weight") return mat_of(k.dim, kv_dim, L.w[kWv]);
+  if (rest == "attn_output.weight") return mat_of(q_dim, k.dim, L.w[kWo]);
+  if (rest == "ffn_gate.weight") return mat_of(k.dim, k.hidden_dim, L.w[kW1]);
+  if (rest == "ffn_down.weight") return mat_of(k.hidden_dim, k.dim, L.w[kW2]);
+  if (rest == "ffn_up.weight") return mat_of(k.dim, k.hidden_dim, L.w[kW3]);
+  return fail(kErrInvalid, "unknown tensor '" + name + "'");
+}
+
+int Model::finalize() {
+  PRANA_CHECK(emb != nullptr, "model: token_embd.weight missing");
+  PRANA_CHECK(has_rms_final, "model: output_norm.weight missing");
+  for (size_t l = 0; l < layers.size(); l++) {
+    for (int i = 0; i < 7; i++)
+      if (!layers[l].w[i]) return fail(kErrInvalid, "model: layer " + std::to_string(l) + " is missing a projection");
+    if (!layers[l].has[kRmsAtt] || !layers[l].has[kRmsFfn])
+      return fail(kErrInvalid, "model: layer " + std::to_string(l) + " is missing a norm weight");
+  }
+  // RoPE table: (cosf, sinf) of (pos as f32) * powf(theta, -(2m)/hd), the
+  // values attention.rs:95-96 / 114-115 compute for every pair.
+  size_t half = c.head_dim / 2;
+  std::vector<float> tab(c.seq_len * half * 2);
+  for (size_t m = 0; m < half; m++) {
+    float freq = std::pow(c.rope_theta, -(2.0f * static_cast<float>(m)) / static_cast<float>(c.head_dim));
+    for (size_t p = 0; p < c.seq_len; p++) {
+      float ang = static_cast<float>(p) * freq;
+      tab[(p * half + m) * 2] = std::cos(ang);
+      tab[(p * half + m) * 2 + 1] = std::sin(ang);
+    }
+  }
+  int rc = rope.alloc(tab.size() * 4);
+  if (rc) return rc;
+  PRANA_HIP(hipMemcpy(rope.p, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+  finalized = true;
+  return kOk;
+}
+
+size_t Model::stream_bytes() const {
+  size_t b = 0;
+  for (auto& L : layers)
+    for (auto& w : L.w)
+      if (w) b += w->stream_bytes;
+  b += head().stream_bytes;
+  return b;
+}
+
+const Mat& Model::head() const { return wcls ? *wcls : *emb; }
+
+// ------------------------------------------------------------------ workspace
+int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
+  size_t q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+  size_t kmax = std::max(c.dim, std::max(q_dim, c.hidden_dim));
+  int rc;
+  if (n_tok > ws.cap_tok) {
+    size_t n = n_tok;
+    if ((rc = ws.x.alloc(n * c.dim * 4)) || (rc = ws.xb.alloc(n * c.dim * 4)) || (rc = ws.q.alloc(n * q_dim * 4)) ||
+        (rc = ws.k.alloc(n * kv_dim * 4)) || (rc = ws.v.alloc(n * kv_dim * 4)) ||
+        (rc = ws.attn.alloc(n * q_dim * 4)) || (rc = ws.gate.alloc(n * c.hidden_dim * 4)) ||
+        (rc = ws.up.alloc(n * c.hidden_dim * 4)) || (rc = ws.logits.alloc(n * c.vocab_size * 4)) ||
+        (rc = ws.qa.alloc(n * kmax)) || (rc = ws.sa.alloc(n * (kmax / 32 + 1) * 4)) ||
+        (rc = ws.sums.alloc(n * (kmax / 32 + 1) * 4)) || (rc = ws.tokens.alloc(n * 4)) ||
+        (rc = ws.argmax.alloc(n * 4)))
+      return rc;
+    ws.cap_tok = n;
+  }
+  size_t need = std::max(n_tok * c.n_heads * ctx_cap, prefill_attn ? c.n_heads * n_tok * n_tok : 0) * 4;
+  if ((rc = ws.scratch.ensure(need))) return rc;
+  return kOk;
+}
+
+// ------------------------------------------------------------------ cache
+int Cache::create(const Model& m, size_t positions) {
+  len = std::min(positions, m.c.seq_len);
+  kv_dim = m.c.n_kv_heads * m.c.head_dim;
+  n_layers = m.c.n_layers;
+  size_t per = len * kv_dim * 2;
+  int rc = buf.alloc(std::max<size_t>(per * 2 * n_layers, 2));
+  if (rc) return rc;
+  PRANA_HIP(hipMemset(buf.p, 0, buf.bytes));
+  return kOk;
+}
+
+uint16_t* Cache::k(size_t l) const { return buf.as<uint16_t>() + (2 * l) * len * kv_dim; }
+uint16_t* Cache::v(size_t l) const { return buf.as<uint16_t>() + (2 * l + 1) * len * kv_dim; }
+
+// ------------------------------------------------------------------ forward pieces
+int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s) {
+  GemvProfile& gp = gemv_profile();
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (gp.on) {
+    PRANA_HIP(hipEventCreate(&e0));
+    PRANA_HIP(hipEventCreate(&e1));
+    PRANA_HIP(hipEventRecord(e0, s));
+  }
+  int rc = launch_gemv(w.d, xf, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, o, s);
+  if (gp.on) {
+    PRANA_HIP(hipEventRecord(e1, s));
+    gp.pending.push_back({e0, e1, w.stream_bytes, n});
+  }
+  return rc;
+}
+
+GemvProfile& gemv_profile() {
+  static GemvProfile p;
+  return p;
+}
+
+int GemvProfile::collect() {
+  for (auto& r : pending) {
+    PRANA_HIP(hipEventSynchronize(r.e1));
+    float ms = 0.0f;
+    PRANA_HIP(hipEventElapsedTime(&ms, r.e0, r.e1));
+    launches += 1;
+    seconds += ms * 1e-3;
+    bytes += static_cast<double>(r.bytes);
+    (void)hipEventDestroy(r.e0);
+    (void)hipEventDestroy(r.e1);
+  }
+  pending.clear();
+  return kOk;
+}
+
+// Greedy decode of n_steps tokens over an existing cache: feed `token` at
+// `pos`, take the argmax, feed it at pos+1, ... (the sampled part of the
+// generate loop, infer.rs:729-763, without prompt handling or stop ids).
+int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out) {
+  hipStream_t s = ctx().stream;
+  PRANA_CHECK(pos + n_steps <= cache.len, "decode: positions beyond the cache length");
+  int rc = ensure_ws(1, cache.len, false);
+  if (rc) return rc;
+  if ((rc = ws.stream_out.ensure((n_steps + 1) * 4))) return rc;
+  uint32_t* ids = ws.stream_out.as<uint32_t>();
+  // ids[i] feeds step i; step i's argmax lands in ids[i+1].
+  PRANA_HIP(hipMemcpyAsync(ids, &token, 4, hipMemcpyHostToDevice, s));
+  for (size_t i = 0; i < n_steps; i++) {
+    if ((rc = forward_dev(cache, nullptr, ids + i, pos + i, true, s))) return rc;
+    if ((rc = launch_argmax(ws.logits.as<float>(), 1, c.vocab_size, ids + i + 1, s))) return rc;
+  }
+  if (out && n_steps) PRANA_HIP(hipMemcpyAsync(out, ids + 1, n_steps * 4, hipMemcpyDeviceToHost, s));
+  PRANA_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int Model::norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s) {
+  return launch_rmsnorm(x, w.as<float>(), n, c.dim, c.norm_eps, ws.xb.as<float>(), ws.qa.as<int8_t>(),
+                        ws.sa.as<float>(), ws.sums.as<int>(), s);
+}
+
+// The layer stack shared by forward (n = 1), prefill and forward_batch.
+// mode: 0 decode (pos0 = pos), 1 prefill (f32-K/V attention over the window,
+// positions 0..n), 2 verify (cache attention at pos0..pos0+n).
+int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s) {
+  size_t hd = c.head_dim, q_dim = c.n_heads * hd, kv_dim = c.n_kv_heads * hd;
+  float* x = ws.x.as<float>();
+  const float2* tab = rope.as<float2>();
+  int rc;
+  for (size_t l = 0; l < layers.size(); l++) {
+    Layer& L = layers[l];
+    uint16_t* kc = cache.k(l);
+    uint16_t* vc = cache.v(l);
+    // --- attention block (infer.rs:163-188)
+    if ((rc = norm_quant(x, L.vec[kRmsAtt], n, s))) return rc;
+    GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
+    GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
+    GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
+    if ((rc = apply(*L.w[kWq], n, ws.xb.as<float>(), oq, s))) return rc;
+    if ((rc = apply(*L.w[kWk], n, ws.xb.as<float>(), ok, s))) return rc;
+    if ((rc = apply(*L.w[kWv], n, ws.xb.as<float>(), ov, s))) return rc;
+    if (mode == 0) {
+      if ((rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd, tab,
+                               c.rope_neox, kc, vc, nullptr, pos0, s)))
+        return rc;
+      if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
+                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s)))
+        return rc;
+    } else {
+      if ((rc = launch_rope(ws.q.as<float>(), n, q_dim, q_dim, hd, tab, pos0, c.rope_neox, s))) return rc;
+      if ((rc = launch_rope(ws.k.as<float>(), n, kv_dim, kv_dim, hd, tab, pos0, c.rope_neox, s))) return rc;
+      if ((rc = launch_kv_write(kc, pos0, kv_dim, ws.k.as<float>(), n * kv_dim, s))) return rc;
+      if ((rc = launch_kv_write(vc, pos0, kv_dim, ws.v.as<float>(), n * kv_dim, s))) return rc;
+      if (mode == 1)
+        rc = launch_attention_prefill(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, c.n_heads,
+                                      c.n_kv_heads, hd, ws.attn.as<float>(), ws.scratch.as<float>(), s);
+      else
+        rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, n, c.n_heads, c.n_kv_heads, hd,
+                                    ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s);
+      if (rc) return rc;
+    }
+    if ((rc = launch_quantize_acts(ws.attn.as<float>(), n, q_dim, ws.qa.as<int8_t>(), ws.sa.as<float>(),
+                                   ws.sums.as<int>(), s)))
+      return rc;
+    GemvOut ores{x, c.dim, nullptr, 1};
+    if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
+    // --- gated MLP block (infer.rs:191-203)
+    if ((rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
+    GemvOut og{ws.gate.as<float>(), c.hidden_dim, nullptr, 0};
+    GemvOut ou{ws.up.as<float>(), c.hidden_dim, nullptr, 0};
+    if ((rc = apply(*L.w[kW1], n, ws.xb.as<float>(), og, s))) return rc;
+    if ((rc = apply(*L.w[kW3], n, ws.xb.as<float>(), ou, s))) return rc;
+    if ((rc = launch_act_mul(ws.gate.as<float>(), ws.up.as<float>(), n * c.hidden_dim, c.act, ws.qa.as<int8_t>(),
+                             ws.sa.as<float>(), ws.sums.as<int>(), s)))
+      return rc;
+    if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s))) return rc;
+  }
+  return kOk;
+}
+
+// Model::logits / logits_batch (checkpoint.rs:239-265): final norm, then the
+// head over n rows into ws.logits.
+int Model::logits_pass(size_t n, hipStream_t s) {
+  int rc = norm_quant(ws.x.as<float>(), rms_final, n, s);
+  if (rc) return rc;
+  GemvOut o{ws.logits.as<float>(), c.vocab_size, nullptr, 0};
+  return apply(head(), n, ws.xb.as<float>(), o, s);
+}
+
+int Model::embed_tokens(const uint32_t* dev_ids, size_t n, hipStream_t s) {
+  return launch_embed(emb->d, dev_ids, n, c.emb_scale, ws.x.as<float>(), s);
+}
+
+int Model::check_tokens(const uint32_t* t, size_t n) {
+  for (size_t i = 0; i < n; i++)
+    if (t[i] >= c.vocab_size) return fail(kErrInvalid, "token id " + std::to_string(t[i]) + " out of vocabulary");
+  return kOk;
+}
+
+int Model::forward_dev(Cache& cache, const uint32_t* host_token, const uint32_t* dev_token, size_t pos,
+                       bool need_logits, hipStream_t s) {
+  PRANA_CHECK(finalized, "model not finalized");
+  PRANA_CHECK(pos < cache.len, "forward: position beyond the cache length");
+  int rc = ensure_ws(1, cache.len, false);
+  if (rc) return rc;
+  if (host_token) {
+    if ((rc = check_tokens(host_token, 1))) return rc;
+    PRANA_HIP(hipMemcpyAsync(ws.tokens.p, host_token, 4, hipMemcpyHostToDevice, s));
+  }
+  if ((rc = embed_tokens(dev_token ? dev_token : ws.tokens.as<uint32_t>(), 1, s))) return rc;
+  if ((rc = layers_pass(cache, 1, pos, 0, s))) return rc;
+  if (need_logits && (rc = logits_pass(1, s))) return rc;
+  return kOk;
+}
+
+int Model::forward(Cache& cache, uint32_t token, size_t pos, bool need_logits, float* logits_host) {
+  hipStream_t s = ctx().stream;
+  int rc = forward_dev(cache, &token, nullptr, pos, need_logits, s);
+  if (rc) return rc;
+  if (need_logits && logits_host)
+    PRANA_HIP(hipMemcpyAsync(logits_host, ws.logits.p, c.vocab_size * 4, hipMemcpyDeviceToHost, s));
+  PRANA_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int Model::batch_dev(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, int mode, hipStream_t s) {
+  PRANA_CHECK(finalized, "model not finalized");
+  PRANA_CHECK(n > 0, "empty token batch");
+  PRANA_CHECK(pos0 + n <= cache.len, "batch: positions beyond the cache length");
+  int rc = check_tokens(tokens, n);
+  if (rc) return rc;
+  if ((rc = ensure_ws(n, cache.len, mode == 1))) return rc;
+  PRANA_HIP(hipMemcpyAsync(ws.tokens.p, tokens, n * 4, hipMemcpyHostToDevice, s));
+  if ((rc = embed_tokens(ws.tokens.as<uint32_t>(), n, s))) return rc;
+  return layers_pass(cache, n, pos0, mode, s);
+}
+
+int Model::prefill(Cache& cache, const uint32_t* tokens, size_t n) {
+  hipStream_t s = ctx().stream;
+  if (n == 0) return kOk;
+  int rc = batch_dev(cache, tokens, n, 0, 1, s);
+  if (rc) return rc;
+  PRANA_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int Model::forward_batch(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, float* logits_host) {
+  hipStream_t s = ctx().stream;
+  int rc = batch_dev(cache, tokens, n, pos0, 2, s);
+  if (!rc) rc = logits_pass(n, s);
+  if (rc) return rc;
+  if (logits_host)
+    PRANA_HIP(hipMemcpyAsync(logits_host, ws.logits.p, n * c.vocab_size * 4, hipMemcpyDeviceToHost, s));
+  PRANA_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+// ------------------------------------------------------------------ generation
+namespace {
+bool is_stop(uint32_t t, const uint32_t* stops, size_t n) {
+  for (size_t i = 0; i < n; i++)
+    if (stops[i] == t) return true;
+  return false;
+}
+}  // namespace
+
+// generate (infer.rs:696-771), greedy. The sampled id goes from the device
+// argmax straight into the next step's embedding input; the host reads it back
+// only to emit it and test the stop set.
+int Model::generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
+                    uint32_t* out, size_t* n_out, prana_gen_stats* st) {
+  PRANA_CHECK(p > 0, "prompt encoded to zero tokens");
+  hipStream_t s = ctx().stream;
+  size_t max_pos = std::min(c.seq_len, p + steps);
+  Cache cache;
+  int rc = cache.create(*this, max_pos);
+  if (rc) return rc;
+  if ((rc = check_tokens(prompt, p))) return rc;
+  double t0 = now_s();
+  uint32_t token = prompt[0];
+  size_t start_pos = 0, generated = 0;
+  if (p > 1 && p <= max_pos) {
+    if ((rc = prefill(cache, prompt, p - 1))) return rc;
+    start_pos = p - 1;
+    token = prompt[p - 1];
+  }
+  double t1 = now_s();
+  bool token_on_device = false;
+  for (size_t pos = start_pos; pos < max_pos; pos++) {
+    bool need = pos + 1 >= p && pos + 1 < max_pos;
+    if ((rc = forward_dev(cache, token_on_device ? nullptr : &token, nullptr, pos, need, s))) return rc;
+    if (pos + 1 >= max_pos) break;
+    uint32_t next;
+    if (pos + 1 < p) {
+      next = prompt[pos + 1];
+      token_on_device = false;
+    } else {
+      if ((rc = launch_argmax(ws.logits.as<float>(), 1, c.vocab_size, ws.tokens.as<uint32_t>(), s))) return rc;
+      PRANA_HIP(hipMemcpyAsync(&next, ws.tokens.p, 4, hipMemcpyDeviceToHost, s));
+      PRANA_HIP(hipStreamSynchronize(s));
+      token_on_device = true;
+    }
+    if (pos + 1 >= p) {
+      if (is_stop(next, stops, n_stops)) break;
+      out[generated++] = next;
+    }
+    token = next;
+  }
+  PRANA_HIP(hipStreamSynchronize(s));
+  double t2 = now_s();
+  if (n_out) *n_out = generated;
+  if (st) {
+    st->prompt_tokens = p;
+    st->generated_tokens = generated;
+    st->proposed = st->accepted = 0;
+    st->seconds = t2 - t0;
+    st->prefill_seconds = t1 - t0;
+    st->decode_seconds = t2 - t1;
+  }
+  return kOk;
+}
+
+// generate_speculative (infer.rs:581-690), greedy.
+int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, size_t p, size_t steps, size_t k,
+                         const uint32_t* stops, size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* st) {
+  PRANA_CHECK(k >= 1, "draft length must be >= 1");
+  PRANA_CHECK(target.c.vocab_size == draft.c.vocab_size, "draft and target must share a vocabulary");
+  PRANA_CHECK(p > 0, "prompt encoded to zero tokens");
+  hipStream_t s = ctx().stream;
+  size_t V = target.c.vocab_size;
+  size_t max_pos = std::min(target.c.seq_len, p + steps);
+  Cache tc, dc;
+  int rc = tc.create(target, max_pos);
+  if (!rc) rc = dc.create(draft, max_pos);
+  if (rc) return rc;
+  if ((rc = target.check_tokens(prompt, p))) return rc;
+  double t0 = now_s();
+  if (p > 1) {
+    if ((rc = target.prefill(tc, prompt, p - 1))) return rc;
+    if ((rc = draft.prefill(dc, prompt, p - 1))) return rc;
+  }
+  double t1 = now_s();
+  size_t pos = p - 1, generated = 0, proposed = 0, accepted = 0;
+  uint32_t last = prompt[p - 1];
+  std::vector<uint32_t> drafts(k), inputs(k + 1), tnext(k + 1);
+  bool done = false;
+  while (!done && pos + 1 < max_pos) {
+    size_t budget = std::min(max_pos - 1 - pos, k);
+    uint32_t d_tok = last;
+    for (size_t j = 0; j < budget; j++) {
+      if ((rc = draft.forward_dev(dc, &d_tok, nullptr, pos + j, true, s))) return rc;
+      if ((rc = launch_argmax(draft.ws.logits.as<float>(), 1, V, draft.ws.argmax.as<uint32_t>(), s))) return rc;
+      PRANA_HIP(hipMemcpyAsync(&d_tok, draft.ws.argmax.p, 4, hipMemcpyDeviceToHost, s));
+      PRANA_HIP(hipStreamSynchronize(s));
+      drafts[j] = d_tok;
+    }
+    proposed += budget;
+    inputs[0] = last;
+    for (size_t j = 0; j < budget; j++) inputs[j + 1] = drafts[j];
+    if ((rc = target.batch_dev(tc, inputs.data(), budget + 1, pos, 2, s))) return rc;
+    if ((rc = target.logits_pass(budget + 1, s))) return rc;
+    if ((rc = launch_argmax(target.ws.logits.as<float>(), budget + 1, V, target.ws.argmax.as<uint32_t>(), s)))
+      return rc;
+    PRANA_HIP(hipMemcpyAsync(tnext.data(), target.ws.argmax.p, (budget + 1) * 4, hipMemcpyDeviceToHost, s));
+    PRANA_HIP(hipStreamSynchronize(s));
+    for (size_t i = 0; i <= budget; i++) {
+      uint32_t tn = tnext[i];
+      if (i < budget && tn == drafts[i]) accepted++;
+      if (is_stop(tn, stops, n_stops)) {
+        done = true;
+        break;
+      }
+      out[generated++] = tn;
+      pos += 1;
+      last = tn;
+      if (generated >= steps || pos + 1 >= max_pos) {
+        done = true;
+        break;
+      }
+      if (i == budget || tn != drafts[i]) break;
+    }
+  }
+  double t2 = now_s();
+  if (n_out) *n_out = generated;
+  if (st) {
+    st->prompt_tokens = p;
+    st->generated_tokens = generated;
+    st->proposed = proposed;
+    st->accepted = accepted;
+    st->seconds = t2 - t0;
+    st->prefill_seconds = t1 - t0;
+    st->decode_seconds = t2 - t1;
+  }
+  return kOk;
+}
+
+}  // namespace prana

@@ -1,0 +1,112 @@
+// Device-resident Model / KvCache (prana-model checkpoint.rs:32-265,
+// infer.rs:25-45) and the forward passes.
+#pragma once
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/prana_hip.h"
+#include "runtime.h"
+
+namespace prana {
+
+struct Model;
+
+enum LayerMat { kWq = 0, kWk, kWv, kWo, kW1, kW2, kW3 };
+enum LayerVec { kRmsAtt = 0, kRmsFfn, kBq, kBk, kBv };
+
+struct Layer {
+  std::unique_ptr<Mat> w[7];
+  DevBuf vec[5];
+  bool has[5] = {false, false, false, false, false};
+};
+
+// KvCache::with_len: per layer K then V, each [len][kv_dim] f16, one allocation.
+struct Cache {
+  size_t len = 0, kv_dim = 0, n_layers = 0;
+  DevBuf buf;
+  int create(const Model& m, size_t positions);
+  uint16_t* k(size_t l) const;
+  uint16_t* v(size_t l) const;
+};
+
+// Per-model scratch for the passes (single stream; grown on demand).
+struct Workspace {
+  size_t cap_tok = 0;
+  DevBuf x, xb, q, k, v, attn, gate, up, logits;
+  DevBuf qa, sa, sums;  // quantized activations of the current GEMV input
+  DevBuf scratch;       // attention scores
+  DevBuf tokens, argmax;
+  DevBuf stream_out;  // device-side token stream of decode()
+};
+
+// Optional per-launch timing of the model's GEMVs (HIP events on the stream
+// the GEMV runs on), for roofline accounting.
+struct GemvProfile {
+  struct Rec {
+    hipEvent_t e0, e1;
+    size_t bytes, n_tok;
+  };
+  bool on = false;
+  std::vector<Rec> pending;
+  double seconds = 0.0, bytes = 0.0;
+  size_t launches = 0;
+  int collect();
+};
+GemvProfile& gemv_profile();
+
+struct Model {
+  prana_config c{};
+  std::vector<Layer> layers;
+  DevBuf rms_final;
+  bool has_rms_final = false;
+  std::unique_ptr<Mat> emb;   // packed (Q4_0/Q4_K/Q6_K) or dense f32 table
+  std::unique_ptr<Mat> wcls;  // null => classifier tied to emb
+  DevBuf rope;                // float2 [seq_len][head_dim/2] (cos, sin)
+  bool finalized = false;
+  Workspace ws;
+
+  int set_tensor(const std::string& name, int ggml_type, const uint64_t* dims, int n_dims, const void* bytes,
+                 size_t nbytes);
+  int finalize();
+  size_t stream_bytes() const;
+  const Mat& head() const;
+
+  int ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn);
+  int check_tokens(const uint32_t* t, size_t n);
+  int apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s);
+  int norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s);
+  int embed_tokens(const uint32_t* dev_ids, size_t n, hipStream_t s);
+  int layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s);
+  int logits_pass(size_t n, hipStream_t s);
+
+  // The token comes from host_token when given, else from dev_token (a
+  // device id), else from ws.tokens[0].
+  int forward_dev(Cache& cache, const uint32_t* host_token, const uint32_t* dev_token, size_t pos,
+                  bool need_logits, hipStream_t s);
+  int batch_dev(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, int mode, hipStream_t s);
+
+  int forward(Cache& cache, uint32_t token, size_t pos, bool need_logits, float* logits_host);
+  int decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out);
+  int prefill(Cache& cache, const uint32_t* tokens, size_t n);
+  int forward_batch(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, float* logits_host);
+  int generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
+               uint32_t* out, size_t* n_out, prana_gen_stats* st);
+};
+
+int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, size_t p, size_t steps, size_t k,
+                         const uint32_t* stops, size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* st);
+
+}  // namespace prana
+
+struct prana_model {
+  prana::Model m;
+};
+struct prana_cache {
+  prana::Cache c;
+  prana_model* owner;
+};
+struct prana_mat {
+  prana::Mat m;
+};

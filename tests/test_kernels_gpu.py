@@ -1,0 +1,271 @@
+"""GPU parity: every kernel entry point of libprana_hip against the CPU oracle
+on the same seeded inputs. Integer and f32 results must be bit-identical
+(compared as raw bits), except gelu_tanh (libm tanhf boundary, 1e-6 rel)."""
+import numpy as np
+import pytest
+
+import prana_amd as P
+from oracle import oracle as O
+from tests import fixtures as fx
+
+pytestmark = pytest.mark.gpu
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ quantize_acts
+@pytest.mark.parametrize("rows,k", [(1, 32), (3, 288), (2, 4096), (5, 14336)])
+def test_quantize_acts(rows, k):
+    x = rng(k).standard_normal((rows, k)).astype(np.float32) * 2
+    x[0, :32] = 0.0            # zero block
+    x[-1, -32:] *= 1e-30       # tiny block
+    q, s, m = P.quantize_acts(x)
+    qo, so, mo = O.quantize_acts(x)
+    assert np.array_equal(q, qo) and same_bits(s, so) and np.array_equal(m, mo)
+
+
+# ------------------------------------------------------------------ matmul per format
+def _mat_pair(ty, rows, cols, seed, real=False):
+    if real:
+        raw = P.synth_tensor(ty, rows, cols, seed, 0.02)
+    else:
+        raw = fx.pseudo_blocks(ty, rows, cols, seed)
+    return raw, P.Matrix(ty, rows, cols, raw), O.Mat.from_ggml(ty, rows, cols, raw)
+
+
+@pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0, fx.Q4_K, fx.Q6_K])
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_matmul_formats_small(ty, n_tok):
+    rows, cols = 37, 512
+    raw, g, o = _mat_pair(ty, rows, cols, 21 + n_tok)
+    a = fx.sin_row(n_tok * cols, 0.013).reshape(n_tok, cols)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0, fx.Q4_K, fx.Q6_K])
+def test_block_sums_exact(ty):
+    rows, cols = 19, 1024
+    raw, g, o = _mat_pair(ty, rows, cols, 5)
+    a = rng(9).standard_normal((2, cols)).astype(np.float32)
+    q, s, m = O.quantize_acts(a)
+    got = g.block_sums(q, m)
+    for t in range(2):
+        assert np.array_equal(got[t], fx.np_block_isums(ty, raw, rows, cols, q[t]))
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)])
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_q8_0_config1_shapes(shape, n_tok):
+    rows, cols = shape
+    raw, g, o = _mat_pair(fx.Q8_0, rows, cols, 100 + rows + cols, real=True)
+    a = rng(rows).standard_normal((n_tok, cols)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("shape", [(6144, 4096), (4096, 14336)])
+def test_q4_0_7b_shapes(shape):
+    rows, cols = shape
+    raw, g, o = _mat_pair(fx.Q4_0, rows, cols, 7, real=True)
+    a = rng(3).standard_normal((1, cols)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+def test_matmul_prefill_rows_equal_decode():
+    rows, cols, n = 300, 896, 6
+    raw, g, o = _mat_pair(fx.Q4_0, rows, cols, 31, real=True)
+    a = rng(4).standard_normal((n, cols)).astype(np.float32)
+    q, s, m = O.quantize_acts(a)
+    pre = g.apply_prefill(q, s, m)
+    assert same_bits(pre, o.apply_prefill(q, s, m))
+    for t in range(n):
+        assert same_bits(pre[t], g.apply(a[t])[0])
+
+
+def test_q8_f32_scales_parts():
+    w = rng(2).standard_normal((64, 256)).astype(np.float32)
+    q, s = O.quantize_q8(w)
+    g, o = P.Matrix.q8_parts(q, s), O.Mat.q8_parts(q, s)
+    a = rng(8).standard_normal((2, 256)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("cols", [32, 288, 301])
+def test_dense_f32(cols):
+    w = rng(cols).standard_normal((70, cols)).astype(np.float32)
+    a = rng(cols + 1).standard_normal((3, cols)).astype(np.float32)
+    g = P.Matrix(fx.F32, 70, cols, w.view(np.uint8).reshape(-1))
+    assert same_bits(g.apply(a), O.Mat.f32(w).apply(a))
+
+
+@pytest.mark.parametrize("ty", [fx.F32, fx.Q8_0, fx.Q4_0, fx.Q4_K, fx.Q6_K])
+def test_embed_rows(ty):
+    rows, cols = 50, 512
+    if ty == fx.F32:
+        w = rng(1).standard_normal((rows, cols)).astype(np.float32)
+        raw = w.view(np.uint8).reshape(-1)
+    else:
+        raw = fx.pseudo_blocks(ty, rows, cols, 17)
+    g = P.Matrix(ty, rows, cols, raw)
+    toks = [0, 7, 49, 7]
+    got = g.embed_rows(toks)
+    ref = fx.np_dequant(ty, raw, rows, cols) if ty != fx.F32 else w
+    om = O.Mat.from_ggml(ty, rows, cols, raw)
+    for i, t in enumerate(toks):
+        assert same_bits(got[i], om.row_f32(t))
+    assert np.allclose(got, ref[toks], rtol=0, atol=1e-6)
+    assert same_bits(g.embed_rows([3], scale=2.5)[0], om.row_f32(3) * np.float32(2.5))
+
+
+# ------------------------------------------------------------------ norms / activations
+@pytest.mark.parametrize("rows,dim", [(1, 288), (4, 896), (2, 4096)])
+def test_rmsnorm(rows, dim):
+    x = rng(dim).standard_normal((rows, dim)).astype(np.float32)
+    w = (1 + 0.1 * rng(dim + 1).standard_normal(dim)).astype(np.float32)
+    assert same_bits(P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5))
+
+
+def test_silu_and_expf():
+    x = np.concatenate([rng(1).standard_normal(100000).astype(np.float32) * 10,
+                        np.array([0.0, -0.0, 88.0, -88.0, 100.0, -104.0, -110.0, np.inf, -np.inf], np.float32)])
+    assert same_bits(P.silu(x), O.silu(x))
+    # device expf against the host glibc expf on the same points
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    pts = np.concatenate([x[:3000], x[-9:]])
+    want = np.array([libm.expf(float(v)) for v in pts], np.float32)
+    assert same_bits(P.expf(pts), want)
+
+
+def test_expf_exhaustive():
+    # Device expf vs the host glibc expf over every f32 bit pattern (16 chunks).
+    import ctypes
+    lib = P.load()
+    n = 1 << 28
+    d = P.DeviceArray((n,), np.float32)
+    for c in range(16):
+        base = c * n
+        x = np.arange(base, base + n, dtype=np.uint32).view(np.float32)
+        dx = P.DeviceArray.from_host(x)
+        P.check(lib.prana_expf(dx.ptr, n, d.ptr, None))
+        got = d.to_host()
+        want = O.expf_bits(base, n, 16)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), c
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), c
+        dx.free()
+
+
+def test_gelu_tanh_tolerance():
+    # gelu_tanh is Gemma-only; device tanhf vs glibc tanhf is the libm
+    # boundary, so this is a tolerance check (1e-6 relative + 1e-7).
+    x = rng(5).standard_normal(50000).astype(np.float32) * 4
+    g, o = P.gelu_tanh(x), O.gelu_tanh(x)
+    assert np.all(np.abs(g - o) <= 1e-6 * np.abs(o) + 1e-7)
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 256, 2049])
+def test_softmax(n):
+    x = rng(n).standard_normal((3, n)).astype(np.float32) * 5
+    got = P.softmax(x)
+    for r in range(3):
+        assert same_bits(got[r], O.softmax(x[r]))
+
+
+# ------------------------------------------------------------------ RoPE / KV
+@pytest.mark.parametrize("neox", [0, 1])
+@pytest.mark.parametrize("hd,theta", [(48, 1e4), (64, 1e6), (128, 1e4)])
+def test_rope(neox, hd, theta):
+    nh, rows, pos0 = 4, 5, 250
+    x = rng(hd).standard_normal((rows, nh * hd)).astype(np.float32)
+    got = P.rope(x, pos0, hd, theta, neox)
+    f = O.rope_neox if neox else O.rope_interleaved
+    for t in range(rows):
+        assert same_bits(got[t], f(x[t], pos0 + t, hd, theta))
+
+
+def test_kv_write_f16_all_patterns():
+    # f32 -> f16 on tie points, specials and randoms, against the oracle.
+    h = np.arange(0, 0x7BFF, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)
+    x = np.concatenate([mid, np.nextafter(mid, np.float32(1e9)), rng(1).standard_normal(50000).astype(np.float32),
+                        np.array([np.inf, -np.inf, np.nan, 1e30, -1e-30, 65520.0], np.float32)])
+    x = np.concatenate([x, -x])
+    got = P.f32_to_f16(x)
+    want = np.array([O.f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+    allh = np.arange(65536, dtype=np.uint16)
+    back = P.f16_to_f32(allh)
+    wantb = np.array([O.f16_to_f32(int(v)) for v in allh], np.float32)
+    assert np.array_equal(back.view(np.uint32), wantb.view(np.uint32))
+
+
+def test_kv_write_rows():
+    kv_stride, rows = 64, 6
+    cache = np.zeros(rows * kv_stride, np.uint16)
+    src = rng(2).standard_normal(2 * kv_stride).astype(np.float32)
+    dc = P.DeviceArray.from_host(cache)
+    ds = P.DeviceArray.from_host(src)
+    P.check(P.load().prana_kv_write_f16(dc.ptr, 3, kv_stride, ds.ptr, src.size, None))
+    assert np.array_equal(dc.to_host(), O.f16_kv_write(cache, 3, kv_stride, src))
+
+
+# ------------------------------------------------------------------ attention
+def _cache(n, nkv, hd, seed):
+    r = rng(seed)
+    kc = r.standard_normal(n * nkv * hd).astype(np.float32).astype(np.float16).view(np.uint16)
+    vc = r.standard_normal(n * nkv * hd).astype(np.float32).astype(np.float16).view(np.uint16)
+    return kc, vc
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 255), (14, 2, 64, 700), (32, 8, 128, 1030)])
+def test_attention_decode(nh, nkv, hd, pos):
+    kc, vc = _cache(pos + 1, nkv, hd, pos)
+    q = rng(pos + 3).standard_normal(nh * hd).astype(np.float32)
+    assert same_bits(P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd))
+
+
+def test_attention_verify():
+    nh, nkv, hd, pos0, seq = 32, 8, 128, 512, 9
+    kc, vc = _cache(pos0 + seq, nkv, hd, 4)
+    q = rng(5).standard_normal(seq * nh * hd).astype(np.float32)
+    assert same_bits(P.attention_verify(q, kc, vc, pos0, seq, nh, nkv, hd),
+                     O.attention_verify(q, kc, vc, pos0, seq, nh, nkv, hd))
+
+
+@pytest.mark.parametrize("seq,nh,nkv,hd", [(1, 2, 2, 16), (37, 14, 2, 64), (64, 6, 6, 48)])
+def test_attention_prefill(seq, nh, nkv, hd):
+    r = rng(seq)
+    q = r.standard_normal(seq * nh * hd).astype(np.float32)
+    k = r.standard_normal(seq * nkv * hd).astype(np.float32)
+    v = r.standard_normal(seq * nkv * hd).astype(np.float32)
+    assert same_bits(P.attention_prefill(q, k, v, seq, nh, nkv, hd), O.attention(q, k, v, seq, nh, nkv, hd))
+
+
+# ------------------------------------------------------------------ argmax
+def test_argmax_semantics():
+    rows = [
+        rng(1).standard_normal(32000).astype(np.float32),
+        np.array([1.0, 3.0, 3.0, 2.0], np.float32),             # first max wins
+        np.array([np.nan, 5.0, 7.0], np.float32),               # NaN at 0 pins 0
+        np.array([5.0, np.nan, 7.0, 7.0], np.float32),          # later NaN ignored
+        np.full(10, -np.inf, np.float32),                       # all -inf -> 0
+        np.array([-np.inf, np.nan, -1.0], np.float32),
+    ]
+    for r in rows:
+        assert P.argmax(r)[0] == O.argmax(r), r
+    big = rng(2).standard_normal((5, 151936)).astype(np.float32)
+    big[3, 1000] = big[3, 2000] = 100.0
+    got = P.argmax(big)
+    assert [int(v) for v in got] == [O.argmax(b) for b in big]

@@ -1,0 +1,155 @@
+"""GPU parity of the model layer: logits, KV caches and greedy token streams
+of the device Model against the CPU oracle built from the same tensor bytes,
+from the reference's tiny test models up to the 7B benchmark shape."""
+import numpy as np
+import pytest
+
+import prana_amd as P
+from prana_amd import models as M
+from oracle import oracle as O
+from tests import fixtures as fx
+
+pytestmark = pytest.mark.gpu
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def pair(cfg, t):
+    return P.Model(cfg, t), O.Model(cfg, t)
+
+
+# ------------------------------------------------------------------ the reference's tiny GGUF models (F32 weights)
+@pytest.mark.parametrize("arch", ["llama", "qwen2"])
+def test_tiny_forward_logits_and_cache_bitexact(arch):
+    cfg, t = fx.synthetic_model(arch, arch == "qwen2")
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(16), o.cache(16)
+    toks = [5, 3, 9, 44, 0, 17]
+    for pos, tok in enumerate(toks):
+        assert same_bits(gc.forward(tok, pos), oc.forward(tok, pos)), pos
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, len(toks)), oc.read(layer, which, len(toks)))
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen2"])
+def test_tiny_prefill_then_decode_bitexact(arch):
+    cfg, t = fx.synthetic_model(arch, arch == "qwen2")
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(16), o.cache(16)
+    toks = [3, 9, 14, 7, 21]
+    gc.prefill(toks)
+    oc.prefill(toks)
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(gc.read(layer, 0, 5), oc.read(layer, 0, 5))
+    assert same_bits(gc.forward(5, 5), oc.forward(5, 5))
+
+
+def test_tiny_forward_batch_bitexact():
+    cfg, t = fx.synthetic_model("qwen2", True)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(16), o.cache(16)
+    gc.prefill([3, 9, 14])
+    oc.prefill([3, 9, 14])
+    assert same_bits(gc.forward_batch([7, 21, 4, 40], 3), oc.forward_batch([7, 21, 4, 40], 3))
+
+
+@pytest.mark.parametrize("draft_arch", ["qwen2", "llama"])
+def test_tiny_speculative_equals_greedy_and_oracle(draft_arch):
+    cfg, t = fx.synthetic_model("qwen2", True)
+    dcfg, dt = fx.synthetic_model(draft_arch, draft_arch == "qwen2")
+    g, o = pair(cfg, t)
+    gd, od = pair(dcfg, dt)
+    prompt, stops = [5, 7, 9], (46, 47)
+    plain, _ = g.generate(prompt, 8, stops)
+    plain_o, _ = o.generate(prompt, 8, stops)
+    spec, st = P.generate_speculative(g, gd, prompt, 8, 4, stops)
+    spec_o, st_o = O.generate_speculative(o, od, prompt, 8, 4, stops)
+    assert list(plain) == list(plain_o)
+    assert list(spec) == list(spec_o)
+    assert (st.proposed, st.accepted) == (st_o.proposed, st_o.accepted)
+    # The guarantee of gguf.rs:746-799, on the device path.
+    assert list(spec)[: len(plain)] == list(plain)[: len(spec)]
+
+
+# ------------------------------------------------------------------ config 0: 15M shape, Q8_0, 256-step greedy decode
+@pytest.fixture(scope="module")
+def c0():
+    t = M.c0_tensors(seed=1)
+    return M.C0, t
+
+
+def test_c0_greedy_256_token_identical(c0):
+    cfg, t = c0
+    g, o = pair(cfg, t)
+    prompt = np.random.default_rng(20260712).integers(0, cfg["vocab_size"], 5).astype(np.uint32)
+    go, gst = g.generate(prompt, 256)
+    oo, ost = o.generate(prompt, 256)
+    # max_pos = min(256, 5 + 256): positions 4..254 sample, 251 tokens.
+    assert len(oo) == 251
+    assert list(go) == list(oo)
+    assert gst.generated_tokens == ost.generated_tokens == 251
+
+
+def test_c0_logits_bitexact_along_the_stream(c0):
+    cfg, t = c0
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(64), o.cache(64)
+    prompt = [11, 2200, 31999, 0, 17]
+    gc.prefill(prompt[:4])
+    oc.prefill(prompt[:4])
+    tok = prompt[4]
+    for pos in range(4, 40):
+        lg, lo = gc.forward(tok, pos), oc.forward(tok, pos)
+        assert same_bits(lg, lo), pos
+        tok = int(np.argmax(lo))
+
+
+# ------------------------------------------------------------------ config 2: qwen2-0.5B shape, K-quant mixture
+def test_c2_qwen2_05b_short_decode_token_identical():
+    cfg = M.C2
+    t = M.c2_tensors(seed=2)
+    g, o = pair(cfg, t)
+    prompt = np.random.default_rng(2).integers(0, cfg["vocab_size"], 12).astype(np.uint32)
+    go, _ = g.generate(prompt, 6)
+    oo, _ = o.generate(prompt, 6)
+    assert list(go) == list(oo)
+    gc, oc = g.cache(32), o.cache(32)
+    gc.prefill(prompt[:8])
+    oc.prefill(prompt[:8])
+    assert same_bits(gc.forward(int(prompt[8]), 8), oc.forward(int(prompt[8]), 8))
+
+
+# ------------------------------------------------------------------ config 4: 7B shape, Q4_0
+@pytest.fixture(scope="module")
+def c4():
+    return M.C4, M.c4_tensors(seed=4)
+
+
+def test_c4_7b_decode_token_identical(c4):
+    cfg, t = c4
+    g, o = pair(cfg, t)
+    prompt = np.random.default_rng(4).integers(0, cfg["vocab_size"], 4).astype(np.uint32)
+    go, _ = g.generate(prompt, 5)
+    oo, _ = o.generate(prompt, 5)
+    assert len(oo) == 5
+    assert list(go) == list(oo)
+
+
+@pytest.mark.parametrize("k", [4, 8])
+def test_c4_speculative_equals_plain_greedy(c4, k):
+    cfg, t = c4
+    g = P.Model(cfg, t)
+    draft = P.Model(M.c4_draft_config(), M.synth_tensors(M.c4_draft_config(), M.types_c0, 1))
+    prompt = np.random.default_rng(44).integers(0, cfg["vocab_size"], 32).astype(np.uint32)
+    plain, _ = g.generate(prompt, 24)
+    spec, st = P.generate_speculative(g, draft, prompt, 24, k)
+    assert list(spec) == list(plain)
+    # self-draft: the target drafting for itself accepts everything
+    spec2, st2 = P.generate_speculative(g, g, prompt, 12, k)
+    assert list(spec2) == list(plain[:12])
+    assert st2.accepted == st2.proposed
