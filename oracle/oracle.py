@@ -34,6 +34,8 @@ _SIGS = {
     "po_f16_to_f32": (c_float, [C.c_uint16]),
     "po_f32_to_f16": (C.c_uint16, [c_float]),
     "po_expf_bits": (None, [C.c_uint32, c_size, c_vp, c_int]),
+    "po_f16_to_f32_n": (None, [c_vp, c_size, c_vp]),
+    "po_f32_to_f16_n": (None, [c_vp, c_size, c_vp]),
     "po_quantize_acts": (None, [c_vp, c_size, c_vp, c_vp, c_vp]),
     "po_quantize_q8": (None, [c_size, c_size, c_vp, c_vp, c_vp]),
     "po_dot_f32": (c_float, [c_vp, c_vp, c_size]),
@@ -116,6 +118,20 @@ def f16_to_f32(h):
 
 def f32_to_f16(x):
     return lib().po_f32_to_f16(float(x))
+
+
+def f16_to_f32_n(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().po_f16_to_f32_n(P(h), h.size, P(out))
+    return out
+
+
+def f32_to_f16_n(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().po_f32_to_f16_n(P(x), x.size, P(out))
+    return out
 
 
 def expf_bits(base, n, threads=16):

@@ -64,6 +64,13 @@ uint16_t po_f32_to_f16(float x) {
   return sign | (uint16_t)(half + round);
 }
 
+void po_f16_to_f32_n(const uint16_t *h, size_t n, float *out) {
+  for (size_t i = 0; i < n; i++) out[i] = po_f16_to_f32(h[i]);
+}
+void po_f32_to_f16_n(const float *x, size_t n, uint16_t *out) {
+  for (size_t i = 0; i < n; i++) out[i] = po_f32_to_f16(x[i]);
+}
+
 typedef struct { uint32_t base; size_t i0, i1; float *out; } expf_job;
 static void *expf_run(void *p) {
   expf_job *j = p;

@@ -25,6 +25,10 @@ extern "C" {
 /* ---------------- f16 (prana-kernels/src/lib.rs:57-113) ---------------- */
 float po_f16_to_f32(uint16_t h);
 uint16_t po_f32_to_f16(float x);
+/* Bulk forms (results written as raw bits: no float->double hop that would
+ * quiet signalling NaNs on the way to a caller). */
+void po_f16_to_f32_n(const uint16_t *h, size_t n, float *out);
+void po_f32_to_f16_n(const float *x, size_t n, uint16_t *out);
 
 /* Bulk host-libm expf over [base, base+n) f32 bit patterns (the reference's
  * f32::exp is glibc expf), threaded; for exhaustive device comparisons. */

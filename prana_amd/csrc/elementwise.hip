@@ -5,6 +5,7 @@
 // order by a single lane; order-free parts (max, integer sums, elementwise
 // products) run in parallel.
 #include "common.h"
+#include "exact_sum.h"
 #include "kernels.h"
 
 namespace prana {
@@ -48,16 +49,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                                                       int dim, float eps, float* __restrict__ out,
                                                       int8_t* __restrict__ q, float* __restrict__ sa,
                                                       int* __restrict__ sums) {
-  __shared__ float s_inv;
+  extern __shared__ float sq[];  // dim squares
   const float* row = x + (size_t)blockIdx.x * dim;
-  if (threadIdx.x == 0) {
-    float ss = -0.0f;
-    for (int i = 0; i < dim; i++) ss += row[i] * row[i];
-    float mean_sq = ss / static_cast<float>(dim);
-    s_inv = 1.0f / sqrtf(mean_sq + eps);
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    float v = row[i];
+    sq[i] = v * v;
   }
   __syncthreads();
-  float inv = s_inv;
+  // sum of squares in the reference's left-to-right order (norms.rs:15)
+  const float ss = exact::block_seq_sum_nonneg(sq, dim);
+  const float mean_sq = ss / static_cast<float>(dim);
+  const float inv = 1.0f / sqrtf(mean_sq + eps);
   // dim is a multiple of 32 whenever q != nullptr; round the loop up to a
   // whole number of 32-lane groups so every group reduces together.
   int span = q ? ((dim + 255) / 256) * 256 : dim;
@@ -85,7 +87,8 @@ int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, floa
                    float* sa, int* sums, hipStream_t s) {
   if (rows == 0) return kOk;
   PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, w, (int)dim, eps, out, q, sa, sums);
+  PRANA_CHECK(dim * 4 <= 64 * 1024, "rmsnorm: dim above 16384");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), dim * 4, s, x, w, (int)dim, eps, out, q, sa, sums);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -145,13 +148,9 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   for (int i = threadIdx.x; i < n; i += 256) dst[i] = dev_expf(row[i] - mx);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = -0.0f;
-    for (int i = 0; i < n; i++) sum += dst[i];
-    s_inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  }
-  __syncthreads();
-  float inv = s_inv;
+  const float sum = exact::block_seq_sum_nonneg(dst, n);  // norms.rs:53 order
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  (void)s_inv;
   for (int i = threadIdx.x; i < n; i += 256) dst[i] = dst[i] * inv;
 }
 

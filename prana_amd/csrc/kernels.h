@@ -57,9 +57,21 @@ struct GemvOut {
   const float* bias;
   int residual;
 };
+// Token counts up to this use the weight-streaming decode kernel (and
+// launch_gemv_act); larger batches use the tiled kernel.
+constexpr size_t kGemvDecodeMaxTokens = 16;
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s);
+// Up to three quantized matrices of one kind sharing the input (fused
+// Q|K|V), one launch.
+int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
+                      size_t n_tok, hipStream_t s);
+// gate|up in one launch with the activation fused: h = act(gate) * up
+// (norms.rs:27-41, infer.rs:193-199), quantized for the down projection;
+// act 0 = silu, 1 = gelu_tanh. h (f32) is optional.
+int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t* q, const float* sa, const int* sums,
+                    size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
 // The exact i32 part of every term (debug / bit-exactness entry point):
 // isums[t][r][term] with T terms per row (cols/32, or cols/16 for Q6_K).
 int launch_block_isums(const DevMat& m, const int8_t* q, const int* sums, size_t n_tok, int* isums, hipStream_t s);

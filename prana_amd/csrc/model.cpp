@@ -186,7 +186,9 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
         (rc = ws.attn.alloc(n * q_dim * 4)) || (rc = ws.gate.alloc(n * c.hidden_dim * 4)) ||
         (rc = ws.up.alloc(n * c.hidden_dim * 4)) || (rc = ws.logits.alloc(n * c.vocab_size * 4)) ||
         (rc = ws.qa.alloc(n * kmax)) || (rc = ws.sa.alloc(n * (kmax / 32 + 1) * 4)) ||
-        (rc = ws.sums.alloc(n * (kmax / 32 + 1) * 4)) || (rc = ws.tokens.alloc(n * 4)) ||
+        (rc = ws.sums.alloc(n * (kmax / 32 + 1) * 4)) || (rc = ws.hq.alloc(n * c.hidden_dim)) ||
+        (rc = ws.hsa.alloc(n * (c.hidden_dim / 32) * 4)) || (rc = ws.hsum.alloc(n * (c.hidden_dim / 32) * 4)) ||
+        (rc = ws.tokens.alloc(n * 4)) ||
         (rc = ws.argmax.alloc(n * 4)))
       return rc;
     ws.cap_tok = n;
@@ -212,7 +214,8 @@ uint16_t* Cache::k(size_t l) const { return buf.as<uint16_t>() + (2 * l) * len *
 uint16_t* Cache::v(size_t l) const { return buf.as<uint16_t>() + (2 * l + 1) * len * kv_dim; }
 
 // ------------------------------------------------------------------ forward pieces
-int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s) {
+template <class F>
+int Model::timed(size_t bytes, size_t n, hipStream_t s, F&& launch) {
   GemvProfile& gp = gemv_profile();
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (gp.on) {
@@ -220,12 +223,62 @@ int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipS
     PRANA_HIP(hipEventCreate(&e1));
     PRANA_HIP(hipEventRecord(e0, s));
   }
-  int rc = launch_gemv(w.d, xf, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, o, s);
+  int rc = launch();
   if (gp.on) {
     PRANA_HIP(hipEventRecord(e1, s));
-    gp.pending.push_back({e0, e1, w.stream_bytes, n});
+    gp.pending.push_back({e0, e1, bytes, n});
   }
   return rc;
+}
+
+int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s, bool hset) {
+  return timed(w.stream_bytes, n, s, [&] {
+    if (hset) return launch_gemv(w.d, xf, ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), n, o, s);
+    return launch_gemv(w.d, xf, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, o, s);
+  });
+}
+
+int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s) {
+  int i = 0;
+  while (i < n_mats) {
+    int j = i + 1;
+    while (j < n_mats && j - i < 3 && w[j]->d.kind == w[i]->d.kind && w[j]->d.cols == w[i]->d.cols) j++;
+    if (j - i == 1 || w[i]->d.kind == kKindF32) {
+      for (int k = i; k < j; k++)
+        if (int rc = apply(*w[k], n, xf, o[k], s)) return rc;
+    } else {
+      DevMat d[3];
+      size_t bytes = 0;
+      for (int k = i; k < j; k++) {
+        d[k - i] = w[k]->d;
+        bytes += w[k]->stream_bytes;
+      }
+      int rc = timed(bytes, n, s, [&] {
+        return launch_gemv_multi(d, o + i, j - i, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, s);
+      });
+      if (rc) return rc;
+    }
+    i = j;
+  }
+  return kOk;
+}
+
+int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s) {
+  const size_t H = c.hidden_dim;
+  const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens;
+  if (fuse) {
+    return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {
+      return launch_gemv_act(gate.d, up.d, c.act, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n,
+                             ws.gate.as<float>(), ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s);
+    });
+  }
+  GemvOut og{ws.gate.as<float>(), H, nullptr, 0};
+  GemvOut ou{ws.up.as<float>(), H, nullptr, 0};
+  const Mat* w[2] = {&gate, &up};
+  const GemvOut o[2] = {og, ou};
+  if (int rc = apply_multi(w, o, 2, n, ws.xb.as<float>(), s)) return rc;
+  return launch_act_mul(ws.gate.as<float>(), ws.up.as<float>(), n * H, c.act, ws.hq.as<int8_t>(), ws.hsa.as<float>(),
+                        ws.hsum.as<int>(), s);
 }
 
 GemvProfile& gemv_profile() {
@@ -291,9 +344,11 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
     GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
     GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
-    if ((rc = apply(*L.w[kWq], n, ws.xb.as<float>(), oq, s))) return rc;
-    if ((rc = apply(*L.w[kWk], n, ws.xb.as<float>(), ok, s))) return rc;
-    if ((rc = apply(*L.w[kWv], n, ws.xb.as<float>(), ov, s))) return rc;
+    {
+      const Mat* w[3] = {L.w[kWq].get(), L.w[kWk].get(), L.w[kWv].get()};
+      const GemvOut o[3] = {oq, ok, ov};
+      if ((rc = apply_multi(w, o, 3, n, ws.xb.as<float>(), s))) return rc;
+    }
     if (mode == 0) {
       if ((rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd, tab,
                                c.rope_neox, kc, vc, nullptr, pos0, s)))
@@ -321,14 +376,8 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
     // --- gated MLP block (infer.rs:191-203)
     if ((rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
-    GemvOut og{ws.gate.as<float>(), c.hidden_dim, nullptr, 0};
-    GemvOut ou{ws.up.as<float>(), c.hidden_dim, nullptr, 0};
-    if ((rc = apply(*L.w[kW1], n, ws.xb.as<float>(), og, s))) return rc;
-    if ((rc = apply(*L.w[kW3], n, ws.xb.as<float>(), ou, s))) return rc;
-    if ((rc = launch_act_mul(ws.gate.as<float>(), ws.up.as<float>(), n * c.hidden_dim, c.act, ws.qa.as<int8_t>(),
-                             ws.sa.as<float>(), ws.sums.as<int>(), s)))
-      return rc;
-    if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s))) return rc;
+    if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s))) return rc;
+    if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s, true))) return rc;
   }
   return kOk;
 }

@@ -36,6 +36,7 @@ struct Workspace {
   size_t cap_tok = 0;
   DevBuf x, xb, q, k, v, attn, gate, up, logits;
   DevBuf qa, sa, sums;  // quantized activations of the current GEMV input
+  DevBuf hq, hsa, hsum;  // quantized MLP hidden state (input of the down projection)
   DevBuf scratch;       // attention scores
   DevBuf tokens, argmax;
   DevBuf stream_out;  // device-side token stream of decode()
@@ -75,7 +76,16 @@ struct Model {
 
   int ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn);
   int check_tokens(const uint32_t* t, size_t n);
-  int apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s);
+  // hset: read the quantized MLP hidden state (ws.hq) instead of ws.qa.
+  int apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s, bool hset = false);
+  // Several matrices over the same input (Q|K|V); runs of equal kind share a launch.
+  int apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s);
+  // gate/up projections with the activation and the down projection's
+  // quantization fused when both share a kind; h lands in ws.gate (f32) and
+  // ws.hq/hsa/hsum (quantized).
+  int apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s);
+  template <class F>
+  int timed(size_t bytes, size_t n, hipStream_t s, F&& launch);
   int norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s);
   int embed_tokens(const uint32_t* dev_ids, size_t n, hipStream_t s);
   int layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s);

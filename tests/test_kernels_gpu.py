@@ -203,12 +203,10 @@ def test_kv_write_f16_all_patterns():
                         np.array([np.inf, -np.inf, np.nan, 1e30, -1e-30, 65520.0], np.float32)])
     x = np.concatenate([x, -x])
     got = P.f32_to_f16(x)
-    want = np.array([O.f32_to_f16(float(v)) for v in x], np.uint16)
-    assert np.array_equal(got, want)
+    assert np.array_equal(got, O.f32_to_f16_n(x))
+    # every half, NaN payloads included, compared as raw bits
     allh = np.arange(65536, dtype=np.uint16)
-    back = P.f16_to_f32(allh)
-    wantb = np.array([O.f16_to_f32(int(v)) for v in allh], np.float32)
-    assert np.array_equal(back.view(np.uint32), wantb.view(np.uint32))
+    assert np.array_equal(P.f16_to_f32(allh).view(np.uint32), O.f16_to_f32_n(allh).view(np.uint32))
 
 
 def test_kv_write_rows():

@@ -149,7 +149,10 @@ def test_c4_speculative_equals_plain_greedy(c4, k):
     plain, _ = g.generate(prompt, 24)
     spec, st = P.generate_speculative(g, draft, prompt, 24, k)
     assert list(spec) == list(plain)
-    # self-draft: the target drafting for itself accepts everything
+    # Self-draft. The reference's loop advances past the last accepted draft
+    # token without feeding it to the draft (infer.rs:629-681), so the draft
+    # cache keeps a stale row and acceptance is high but not total; the
+    # reference test asserts accepted > 0 (gguf.rs:795-797).
     spec2, st2 = P.generate_speculative(g, g, prompt, 12, k)
     assert list(spec2) == list(plain[:12])
-    assert st2.accepted == st2.proposed
+    assert 0 < st2.accepted <= st2.proposed
