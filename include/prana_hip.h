@@ -107,7 +107,7 @@ int prana_matmul_block_sums(prana_mat_t w, const int8_t *q, const int32_t *sums,
  * scale when scale != 1 (infer.rs:155-159). out[n*cols]. */
 int prana_embed_rows(prana_mat_t table, const uint32_t *tokens, size_t n, float scale, float *out,
                      prana_stream_t stream);
-/* rmsnorm (norms.rs:9-23), rows x dim. */
+/* rmsnorm (norms.rs:9-23), rows x dim, dim <= 16320. */
 int prana_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float eps, float *out,
                   prana_stream_t stream);
 /* silu in place (norms.rs:27-31); gelu_tanh in place (norms.rs:35-41). */

@@ -5,7 +5,12 @@
 //            sum = fold_t e_t (the sequential fold, evaluated exactly by
 //            the whole workgroup), p_t = e_t * (1/sum)
 //   out[d]  = fold_t p_t * v_t[d] from 0.0                     parallel over d
-// One workgroup per (query row, head).
+//
+// One workgroup per (query row, head, slice of head dims). Every slice
+// recomputes the head's probabilities (K rows are shared through L2: the
+// slices and the heads of one KV group are placed on the same XCD) and then
+// folds its own dims; V rows of the slice stream through LDS in chunks that
+// are fetched with 16-byte loads one chunk ahead of the fold.
 #include "common.h"
 #include "exact_sum.h"
 #include "kernels.h"
@@ -14,34 +19,35 @@ namespace prana {
 
 namespace {
 
+constexpr int kNT = 256;             // lanes per workgroup
+constexpr int kScoreLds = 4096;      // probabilities kept in LDS up to this length
+constexpr int kVChunkBytes = 16384;  // V slice bytes per LDS chunk
+constexpr int kVLoads = kVChunkBytes / 16 / kNT;  // 16-byte loads per lane per chunk
+
 template <bool F16>
-struct KvSrc;
+struct Elem;
 template <>
-struct KvSrc<true> {
-  const uint16_t* k;
-  const uint16_t* v;
-  __device__ float kval(size_t i) const { return f16_to_f32(k[i]); }
-  __device__ float vval(size_t i) const { return f16_to_f32(v[i]); }
+struct Elem<true> {
+  using T = uint16_t;
+  static __device__ float get(T v) { return f16_to_f32(v); }
 };
 template <>
-struct KvSrc<false> {
-  const float* k;
-  const float* v;
-  __device__ float kval(size_t i) const { return k[i]; }
-  __device__ float vval(size_t i) const { return v[i]; }
+struct Elem<false> {
+  using T = float;
+  static __device__ float get(T v) { return v; }
 };
 
 // Dot of q (LDS) with one K row, folded left to right from -0.0. HD > 0: the
 // head width is a compile-time constant, the row start is 16-byte aligned and
-// the row is fetched with 16-byte loads (f16: whole row in flight, HD/2 VGPRs;
-// f32: 32-wide chunks) before the chain; HD == 0: runtime width.
+// the row is fetched with 16-byte loads before the chain; HD == 0: runtime
+// width, scalar loads.
 template <int HD, bool F16>
-__device__ __forceinline__ float row_dot(const float* s_q, KvSrc<F16> kv, size_t base, int hd) {
+__device__ __forceinline__ float row_dot(const float* s_q, const typename Elem<F16>::T* krow, int hd) {
   float dot = -0.0f;
   if constexpr (HD > 0 && F16) {
     static_assert(HD % 8 == 0, "f16 rows load 8 halves at a time");
     uint4 raw[HD / 8];
-    const uint4* p = reinterpret_cast<const uint4*>(kv.k + base);
+    const uint4* p = reinterpret_cast<const uint4*>(krow);
 #pragma unroll
     for (int i = 0; i < HD / 8; i++) raw[i] = p[i];
 #pragma unroll
@@ -55,7 +61,7 @@ __device__ __forceinline__ float row_dot(const float* s_q, KvSrc<F16> kv, size_t
     }
   } else if constexpr (HD > 0) {
     static_assert(HD % 16 == 0, "f32 rows load in chunks of 16");
-    const float4* p = reinterpret_cast<const float4*>(kv.k + base);
+    const float4* p = reinterpret_cast<const float4*>(krow);
 #pragma unroll
     for (int c = 0; c < HD / 16; c++) {
       float4 raw[4];
@@ -71,107 +77,240 @@ __device__ __forceinline__ float row_dot(const float* s_q, KvSrc<F16> kv, size_t
       }
     }
   } else {
-    for (int d = 0; d < hd; d++) dot += s_q[d] * kv.kval(base + d);
+    for (int d = 0; d < hd; d++) dot += s_q[d] * Elem<F16>::get(krow[d]);
   }
   return dot;
 }
 
-// q_row: this query row (n_heads*hd); pos: its absolute position; scores:
-// scratch of pos+1 floats owned by this workgroup.
+struct HeadJob {
+  const float* q_row;  // this query row (n_heads*hd)
+  const void* k;       // K rows (kv_stride elements apart)
+  const void* v;
+  int pos;  // absolute position: attends to rows 0..=pos
+  int h, kvh, kv_stride, hd;
+  int d0, dw;        // dims folded by this workgroup
+  float* dst;        // output row (n_heads*hd)
+  float* gscores;    // global scratch of >= pos+1 floats (used beyond kScoreLds)
+  bool vec;          // 16-byte aligned rows: V streams through LDS chunks
+};
+
+struct Lds {
+  float* q;       // hd floats
+  float* red;     // kNT/64 floats
+  float* scores;  // kScoreLds floats
+  uint4* v;       // kVChunkBytes
+};
+
+// V chunk: rows [t0, t0+nr) of dims [d0, d0+dw), packed row-major in LDS.
+// Lane i fetches 16-byte piece p = i + kNT*j of the chunk; pieces past the
+// chunk re-read its first row (in bounds) and are not stored.
+struct VRegs {
+  uint4 r0, r1, r2, r3;
+};
+static_assert(kVLoads == 4, "VRegs holds four pieces per lane");
+
+template <bool F16>
+__device__ __forceinline__ VRegs fetch_v(const HeadJob& J, int t0, int nr) {
+  using T = typename Elem<F16>::T;
+  constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte piece
+  const int ppr = J.dw / EPV;          // pieces per row
+  const T* base = static_cast<const T*>(J.v) + (size_t)J.kvh * J.hd + J.d0 + (size_t)t0 * J.kv_stride;
+  auto piece = [&](int j) {
+    const int p = threadIdx.x + kNT * j;
+    int row = p / ppr, col = p % ppr;
+    if (row >= nr) row = 0;
+    return *reinterpret_cast<const uint4*>(base + (size_t)row * J.kv_stride + col * EPV);
+  };
+  VRegs r;
+  r.r0 = piece(0);
+  r.r1 = piece(1);
+  r.r2 = piece(2);
+  r.r3 = piece(3);
+  return r;
+}
+
+template <bool F16>
+__device__ __forceinline__ void store_v(uint4* s_v, int nr, int dw, const VRegs& r) {
+  using T = typename Elem<F16>::T;
+  const int lim = nr * (dw / (16 / static_cast<int>(sizeof(T))));  // pieces in the chunk
+  const int p = threadIdx.x;
+  if (p < lim) s_v[p] = r.r0;
+  if (p + kNT < lim) s_v[p + kNT] = r.r1;
+  if (p + 2 * kNT < lim) s_v[p + 2 * kNT] = r.r2;
+  if (p + 3 * kNT < lim) s_v[p + 3 * kNT] = r.r3;
+}
+
+// Scores of rows 0..n into sc; returns the workgroup-wide max (every lane).
 template <int HD, bool F16>
-__device__ void one_head(const float* __restrict__ q_row, KvSrc<F16> kv, int pos, int h, int group, int kv_stride,
-                         int hd, float* __restrict__ dst, float* __restrict__ scores) {
-  __shared__ float s_q[256];
-  __shared__ float s_red[4];
-  const int kvh = h / group;
+__device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, float* sc) {
+  using T = typename Elem<F16>::T;
+  const int tid = threadIdx.x;
+  const int n = J.pos + 1;
+  const int hd = HD > 0 ? HD : J.hd;
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) s_q[d] = q_row[h * hd + d];
-  __syncthreads();
+  const T* kb = static_cast<const T*>(J.k) + (size_t)J.kvh * hd;
   float mx = -INFINITY;
-  for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
-    float sc = row_dot<HD, F16>(s_q, kv, (size_t)t * kv_stride + (size_t)kvh * hd, hd) * scale;
-    scores[t] = sc;
-    mx = fmaxf(mx, sc);
+  for (int t = tid; t < n; t += kNT) {
+    float s = row_dot<HD, F16>(L.q, kb + (size_t)t * J.kv_stride, hd) * scale;
+    sc[t] = s;
+    mx = fmaxf(mx, s);
+  }
+  return mx;
+}
+
+template <bool F16>
+__device__ __forceinline__ void one_head(const HeadJob& J, int vec_hd, const Lds& L) {
+  using T = typename Elem<F16>::T;
+  const int tid = threadIdx.x;
+  const int n = J.pos + 1;
+  float* sc = n <= kScoreLds ? L.scores : J.gscores;
+  for (int d = tid; d < J.hd; d += kNT) L.q[d] = J.q_row[J.h * J.hd + d];
+  __syncthreads();
+  float mx;
+  switch (vec_hd) {
+    case 48: mx = head_scores<48, F16>(J, L, sc); break;
+    case 64: mx = head_scores<64, F16>(J, L, sc); break;
+    case 128: mx = head_scores<128, F16>(J, L, sc); break;
+    default: mx = head_scores<0, F16>(J, L, sc); break;
   }
   mx = wave_max_f32(mx);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+  if ((tid & 63) == 0) L.red[tid >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  for (int t = threadIdx.x; t <= pos; t += blockDim.x) scores[t] = dev_expf(scores[t] - mx);
+#pragma unroll
+  for (int w = 0; w < kNT / 64; w++) mx = fmaxf(mx, L.red[w]);
+  for (int t = tid; t < n; t += kNT) sc[t] = dev_expf(sc[t] - mx);
+  const bool in_lds = n <= kScoreLds;
+  if (in_lds)  // zero fill for the single-lane fold
+    for (int t = n + tid; t < exact::lane_pad(n); t += kNT) sc[t] = 0.0f;
   __syncthreads();
   // softmax sum in the reference's left-to-right order (norms.rs:53)
-  const float sum = exact::block_seq_sum_nonneg(scores, pos + 1);
+  const float sum = in_lds ? exact::block_seq_sum_nonneg<kNT, true>(sc, n)
+                           : exact::block_seq_sum_nonneg<kNT, false>(sc, n);
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  for (int t = threadIdx.x; t <= pos; t += blockDim.x) scores[t] = scores[t] * inv;
+  for (int t = tid; t < n; t += kNT) sc[t] = sc[t] * inv;
   __syncthreads();
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.0f;
-    const size_t base = (size_t)kvh * hd + d;
-    int t = 0;
-    for (; t + 8 <= pos + 1; t += 8) {  // 8 loads in flight ahead of the chain
-      float v[8], p[8];
+
+  // ---- PV over dims [d0, d0+dw): lane d folds dim d0 + d
+  const int d = tid;
+  const bool folder = d < J.dw;
+  float acc = 0.0f;
+  if (J.vec) {
+    const int rows_per_chunk = kVChunkBytes / (J.dw * static_cast<int>(sizeof(T)));
+    const T* s_vt = reinterpret_cast<const T*>(L.v);
+    int t0 = 0;
+    VRegs r = fetch_v<F16>(J, t0, min(rows_per_chunk, n - t0));
+    while (t0 < n) {
+      const int nr = min(rows_per_chunk, n - t0);
+      store_v<F16>(L.v, nr, J.dw, r);
+      __syncthreads();
+      const int t1 = t0 + nr;
+      if (t1 < n) r = fetch_v<F16>(J, t1, min(rows_per_chunk, n - t1));  // in flight during the fold
+      if (folder) {
+        int i = 0;
+        for (; i + 8 <= nr; i += 8) {
+          float vv[8], pp[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        v[j] = kv.vval(base + (size_t)(t + j) * kv_stride);
-        p[j] = scores[t + j];
+          for (int j = 0; j < 8; j++) {
+            vv[j] = Elem<F16>::get(s_vt[(i + j) * J.dw + d]);
+            pp[j] = sc[t0 + i + j];
+          }
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc += pp[j] * vv[j];
+        }
+        for (; i < nr; i++) acc += sc[t0 + i] * Elem<F16>::get(s_vt[i * J.dw + d]);
       }
-#pragma unroll
-      for (int j = 0; j < 8; j++) acc += p[j] * v[j];
+      __syncthreads();
+      t0 = t1;
     }
-    for (; t <= pos; t++) acc += scores[t] * kv.vval(base + (size_t)t * kv_stride);
-    dst[h * hd + d] = acc;
+  } else if (folder) {
+    const T* vb = static_cast<const T*>(J.v) + (size_t)J.kvh * J.hd + J.d0 + d;
+    for (int t = 0; t < n; t++) acc += sc[t] * Elem<F16>::get(vb[(size_t)t * J.kv_stride]);
   }
+  if (folder) J.dst[J.h * J.hd + J.d0 + d] = acc;
 }
 
-// vec_hd: the compiled head width when K is 16-byte aligned at every row
-// start (checked on the host), else 0 for the generic path.
-template <bool F16, class KV>
-__device__ void one_head_dispatch(const float* q_row, KV kv, int pos, int h, int group, int kv_stride, int hd,
-                                  int vec_hd, float* dst, float* scores) {
-  switch (vec_hd) {
-    case 48: one_head<48, F16>(q_row, kv, pos, h, group, kv_stride, hd, dst, scores); break;
-    case 64: one_head<64, F16>(q_row, kv, pos, h, group, kv_stride, hd, dst, scores); break;
-    case 128: one_head<128, F16>(q_row, kv, pos, h, group, kv_stride, hd, dst, scores); break;
-    default: one_head<0, F16>(q_row, kv, pos, h, group, kv_stride, hd, dst, scores); break;
-  }
+// blockIdx.x -> (head, dim slice). When the count divides by the 8 XCDs,
+// consecutive logical blocks (the slices of one head, then the heads of one
+// KV group) land on one XCD, so they share its L2 for K and V.
+__device__ __forceinline__ int logical_block(int nb) {
+  const int b = blockIdx.x;
+  if (nb % 8 != 0) return b;
+  return (b % 8) * (nb / 8) + b / 8;
 }
 
-// Head widths with a compiled row loader, used when every K row start is
-// 16-byte aligned (base pointer aligned and hd a multiple of the vector).
-int pick_vec_hd(const void* k, size_t hd, size_t elem) {
-  if (reinterpret_cast<uintptr_t>(k) % 16 != 0) return 0;
-  if ((hd * elem) % 16 != 0 || (elem == 4 && hd % 16 != 0)) return 0;
-  return (hd == 48 || hd == 64 || hd == 128) ? static_cast<int>(hd) : 0;
-}
-
-// grid: (n_heads, n_q). Row i attends to cache rows 0..=pos0+i.
-__global__ __launch_bounds__(256) void attn_cache_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                         const uint16_t* __restrict__ vc, int pos0, int n_heads,
-                                                         int group, int hd, float* __restrict__ out,
-                                                         float* __restrict__ scratch, int ctx_cap,
-                                                         const int* __restrict__ pos_dev, int vec_hd) {
-  const int h = blockIdx.x, i = blockIdx.y;
+// grid: (n_heads*dsplit, n_q). Query row i sits at position p0 + i.
+// mode: 0 scalar rows; -1 vector V chunks with a runtime head width;
+// 48/64/128 vector K and V loads with that compiled head width.
+template <bool F16>
+__global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, const void* __restrict__ k,
+                                                   const void* __restrict__ v, int pos0,
+                                                   const int* __restrict__ pos_dev, int n_heads, int group, int hd,
+                                                   int dsplit, float* __restrict__ out, float* __restrict__ scratch,
+                                                   int scratch_stride, int mode) {
+  __shared__ float s_q[256];
+  __shared__ float s_red[kNT / 64];
+  __shared__ __align__(16) float s_scores[exact::lane_pad(kScoreLds)];
+  __shared__ uint4 s_v[kVChunkBytes / 16];
+  const int lb = logical_block(n_heads * dsplit);
+  const int h = lb / dsplit, ds = lb % dsplit, i = blockIdx.y;
   const int p0 = pos_dev ? *pos_dev : pos0;
-  const int q_stride = n_heads * hd;
-  const int kv_stride = (n_heads / group) * hd;
-  KvSrc<true> kv{kc, vc};
-  one_head_dispatch<true>(q + (size_t)i * q_stride, kv, p0 + i, h, group, kv_stride, hd, vec_hd,
-                          out + (size_t)i * q_stride, scratch + ((size_t)i * n_heads + h) * ctx_cap);
+  HeadJob J;
+  J.q_row = q + (size_t)i * n_heads * hd;
+  J.k = k;
+  J.v = v;
+  J.pos = p0 + i;
+  J.h = h;
+  J.kvh = h / group;
+  J.kv_stride = (n_heads / group) * hd;
+  J.hd = hd;
+  J.dw = hd / dsplit;
+  J.d0 = ds * J.dw;
+  J.dst = out + (size_t)i * n_heads * hd;
+  J.gscores = scratch ? scratch + ((size_t)i * n_heads * dsplit + lb) * scratch_stride : nullptr;
+  J.vec = mode != 0;
+  Lds L{s_q, s_red, s_scores, s_v};
+  one_head<F16>(J, mode, L);
 }
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                           const float* __restrict__ v, int seq, int n_heads,
-                                                           int group, int hd, float* __restrict__ out,
-                                                           float* __restrict__ scratch, int vec_hd) {
-  const int h = blockIdx.x, i = blockIdx.y;
-  const int q_stride = n_heads * hd;
-  const int kv_stride = (n_heads / group) * hd;
-  KvSrc<false> kv{k, v};
-  one_head_dispatch<false>(q + (size_t)i * q_stride, kv, i, h, group, kv_stride, hd, vec_hd, out + (size_t)i * q_stride,
-                           scratch + ((size_t)i * n_heads + h) * seq);
+template <bool F16>
+int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const int* pos_dev, size_t n_q,
+                size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
+                hipStream_t s) {
+  const size_t elem = F16 ? 2 : 4;
+  const bool aligned = reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                       (hd * elem) % 16 == 0;
+  int mode = 0;
+  if (aligned) {
+    const bool compiled = (hd == 48 || hd == 64 || hd == 128) && (F16 || hd % 16 == 0);
+    mode = compiled ? static_cast<int>(hd) : -1;
+  }
+  const int ds = attention_dim_slices(n_q, n_heads, hd, elem, aligned);
+  PRANA_CHECK(ctx_cap <= static_cast<size_t>(kScoreLds) || scratch != nullptr,
+              "attention: contexts beyond 4096 positions need score scratch");
+  hipLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, q, k, v, (int)pos0, pos_dev,
+                     (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
 }
 
 }  // namespace
+
+// Dim slices per head: enough workgroups to keep the V stream parallel when
+// there are few (query row, head) pairs; each slice stays a whole number of
+// 16-byte pieces wide.
+int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, bool aligned) {
+  if (!aligned) return 1;
+  int ds = 1;
+  while (n_q * n_heads * ds < 128 && ds < 4 && hd % (2 * ds) == 0 && (hd / (2 * ds)) * elem % 16 == 0) ds *= 2;
+  return ds;
+}
+
+size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap) {
+  if (ctx_cap <= static_cast<size_t>(kScoreLds)) return 0;
+  size_t ds = 1;  // upper bound of attention_dim_slices
+  while (n_q * n_heads * ds < 128 && ds < 4) ds *= 2;
+  return n_q * n_heads * ds * ctx_cap;
+}
 
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
@@ -181,11 +320,7 @@ int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* v
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
   if (ctx_cap == 0) ctx_cap = pos0 + n_q;
   PRANA_CHECK(pos_dev || pos0 + n_q <= ctx_cap, "attention: scratch capacity below pos0 + n_q");
-  hipLaunchKernelGGL(attn_cache_kernel, dim3(n_heads, n_q), dim3(256), 0, s, q, kc, vc, (int)pos0, (int)n_heads,
-                     (int)(n_heads / n_kv_heads), (int)hd, out, scratch, (int)ctx_cap, pos_dev,
-                     pick_vec_hd(kc, hd, 2));
-  PRANA_LAUNCH_CHECK();
-  return kOk;
+  return launch_attn<true>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, hd, out, scratch, ctx_cap, s);
 }
 
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
@@ -193,10 +328,7 @@ int launch_attention_prefill(const float* q, const float* k, const float* v, siz
   if (seq == 0) return kOk;
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "attention: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, seq), dim3(256), 0, s, q, k, v, (int)seq, (int)n_heads,
-                     (int)(n_heads / n_kv_heads), (int)hd, out, scratch, pick_vec_hd(k, hd, 4));
-  PRANA_LAUNCH_CHECK();
-  return kOk;
+  return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, s);
 }
 
 }  // namespace prana

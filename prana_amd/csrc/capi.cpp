@@ -308,10 +308,12 @@ int attn_entry(const float* q, const uint16_t* kc, const uint16_t* vc, size_t po
   Scratch& sc = scratch();
   std::lock_guard<std::mutex> lk(sc.mu);
   size_t cap = pos0 + seq;
-  int rc = sc.att.ensure(seq * nh * cap * 4);
+  const size_t need = attention_scratch_floats(seq, nh, cap);
+  int rc = sc.att.ensure(need * 4);
   if (rc) return rc;
   hipStream_t s = pick_stream(stream);
-  rc = launch_attention_cache(q, kc, vc, pos0, seq, nh, nkv, hd, out, sc.att.as<float>(), cap, nullptr, s);
+  rc = launch_attention_cache(q, kc, vc, pos0, seq, nh, nkv, hd, out, need ? sc.att.as<float>() : nullptr, cap,
+                              nullptr, s);
   if (rc) return rc;
   PRANA_HIP(hipStreamSynchronize(s));
   return static_cast<int>(kOk);
@@ -336,10 +338,12 @@ int prana_attention_prefill(const float* q, const float* k, const float* v, size
     INIT_OR_RETURN();
     Scratch& sc = scratch();
     std::lock_guard<std::mutex> lk(sc.mu);
-    int rc = sc.att.ensure(n_heads * seq * seq * 4);
+    const size_t need = attention_scratch_floats(seq, n_heads, seq);
+    int rc = sc.att.ensure(need * 4);
     if (rc) return rc;
     hipStream_t s = pick_stream(stream);
-    rc = launch_attention_prefill(q, k, v, seq, n_heads, n_kv_heads, head_dim, out, sc.att.as<float>(), s);
+    rc = launch_attention_prefill(q, k, v, seq, n_heads, n_kv_heads, head_dim, out,
+                                  need ? sc.att.as<float>() : nullptr, s);
     if (rc) return rc;
     PRANA_HIP(hipStreamSynchronize(s));
     return static_cast<int>(kOk);

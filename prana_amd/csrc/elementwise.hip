@@ -1,9 +1,9 @@
 // Elementwise, normalisation, RoPE, KV-cache, embedding and argmax kernels.
 //
 // Every reduction that the reference performs as a sequential f32 fold
-// (rmsnorm's sum of squares, softmax's sum) is performed here in exactly that
-// order by a single lane; order-free parts (max, integer sums, elementwise
-// products) run in parallel.
+// (rmsnorm's sum of squares, softmax's sum) gives exactly that fold's result
+// (exact_sum.h); order-free parts (max, integer sums, elementwise products)
+// run in parallel.
 #include "common.h"
 #include "exact_sum.h"
 #include "kernels.h"
@@ -43,27 +43,31 @@ int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, flo
 
 // ---------------------------------------------------------------- rmsnorm
 // norms.rs:9-23: ms = (sum_seq x*x)/dim; inv = 1/sqrt(ms+eps); y = (x*inv)*w.
-// One workgroup per row. The sum is the reference's left-to-right fold from
-// -0.0 (single lane); the normalise + optional quantize is parallel.
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                      int dim, float eps, float* __restrict__ out,
-                                                      int8_t* __restrict__ q, float* __restrict__ sa,
-                                                      int* __restrict__ sums) {
-  extern __shared__ float sq[];  // dim squares
+// One 1024-lane workgroup per row. The sum of squares is the reference's
+// left-to-right fold from -0.0, evaluated exactly by the whole workgroup; the
+// normalise + optional quantize is parallel.
+constexpr int kNormNT = 1024;
+__global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          int dim, float eps, float* __restrict__ out,
+                                                          int8_t* __restrict__ q, float* __restrict__ sa,
+                                                          int* __restrict__ sums) {
+  extern __shared__ float4 sq4[];  // dim squares, zero-filled up to lane_pad(dim)
+  float* sq = reinterpret_cast<float*>(sq4);
   const float* row = x + (size_t)blockIdx.x * dim;
-  for (int i = threadIdx.x; i < dim; i += 256) {
-    float v = row[i];
+  const int padded = exact::lane_pad(dim);
+  for (int i = threadIdx.x; i < padded; i += kNormNT) {
+    float v = i < dim ? row[i] : 0.0f;
     sq[i] = v * v;
   }
   __syncthreads();
   // sum of squares in the reference's left-to-right order (norms.rs:15)
-  const float ss = exact::block_seq_sum_nonneg(sq, dim);
+  const float ss = exact::block_seq_sum_nonneg<kNormNT, true>(sq, dim);
   const float mean_sq = ss / static_cast<float>(dim);
   const float inv = 1.0f / sqrtf(mean_sq + eps);
   // dim is a multiple of 32 whenever q != nullptr; round the loop up to a
   // whole number of 32-lane groups so every group reduces together.
-  int span = q ? ((dim + 255) / 256) * 256 : dim;
-  for (int i = threadIdx.x; i < span; i += 256) {
+  int span = q ? ((dim + kNormNT - 1) / kNormNT) * kNormNT : dim;
+  for (int i = threadIdx.x; i < span; i += kNormNT) {
     bool live = i < dim;
     float y = live ? row[i] * inv * w[i] : 0.0f;
     if (live && out) out[(size_t)blockIdx.x * dim + i] = y;
@@ -87,8 +91,9 @@ int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, floa
                    float* sa, int* sums, hipStream_t s) {
   if (rows == 0) return kOk;
   PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
-  PRANA_CHECK(dim * 4 <= 64 * 1024, "rmsnorm: dim above 16384");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), dim * 4, s, x, w, (int)dim, eps, out, q, sa, sums);
+  PRANA_CHECK(dim >= 1 && dim <= 16320, "rmsnorm: dim must be in 1..=16320");
+  const size_t lds = static_cast<size_t>(exact::lane_pad(static_cast<int>(dim))) * 4;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormNT), lds, s, x, w, (int)dim, eps, out, q, sa, sums);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -134,10 +139,10 @@ int launch_act_mul(float* g, const float* u, size_t n, int gelu, int8_t* q, floa
 }
 
 // ---------------------------------------------------------------- softmax
-// norms.rs:44-56, one workgroup per row; the sum is a single-lane fold.
+// norms.rs:44-56, one workgroup per row; the sum is the sequential fold,
+// evaluated exactly by the workgroup.
 __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ in, int n, float* __restrict__ out) {
   __shared__ float s_red[4];
-  __shared__ float s_inv;
   const float* row = in + (size_t)blockIdx.x * n;
   float* dst = out + (size_t)blockIdx.x * n;
   float mx = -INFINITY;
@@ -148,9 +153,8 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   for (int i = threadIdx.x; i < n; i += 256) dst[i] = dev_expf(row[i] - mx);
   __syncthreads();
-  const float sum = exact::block_seq_sum_nonneg(dst, n);  // norms.rs:53 order
+  const float sum = exact::block_seq_sum_nonneg<256, false>(dst, n);  // norms.rs:53 order
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  (void)s_inv;
   for (int i = threadIdx.x; i < n; i += 256) dst[i] = dst[i] * inv;
 }
 

@@ -80,13 +80,18 @@ size_t terms_per_row(const DevMat& m);
 // ---- attention.hip
 // attention_decode / attention_verify (attention.rs:129-160, 296-333) over the
 // f16 cache: n_q query rows at positions pos0 + i (pos0 read from pos_dev when
-// non-null). scratch >= n_q*n_heads*ctx_cap floats, ctx_cap >= pos0+n_q
-// (0 = exactly pos0+n_q).
+// non-null). scratch >= attention_scratch_floats(n_q, n_heads, ctx_cap)
+// floats (none up to 4096 positions), ctx_cap >= pos0+n_q (0 = exactly
+// pos0+n_q).
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
                            const int* pos_dev, hipStream_t s);
 // attention (prefill, attention.rs:236-284) over f32 K/V of the window.
-// scratch >= n_heads*seq*seq floats.
+// scratch >= attention_scratch_floats(seq, n_heads, seq) floats.
+// Score scratch a launch needs (probabilities beyond 4096 positions spill
+// from LDS to it), and the dim slices per head a launch uses.
+size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap);
+int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, bool aligned);
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
                              size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s);
 

@@ -132,6 +132,39 @@ def test_rmsnorm(rows, dim):
     assert same_bits(P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5))
 
 
+def _adversarial_rows(dim, seed):
+    """Rows whose squares stress the exact sequential sum: ties against the
+    running sum, powers of two, subnormal squares, zeros, overflow to inf,
+    a wide dynamic range and non-finite inputs."""
+    r = rng(seed)
+    rows = [
+        np.ldexp(1.0, -r.integers(0, 20, dim)).astype(np.float32),            # exact power-of-two squares
+        np.where(np.arange(dim) == 0, 1.0, 2.0 ** -12).astype(np.float32),      # half-ulp ties against 1.0
+        (np.exp2(r.uniform(-70, 30, dim)) * r.choice([-1, 1], dim)).astype(np.float32),  # wide range
+        (r.integers(1, 1 << 10, dim) * 2.0 ** -80).astype(np.float32),          # subnormal squares
+        np.where(r.random(dim) < 0.5, 0.0, r.standard_normal(dim)).astype(np.float32),
+        np.full(dim, 1e19, np.float32),                                         # sum overflows to inf
+        np.zeros(dim, np.float32),
+        r.standard_normal(dim).astype(np.float32) * 1e-3,
+    ]
+    bad = r.standard_normal(dim).astype(np.float32)
+    bad[dim // 2] = np.nan
+    rows.append(bad)
+    inf = r.standard_normal(dim).astype(np.float32)
+    inf[-1] = np.inf
+    rows.append(inf)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("dim", [32, 1000, 4096, 4128, 14336, 16320])
+def test_rmsnorm_adversarial(dim):
+    x = _adversarial_rows(dim, dim)
+    w = np.ones(dim, np.float32)
+    got, want = P.rmsnorm(x, w, 1e-6), O.rmsnorm(x, w, 1e-6)
+    for i in range(x.shape[0]):
+        assert same_bits(got[i], want[i]), i
+
+
 def test_silu_and_expf():
     x = np.concatenate([rng(1).standard_normal(100000).astype(np.float32) * 10,
                         np.array([0.0, -0.0, 88.0, -88.0, 100.0, -104.0, -110.0, np.inf, -np.inf], np.float32)])
@@ -181,6 +214,19 @@ def test_softmax(n):
         assert same_bits(got[r], O.softmax(x[r]))
 
 
+@pytest.mark.parametrize("n", [1, 33, 4096, 4097, 20000])
+def test_softmax_adversarial(n):
+    r = rng(n + 7)
+    rows = [
+        r.standard_normal(n).astype(np.float32) * 60,          # many exps underflow / subnormal
+        np.zeros(n, np.float32),                               # all equal: sum == n
+        np.log(np.arange(1, n + 1, dtype=np.float64)).astype(np.float32),
+        -np.ldexp(1.0, r.integers(-3, 6, n)).astype(np.float32),
+    ]
+    for x in rows:
+        assert same_bits(P.softmax(x[None, :])[0], O.softmax(x))
+
+
 # ------------------------------------------------------------------ RoPE / KV
 @pytest.mark.parametrize("neox", [0, 1])
 @pytest.mark.parametrize("hd,theta", [(48, 1e4), (64, 1e6), (128, 1e4)])
@@ -227,7 +273,8 @@ def _cache(n, nkv, hd, seed):
     return kc, vc
 
 
-@pytest.mark.parametrize("nh,nkv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 255), (14, 2, 64, 700), (32, 8, 128, 1030)])
+@pytest.mark.parametrize("nh,nkv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 255), (14, 2, 64, 700), (32, 8, 128, 1030),
+                                            (32, 8, 128, 5000), (4, 2, 80, 300), (4, 4, 36, 130), (2, 1, 256, 64)])
 def test_attention_decode(nh, nkv, hd, pos):
     kc, vc = _cache(pos + 1, nkv, hd, pos)
     q = rng(pos + 3).standard_normal(nh * hd).astype(np.float32)
@@ -242,7 +289,8 @@ def test_attention_verify():
                      O.attention_verify(q, kc, vc, pos0, seq, nh, nkv, hd))
 
 
-@pytest.mark.parametrize("seq,nh,nkv,hd", [(1, 2, 2, 16), (37, 14, 2, 64), (64, 6, 6, 48)])
+@pytest.mark.parametrize("seq,nh,nkv,hd", [(1, 2, 2, 16), (37, 14, 2, 64), (64, 6, 6, 48), (300, 4, 2, 128),
+                                            (4200, 2, 1, 16), (50, 3, 3, 20)])
 def test_attention_prefill(seq, nh, nkv, hd):
     r = rng(seq)
     q = r.standard_normal(seq * nh * hd).astype(np.float32)
