@@ -264,43 +264,47 @@ __global__ __launch_bounds__(256) void gemv_kernel(DevMat m, const int8_t* __res
 }
 
 // ===================================================================
-// Decode GEMV (v2): few tokens, weights streamed once, loads issued a stage
-// ahead, exact per-row fold in block order.
+// Decode GEMV: few tokens, every weight byte read once.
 //
-// A workgroup (256 lanes) owns RT rows of up to three matrices that share one
-// input (fused Q|K|V, gate|up). The K dimension is walked in stages: in each
-// stage every lane holds U storage units of weights in registers (loaded one
-// stage ahead), computes their f32 terms against the LDS-staged activations
-// and writes them to LDS; then one lane per (token, row) folds the stage's
-// terms in block order. The fold lanes carry their accumulators across
-// stages, so each output is exactly the reference's left-to-right sum.
+// A workgroup (256 lanes) owns a tile of rows of one matrix (for the fused
+// gate|up form, the same 32 rows of both) and walks the row blocks in stages
+// of SB units. In each stage every lane holds U storage units in registers
+// (the next stage's units are already in flight), computes their f32 terms
+// for each token against the LDS-staged activations and writes them to LDS;
+// one lane per (token, row) then folds the stage's terms in block order,
+// carrying its accumulator across stages, so each output is exactly the
+// reference's left-to-right sum. A lane's units sit at the same (row, block
+// offset) in every stage, so their addresses are fixed 32-bit unit indices
+// plus a per-stage step; partial tiles and stages clamp addresses instead of
+// branching and skip the writes.
 // ===================================================================
 
-// Raw storage units held in registers.
+// Raw storage units held in registers: load(quant bytes, scale bytes) of one
+// unit; terms() gives its kTpu f32 terms against the LDS activations.
 template <int KIND>
 struct RegUnit;
 
 template <>
 struct RegUnit<kKindQ4_0> {
-  static constexpr int kUnits = 8;  // units per lane per stage
+  static constexpr int kQB = 16, kSB = 2, kTpu = 1, kElems = 32;
   int4 q;
   uint32_t d;
-  __device__ void load(const DevMat& m, size_t r, int b) {
-    size_t G = m.cols / 32;
-    q = *reinterpret_cast<const int4*>(m.qs + (r * G + b) * 16);
-    d = reinterpret_cast<const uint16_t*>(m.sc)[r * G + b];
+  __device__ void load(const uint8_t* qp, const uint8_t* sp) {
+    q = *reinterpret_cast<const int4*>(qp);
+    d = *reinterpret_cast<const uint16_t*>(sp);
   }
   __device__ void terms(const Acts& a, int b, float* t) const {
-    const int* aw = a.w + b * 8;
+    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
+    const int4 a0 = aw[0], a1 = aw[1];
     int s = 0;
-    s = sdot4(q.x & kMask, aw[0], s);
-    s = sdot4(q.y & kMask, aw[1], s);
-    s = sdot4(q.z & kMask, aw[2], s);
-    s = sdot4(q.w & kMask, aw[3], s);
-    s = sdot4((q.x >> 4) & kMask, aw[4], s);
-    s = sdot4((q.y >> 4) & kMask, aw[5], s);
-    s = sdot4((q.z >> 4) & kMask, aw[6], s);
-    s = sdot4((q.w >> 4) & kMask, aw[7], s);
+    s = sdot4(q.x & kMask, a0.x, s);
+    s = sdot4(q.y & kMask, a0.y, s);
+    s = sdot4(q.z & kMask, a0.z, s);
+    s = sdot4(q.w & kMask, a0.w, s);
+    s = sdot4((q.x >> 4) & kMask, a1.x, s);
+    s = sdot4((q.y >> 4) & kMask, a1.y, s);
+    s = sdot4((q.z >> 4) & kMask, a1.z, s);
+    s = sdot4((q.w >> 4) & kMask, a1.w, s);
     s -= 8 * a.sm[b];
     t[0] = f16_to_f32(static_cast<uint16_t>(d)) * a.sa[b] * static_cast<float>(s);
   }
@@ -308,28 +312,27 @@ struct RegUnit<kKindQ4_0> {
 
 template <int KIND>
 struct RegUnitQ8 {
-  static constexpr int kUnits = 4;
+  static constexpr int kQB = 32, kSB = KIND == kKindQ8F ? 4 : 2, kTpu = 1, kElems = 32;
   int4 q0, q1;
   uint32_t d;  // f16 bits or f32 bits
-  __device__ void load(const DevMat& m, size_t r, int b) {
-    size_t G = m.cols / 32;
-    const int4* p = reinterpret_cast<const int4*>(m.qs + r * m.cols + (size_t)b * 32);
+  __device__ void load(const uint8_t* qp, const uint8_t* sp) {
+    const int4* p = reinterpret_cast<const int4*>(qp);
     q0 = p[0];
     q1 = p[1];
-    d = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[r * G + b]
-                         : reinterpret_cast<const uint16_t*>(m.sc)[r * G + b];
+    d = KIND == kKindQ8F ? *reinterpret_cast<const uint32_t*>(sp) : *reinterpret_cast<const uint16_t*>(sp);
   }
   __device__ void terms(const Acts& a, int b, float* t) const {
-    const int* aw = a.w + b * 8;
+    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
+    const int4 a0 = aw[0], a1 = aw[1];
     int s = 0;
-    s = sdot4(q0.x, aw[0], s);
-    s = sdot4(q0.y, aw[1], s);
-    s = sdot4(q0.z, aw[2], s);
-    s = sdot4(q0.w, aw[3], s);
-    s = sdot4(q1.x, aw[4], s);
-    s = sdot4(q1.y, aw[5], s);
-    s = sdot4(q1.z, aw[6], s);
-    s = sdot4(q1.w, aw[7], s);
+    s = sdot4(q0.x, a0.x, s);
+    s = sdot4(q0.y, a0.y, s);
+    s = sdot4(q0.z, a0.z, s);
+    s = sdot4(q0.w, a0.w, s);
+    s = sdot4(q1.x, a1.x, s);
+    s = sdot4(q1.y, a1.y, s);
+    s = sdot4(q1.z, a1.z, s);
+    s = sdot4(q1.w, a1.w, s);
     float dv = KIND == kKindQ8F ? __uint_as_float(d) : f16_to_f32(static_cast<uint16_t>(d));
     t[0] = dv * a.sa[b] * static_cast<float>(s);
   }
@@ -341,11 +344,10 @@ struct RegUnit<kKindQ8F> : RegUnitQ8<kKindQ8F> {};
 
 template <>
 struct RegUnit<kKindQ4_K> {
-  static constexpr int kUnits = 1;
+  static constexpr int kQB = 144, kSB = 0, kTpu = 8, kElems = 256;
   int4 v[9];
-  __device__ void load(const DevMat& m, size_t r, int b) {
-    size_t nb = m.cols / 256;
-    const int4* p = reinterpret_cast<const int4*>(m.qs + (r * nb + b) * 144);
+  __device__ void load(const uint8_t* qp, const uint8_t*) {
+    const int4* p = reinterpret_cast<const int4*>(qp);
 #pragma unroll
     for (int i = 0; i < 9; i++) v[i] = p[i];
   }
@@ -368,15 +370,14 @@ struct RegUnit<kKindQ4_K> {
 
 template <>
 struct RegUnit<kKindQ6_K> {
-  static constexpr int kUnits = 1;
+  static constexpr int kQB = 208, kSB = 2, kTpu = 16, kElems = 256;
   int4 v[13];
   uint32_t d;
-  __device__ void load(const DevMat& m, size_t r, int b) {
-    size_t nb = m.cols / 256;
-    const int4* p = reinterpret_cast<const int4*>(m.qs + (r * nb + b) * 208);
+  __device__ void load(const uint8_t* qp, const uint8_t* sp) {
+    const int4* p = reinterpret_cast<const int4*>(qp);
 #pragma unroll
     for (int i = 0; i < 13; i++) v[i] = p[i];
-    d = reinterpret_cast<const uint16_t*>(m.sc)[r * nb + b];
+    d = *reinterpret_cast<const uint16_t*>(sp);
   }
   __device__ void terms(const Acts& a, int b, float* t) const {
     const uint8_t* blk = reinterpret_cast<const uint8_t*>(v);
@@ -402,9 +403,11 @@ struct DecodeJob {
   DevMat m[3];
   GemvOut o[3];
   int n_mats;
-  int tiles[3];  // row tiles per matrix (prefix-summed at launch)
-  // act mode: m[0] = gate, m[1] = up (equal shapes); each workgroup owns the
-  // same rt rows of both, and writes h = silu(g)*u (or gelu) quantized.
+  int tiles[3];  // row tiles per matrix
+  int rt;        // rows per matrix per tile
+  int sb;        // units per row per stage
+  // act mode: m[0] = gate, m[1] = up (equal shapes, rt = 32); each tile owns
+  // the same rows of both and writes h = silu(g)*u (or gelu) quantized.
   int act;       // 0 none, 1 silu*up, 2 gelu*up
   float* h;      // optional f32 h [n][rows]
   int8_t* hq;
@@ -412,149 +415,199 @@ struct DecodeJob {
   int* hsum;
 };
 
-constexpr int kDecRT = 16;    // rows per matrix per workgroup (act mode: 32)
-constexpr int kDecMaxTok = 4;
+constexpr int kDecMaxTok = 4;   // tokens per launch (LDS permitting)
+constexpr int kActRows = 32;    // act-mode rows per matrix: one quantization block
 
-// LDS layout: acts [n][K bytes + 8*G] | terms [n][ROWS][S*TPU + 1].
-// Lane mapping per stage: unit u of lane t covers (slot = u*(256/S) + t/S,
-// unit t%S of the stage), so a wave reads contiguous runs of one row.
-template <int KIND, bool ACT>
-__global__ __launch_bounds__(256) void gemv_decode_kernel(DecodeJob job, const int8_t* __restrict__ q,
-                                                          const float* __restrict__ sa,
-                                                          const int* __restrict__ sums, int n_tok) {
-  extern __shared__ int smem[];
+// LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
+// STAGED: more than one stage (double-buffered registers and terms);
+// otherwise the whole row tile is one stage. NT lanes per workgroup.
+template <int KIND, int U, bool ACT, bool STAGED, int NT>
+__global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ sa,
+                                                        const int* __restrict__ sums, int n_tok) {
+  extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
-  using F = Fmt<KIND>;
-  constexpr int U = R::kUnits;
-  constexpr int UNIT = F::kUnit, TPU = F::kTpu;
-  constexpr int RT = ACT ? 32 : kDecRT;      // rows per matrix
-  constexpr int ROWS = ACT ? 2 * RT : RT;    // rows held by the workgroup
-  constexpr int S = 256 * U / ROWS;          // units per row per stage
-  constexpr int LPS = 256 / S;               // slots covered per unit index
-  constexpr int TS = S * TPU + 1;            // padded term row
-  static_assert(S * LPS == 256 && U * LPS == ROWS, "tile shape");
+  constexpr int TPU = R::kTpu;
   const int tid = threadIdx.x;
 
   int mi = 0, tile = blockIdx.x;
   if (!ACT) {
     while (mi < job.n_mats - 1 && tile >= job.tiles[mi]) tile -= job.tiles[mi++];
   }
+  const int rt = job.rt, SB = job.sb;
+  const int ROWS = ACT ? 2 * rt : rt;
   const int K = static_cast<int>(job.m[0].cols);
-  const int G = K / 32, W = K / 4;
-  const int upr = K / UNIT;
-  const int n_stages = (upr + S - 1) / S;
-  const size_t r0 = (size_t)tile * RT;
+  const int nb = K / R::kElems, G = K / 32;
+  const int n_stages = (nb + SB - 1) / SB;
+  const size_t rows_m = job.m[mi].rows;
+  const size_t r0 = (size_t)tile * rt;
+  const int rows_here = static_cast<int>(min((size_t)rt, rows_m - r0));
 
-  const int act_words = (K + 8 * G) / 4;
-  for (int t = 0; t < n_tok; t++) {
-    int* aw = smem + t * act_words;
-    float* as = reinterpret_cast<float*>(aw + W);
+  // ---- this lane's units: (matrix, row, block offset), fixed for all stages
+  const uint8_t* qbase[ACT ? 2 : 1];
+  const uint8_t* sbase[ACT ? 2 : 1];
+#pragma unroll
+  for (int j = 0; j < (ACT ? 2 : 1); j++) {
+    qbase[j] = job.m[ACT ? j : mi].qs;
+    sbase[j] = static_cast<const uint8_t*>(job.m[ACT ? j : mi].sc);
+  }
+  // upk[i] = row << 16 | block offset of unit i (row < 64 + 64, offset < 16384)
+  int upk[U];
+#pragma unroll
+  for (int i = 0; i < U; i++) {
+    const int v = tid + NT * i;
+    const int row = v / SB;
+    upk[i] = (row << 16) | (v - row * SB);
+  }
+  auto unit_row = [&](int i) { return upk[i] >> 16; };
+  auto unit_off = [&](int i) { return upk[i] & 0xffff; };
+  auto unit_up = [&](int i) { return ACT && unit_row(i) >= rt; };
+  auto unit_lr = [&](int i) { return unit_up(i) ? unit_row(i) - rt : unit_row(i); };
+  auto load_stage = [&](R* buf, int s) {
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      const int blk = min(s * SB + unit_off(i), nb - 1);
+      const size_t rr = r0 + min(unit_lr(i), rows_here - 1);
+      const size_t ui = rr * nb + blk;
+      const int j = unit_up(i) ? 1 : 0;
+      buf[i].load(qbase[ACT ? j : 0] + ui * R::kQB, sbase[ACT ? j : 0] + ui * R::kSB);
+    }
+  };
+
+  // token 0's activations go into registers first (the oldest loads), then
+  // the weights; the rest of the tokens are staged after the weights.
+  const int astride = ((K + 8 * G) + 15) & ~15;
+  constexpr int kAw4 = (16384 / 16 + NT - 1) / NT;  // int4 words per lane, K <= 16384
+  constexpr int kAg = (512 + NT - 1) / NT;          // block scales per lane
+  int4 a0w[kAw4];
+  float a0s[kAg];
+  int a0m[kAg];
+  {
+    const int4* qw = reinterpret_cast<const int4*>(q);
+#pragma unroll
+    for (int i = 0; i < kAw4; i++) {
+      const int w = tid + NT * i;
+      a0w[i] = w < K / 16 ? qw[w] : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kAg; i++) {
+      const int g = tid + NT * i;
+      a0s[i] = g < G ? sa[g] : 0.0f;
+      a0m[i] = g < G ? sums[g] : 0;
+    }
+  }
+  R buf0[U];
+  R buf1[STAGED ? U : 1];
+  load_stage(buf0, 0);
+  if (STAGED && n_stages > 1) load_stage(buf1, 1);
+
+  uint8_t* sm8 = reinterpret_cast<uint8_t*>(smem4);
+  {
+    int4* aw = reinterpret_cast<int4*>(sm8);
+    float* as = reinterpret_cast<float*>(sm8 + K);
     int* am = reinterpret_cast<int*>(as + G);
-    const int* qw = reinterpret_cast<const int*>(q + (size_t)t * K);
-    for (int i = tid; i < W; i += 256) aw[i] = qw[i];
-    for (int i = tid; i < G; i += 256) {
+#pragma unroll
+    for (int i = 0; i < kAw4; i++) {
+      const int w = tid + NT * i;
+      if (w < K / 16) aw[w] = a0w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kAg; i++) {
+      const int g = tid + NT * i;
+      if (g < G) {
+        as[g] = a0s[i];
+        am[g] = a0m[i];
+      }
+    }
+  }
+  for (int t = 1; t < n_tok; t++) {
+    int4* aw = reinterpret_cast<int4*>(sm8 + t * astride);
+    float* as = reinterpret_cast<float*>(sm8 + t * astride + K);
+    int* am = reinterpret_cast<int*>(as + G);
+    const int4* qw = reinterpret_cast<const int4*>(q + (size_t)t * K);
+    for (int i = tid; i < K / 16; i += NT) aw[i] = qw[i];
+    for (int i = tid; i < G; i += NT) {
       as[i] = sa[(size_t)t * G + i];
       am[i] = sums[(size_t)t * G + i];
     }
   }
-  float* terms = reinterpret_cast<float*>(smem + n_tok * act_words);
+  const int TS = SB * TPU + 1;  // padded term row
+  float* terms = reinterpret_cast<float*>(sm8 + n_tok * astride);
+  const int buf_floats = n_tok * ROWS * TS;
+  __syncthreads();
 
-  const int bb = tid % S;       // unit within the stage (same for every u)
-  const int slot0 = tid / S;
-  // Per unit index: matrix and row (compile-time matrix choice in act mode).
-  bool live[U];
-  size_t rowi[U];
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    int slot = u * LPS + slot0;
-    int which = ACT ? slot / RT : mi;
-    int rr = ACT ? slot % RT : slot;
-    rowi[u] = r0 + rr;
-    live[u] = rowi[u] < job.m[which].rows;
-  }
-
-  R buf0[U], buf1[U];
-  __syncthreads();  // activations staged
-
-#define PRANA_LOAD_STAGE(BUF, STG)                                          \
-  do {                                                                     \
-    int b_ = (STG) * S + bb;                                               \
-    if (b_ < upr) {                                                        \
-      _Pragma("unroll") for (int u = 0; u < U; u++) {                      \
-        int which_ = ACT ? (u * LPS + slot0) / RT : mi;                    \
-        if (live[u]) BUF[u].load(job.m[which_], rowi[u], b_);              \
-      }                                                                    \
-    }                                                                      \
-  } while (0)
-
-  const int fl_tok = tid / ROWS, fl_slot = tid % ROWS;
-  const bool folder = tid < n_tok * ROWS;
+  const int fl_tok = tid / ROWS, fl_row = tid % ROWS;
+  const int fl_lr = ACT ? (fl_row >= rt ? fl_row - rt : fl_row) : fl_row;
+  const bool folder = tid < n_tok * ROWS && fl_lr < rows_here;
   float acc = 0.0f;
 
-  auto process = [&](const R* buf, int stg) {
-    const int b = stg * S + bb;
-    const int s_units = min(S, upr - stg * S);
-    if (b < upr) {
-      for (int t = 0; t < n_tok; t++) {
-        int* aw = smem + t * act_words;
-        float* as = reinterpret_cast<float*>(aw + W);
-        int* am = reinterpret_cast<int*>(as + G);
-        Acts a{aw, as, am};
-        float* tt = terms + t * ROWS * TS;
+  auto process = [&](const R* buf, int s) {
+    float* tb = terms + (s & 1) * buf_floats;
 #pragma unroll
-        for (int u = 0; u < U; u++)
-          if (live[u]) buf[u].terms(a, b, tt + (u * LPS + slot0) * TS + bb * TPU);
+    for (int i = 0; i < U; i++) {
+      const int blk = s * SB + unit_off(i);
+      if (blk < nb && unit_lr(i) < rows_here) {
+        for (int t = 0; t < n_tok; t++) {
+          const uint8_t* ab = sm8 + t * astride;
+          Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
+                 reinterpret_cast<const int*>(ab + K) + G};
+          buf[i].terms(a, blk, tb + (t * ROWS + unit_row(i)) * TS + unit_off(i) * TPU);
+        }
       }
     }
     __syncthreads();
     if (folder) {
-      const float* tr = terms + fl_tok * ROWS * TS + fl_slot * TS;
-      const int nt = s_units * TPU;
+      const float* tr = tb + (fl_tok * ROWS + fl_row) * TS;
+      const int cnt = min(SB, nb - s * SB) * TPU;
       int i = 0;
-      for (; i + 4 <= nt; i += 4) {
-        float t0 = tr[i], t1 = tr[i + 1], t2 = tr[i + 2], t3 = tr[i + 3];
-        acc += t0;
-        acc += t1;
-        acc += t2;
-        acc += t3;
+      for (; i + 8 <= cnt; i += 8) {
+        float x0 = tr[i], x1 = tr[i + 1], x2 = tr[i + 2], x3 = tr[i + 3];
+        float x4 = tr[i + 4], x5 = tr[i + 5], x6 = tr[i + 6], x7 = tr[i + 7];
+        acc += x0;
+        acc += x1;
+        acc += x2;
+        acc += x3;
+        acc += x4;
+        acc += x5;
+        acc += x6;
+        acc += x7;
       }
-      for (; i < nt; i++) acc += tr[i];
+      for (; i < cnt; i++) acc += tr[i];
     }
-    __syncthreads();
   };
 
-  PRANA_LOAD_STAGE(buf0, 0);
-  for (int stg = 0; stg < n_stages; stg += 2) {
-    if (stg + 1 < n_stages) PRANA_LOAD_STAGE(buf1, stg + 1);
-    process(buf0, stg);
-    if (stg + 1 >= n_stages) break;
-    if (stg + 2 < n_stages) PRANA_LOAD_STAGE(buf0, stg + 2);
-    process(buf1, stg + 1);
+  if (!STAGED) {
+    process(buf0, 0);
+  } else {
+    for (int s = 0; s < n_stages; s += 2) {
+      process(buf0, s);
+      if (s + 1 >= n_stages) break;
+      if (s + 2 < n_stages) load_stage(buf0, s + 2);
+      process(buf1, s + 1);
+      if (s + 3 < n_stages) load_stage(buf1, s + 3);
+    }
   }
-#undef PRANA_LOAD_STAGE
 
   if (!ACT) {
-    if (folder) {
-      size_t r = r0 + fl_slot;
-      if (r < job.m[mi].rows) store_out(job.o[mi], fl_tok, r, acc);
-    }
+    if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
     return;
   }
-  // act epilogue: gate lanes (slot < RT) pair with up lanes (slot + RT);
-  // h = act(g) * u, then quantize each 32-row block (one 32-lane group).
+  // act epilogue: gate lanes (row < 32) pair with up lanes (row + 32);
+  // h = act(g) * u, then quantize the 32-row block (one 32-lane group).
+  __syncthreads();  // every fold read of the term buffers is done
   float* hx = terms;
-  if (folder) hx[fl_tok * ROWS + fl_slot] = acc;
+  if (tid < n_tok * ROWS) hx[tid] = acc;
   __syncthreads();
-  const size_t H = job.m[0].rows;
+  const size_t H = rows_m;
   if (tid < n_tok * ROWS) {
-    const bool gate_lane = fl_slot < RT;
-    size_t r = r0 + fl_slot;
-    bool lv = gate_lane && r < H;
+    const bool gate_lane = fl_row < rt;
+    const size_t r = r0 + fl_row;
+    const bool lv = gate_lane && fl_row < rows_here;
     float v = 0.0f;
     if (gate_lane) {
-      float g = acc, u = hx[fl_tok * ROWS + RT + fl_slot];
+      float g = acc, u = hx[fl_tok * ROWS + rt + fl_row];
       if (job.act == 2) {
-        const float kS = 0.7978846f;
+        const float kS = 0.7978846f;  // norms.rs:36
         float x3 = g * g * g;
         g = 0.5f * g * (1.0f + tanhf(kS * (g + 0.044715f * x3)));
       } else {
@@ -577,52 +630,113 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(DecodeJob job, const i
   }
 }
 
+// Tile geometry: units per lane per stage U, rows per matrix per tile rt,
+// units per row per stage sb and lanes nt, with rows(tile) * sb == nt * U.
+struct TileGeom {
+  int u, rt, sb, nt;
+};
+
 template <int KIND>
-int launch_decode_t(DecodeJob job, const int8_t* q, const float* sa, const int* sums, size_t n_tok, hipStream_t s) {
+TileGeom choose_geom(size_t K, bool act) {
   using R = RegUnit<KIND>;
-  using F = Fmt<KIND>;
-  const bool act = job.act != 0;
-  const int rt = act ? 32 : kDecRT;
-  const int rows_wg = act ? 2 * rt : rt;
-  const size_t K = job.m[0].cols;
-  const int S = 256 * R::kUnits / rows_wg;
-  const size_t act_bytes = K + 8 * (K / 32);
-  const size_t term_bytes = (size_t)rows_wg * (S * F::kTpu + 1) * 4;
-  int total = 0;
-  if (act) {
-    total = static_cast<int>((job.m[0].rows + rt - 1) / rt);
-  } else {
-    for (int i = 0; i < job.n_mats; i++) {
-      job.tiles[i] = static_cast<int>((job.m[i].rows + rt - 1) / rt);
-      total += job.tiles[i];
-    }
+  const int nb = static_cast<int>(K / R::kElems);
+  const bool small_unit = R::kElems == 32;
+  if (act) {  // 32 rows of gate and of up: 64 rows x sb units = nt * u
+    if (small_unit && nb * 64 == 512 * 16) return TileGeom{16, kActRows, nb, 512};  // one stage
+    if (small_unit) return TileGeom{8, kActRows, 32, 256};
+    return TileGeom{1, kActRows, 4, 256};
   }
-  const size_t per_tok = act_bytes + term_bytes;
-  const size_t group = std::min<size_t>(kDecMaxTok, (64 * 1024) / per_tok);
+  const int cand_small[] = {2, 4, 1, 7, 8};
+  const int cand_k[] = {1, 2};
+  const int* cand = small_unit ? cand_small : cand_k;
+  const int nc = small_unit ? 5 : 2;
+  for (int c = 0; c < nc; c++) {  // one stage: whole rows per tile
+    const int u = cand[c];
+    if ((256 * u) % nb == 0 && 256 * u / nb <= 64) return TileGeom{u, 256 * u / nb, nb, 256};
+  }
+  if (small_unit) return TileGeom{2, 8, 64, 256};
+  return TileGeom{1, 32, 8, 256};
+}
+
+template <int KIND, int U, bool ACT, bool STAGED, int NT>
+int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, const float* sa, const int* sums,
+                  size_t n_tok, hipStream_t s) {
+  using R = RegUnit<KIND>;
+  DecodeJob job = job0;
+  job.rt = g.rt;
+  job.sb = g.sb;
+  const size_t K = job.m[0].cols;
+  const int nb = static_cast<int>(K / R::kElems);
+  const int rows_wg = ACT ? 2 * g.rt : g.rt;
+  const int n_stages = (nb + g.sb - 1) / g.sb;
+  PRANA_CHECK(STAGED || n_stages == 1, "gemv: single-stage tile with several stages");
+  const size_t astride = ((K + 8 * (K / 32)) + 15) & ~static_cast<size_t>(15);
+  const size_t term_bytes = (size_t)(n_stages > 1 ? 2 : 1) * rows_wg * (g.sb * R::kTpu + 1) * 4;
+  int total = 0;
+  for (int i = 0; i < (ACT ? 1 : job.n_mats); i++) {
+    job.tiles[i] = static_cast<int>((job.m[i].rows + g.rt - 1) / g.rt);
+    total += job.tiles[i];
+  }
+  const size_t per_tok = astride + term_bytes;
+  size_t group = std::min<size_t>(kDecMaxTok, (64 * 1024) / per_tok);
+  if (ACT) group = std::min<size_t>(group, NT / rows_wg);
+  PRANA_CHECK(K <= 16384, "gemv: decode kernel supports cols <= 16384");
+  PRANA_CHECK(rows_wg * g.sb == NT * U, "gemv: tile geometry mismatch");
   PRANA_CHECK(group >= 1, "gemv: decode tile exceeds LDS");
   for (size_t t0 = 0; t0 < n_tok; t0 += group) {
-    size_t nt = std::min<size_t>(group, n_tok - t0);
-    size_t lds = nt * per_tok;
+    const size_t nt = std::min<size_t>(group, n_tok - t0);
     DecodeJob j = job;
     for (int i = 0; i < 3; i++)
       if (j.o[i].out) j.o[i].out += t0 * j.o[i].ldo;
-    if (act) {
-      size_t H = j.m[0].rows;
+    if (ACT) {
+      const size_t H = j.m[0].rows;
       if (j.h) j.h += t0 * H;
       j.hq += t0 * H;
       j.hsa += t0 * H / 32;
       j.hsum += t0 * H / 32;
     }
-    size_t G = K / 32;
-    if (act)
-      hipLaunchKernelGGL((gemv_decode_kernel<KIND, true>), dim3(total), dim3(256), lds, s, j, q + t0 * K,
-                         sa + t0 * G, sums + t0 * G, (int)nt);
-    else
-      hipLaunchKernelGGL((gemv_decode_kernel<KIND, false>), dim3(total), dim3(256), lds, s, j, q + t0 * K,
-                         sa + t0 * G, sums + t0 * G, (int)nt);
+    const size_t G = K / 32;
+    hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s, j, q + t0 * K,
+                       sa + t0 * G, sums + t0 * G, (int)nt);
     PRANA_LAUNCH_CHECK();
   }
   return kOk;
+}
+
+template <int KIND>
+int launch_decode_t(const DecodeJob& job, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                    hipStream_t s) {
+  constexpr bool kSmall = RegUnit<KIND>::kElems == 32;
+  const bool act = job.act != 0;
+  const TileGeom g = choose_geom<KIND>(job.m[0].cols, act);
+  const int nb = static_cast<int>(job.m[0].cols / RegUnit<KIND>::kElems);
+  const bool staged = g.sb < nb;
+  if (act) {
+    if constexpr (kSmall) {
+      if (g.nt == 512) return launch_tile_u<KIND, 16, true, false, 512>(job, g, q, sa, sums, n_tok, s);
+      if (!staged) return launch_tile_u<KIND, 8, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+      return launch_tile_u<KIND, 8, true, true, 256>(job, g, q, sa, sums, n_tok, s);
+    } else {
+      if (!staged) return launch_tile_u<KIND, 1, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+      return launch_tile_u<KIND, 1, true, true, 256>(job, g, q, sa, sums, n_tok, s);
+    }
+  }
+  if (staged) {
+    if constexpr (kSmall) return launch_tile_u<KIND, 2, false, true, 256>(job, g, q, sa, sums, n_tok, s);
+    else return launch_tile_u<KIND, 1, false, true, 256>(job, g, q, sa, sums, n_tok, s);
+  }
+  switch (g.u) {
+    case 1: return launch_tile_u<KIND, 1, false, false, 256>(job, g, q, sa, sums, n_tok, s);
+    case 2: return launch_tile_u<KIND, 2, false, false, 256>(job, g, q, sa, sums, n_tok, s);
+  }
+  if constexpr (kSmall) {
+    switch (g.u) {
+      case 4: return launch_tile_u<KIND, 4, false, false, 256>(job, g, q, sa, sums, n_tok, s);
+      case 7: return launch_tile_u<KIND, 7, false, false, 256>(job, g, q, sa, sums, n_tok, s);
+      case 8: return launch_tile_u<KIND, 8, false, false, 256>(job, g, q, sa, sums, n_tok, s);
+    }
+  }
+  return fail(kErrInvalid, "gemv: no tile geometry");
 }
 
 template <int KIND>
