@@ -21,15 +21,15 @@ namespace {
 
 constexpr int kNT = 256;             // lanes per workgroup
 constexpr int kScoreLds = 4096;      // probabilities kept in LDS up to this length
-constexpr int kVChunkBytes = 16384;  // V slice bytes per LDS chunk
-constexpr int kVLoads = kVChunkBytes / 16 / kNT;  // 16-byte loads per lane per chunk
+constexpr int kPieces = 2 * kNT;     // 16-byte V pieces per PV chunk (two per lane)
+constexpr int kProdFloats = 512 * 8 + 4 * 256;  // one product buffer: dw*(rows+4) <= this
 
 template <bool F16>
 struct Elem;
 template <>
 struct Elem<true> {
   using T = uint16_t;
-  static __device__ float get(T v) { return f16_to_f32(v); }
+  static __device__ float get(T v) { return f16_operand(v); }  // K/V only feed products
 };
 template <>
 struct Elem<false> {
@@ -55,8 +55,8 @@ __device__ __forceinline__ float row_dot(const float* s_q, const typename Elem<F
       const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        dot += s_q[8 * i + 2 * j] * f16_to_f32(static_cast<uint16_t>(w[j] & 0xffffu));
-        dot += s_q[8 * i + 2 * j + 1] * f16_to_f32(static_cast<uint16_t>(w[j] >> 16));
+        dot += s_q[8 * i + 2 * j] * f16_operand(static_cast<uint16_t>(w[j] & 0xffffu));
+        dot += s_q[8 * i + 2 * j + 1] * f16_operand(static_cast<uint16_t>(w[j] >> 16));
       }
     }
   } else if constexpr (HD > 0) {
@@ -97,47 +97,61 @@ struct HeadJob {
 struct Lds {
   float* q;       // hd floats
   float* red;     // kNT/64 floats
-  float* scores;  // kScoreLds floats
-  uint4* v;       // kVChunkBytes
+  float* scores;  // lane_pad(kScoreLds) floats
+  float* prod;    // 2 x kProdFloats: products p_t*v_t[d] of a PV chunk, [d][row]
 };
 
-// V chunk: rows [t0, t0+nr) of dims [d0, d0+dw), packed row-major in LDS.
-// Lane i fetches 16-byte piece p = i + kNT*j of the chunk; pieces past the
-// chunk re-read its first row (in bounds) and are not stored.
-struct VRegs {
-  uint4 r0, r1, r2, r3;
+// PV in chunks of `ch` rows: every lane turns up to two 16-byte V pieces (EPV
+// consecutive dims of one row) into products p_t * v_t[d] written to LDS as
+// [d][row]; then the fold lanes (one per dim) add their chunk's products in
+// row order. Products of the next chunk are written to the other buffer while
+// the current one is folded; V pieces are fetched one chunk ahead.
+struct VPieces {
+  uint4 a, b;
 };
-static_assert(kVLoads == 4, "VRegs holds four pieces per lane");
 
 template <bool F16>
-__device__ __forceinline__ VRegs fetch_v(const HeadJob& J, int t0, int nr) {
+__device__ __forceinline__ VPieces fetch_v(const HeadJob& J, int t0, int nr, int ppr) {
   using T = typename Elem<F16>::T;
-  constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte piece
-  const int ppr = J.dw / EPV;          // pieces per row
+  constexpr int EPV = 16 / sizeof(T);
   const T* base = static_cast<const T*>(J.v) + (size_t)J.kvh * J.hd + J.d0 + (size_t)t0 * J.kv_stride;
-  auto piece = [&](int j) {
-    const int p = threadIdx.x + kNT * j;
-    int row = p / ppr, col = p % ppr;
-    if (row >= nr) row = 0;
+  auto piece = [&](int p) {
+    int row = p / ppr, col = p - (p / ppr) * ppr;
+    if (row >= nr) row = 0;  // in bounds; not used
     return *reinterpret_cast<const uint4*>(base + (size_t)row * J.kv_stride + col * EPV);
   };
-  VRegs r;
-  r.r0 = piece(0);
-  r.r1 = piece(1);
-  r.r2 = piece(2);
-  r.r3 = piece(3);
-  return r;
+  return VPieces{piece(threadIdx.x), piece(threadIdx.x + kNT)};
 }
 
 template <bool F16>
-__device__ __forceinline__ void store_v(uint4* s_v, int nr, int dw, const VRegs& r) {
+__device__ __forceinline__ void make_products(const VPieces& v, const float* sc, int t0, int nr, int ppr, int ch,
+                                              float* prod) {
   using T = typename Elem<F16>::T;
-  const int lim = nr * (dw / (16 / static_cast<int>(sizeof(T))));  // pieces in the chunk
-  const int p = threadIdx.x;
-  if (p < lim) s_v[p] = r.r0;
-  if (p + kNT < lim) s_v[p + kNT] = r.r1;
-  if (p + 2 * kNT < lim) s_v[p + 2 * kNT] = r.r2;
-  if (p + 3 * kNT < lim) s_v[p + 3 * kNT] = r.r3;
+  constexpr int EPV = 16 / sizeof(T);
+  const int stride = ch + 4;
+  auto one = [&](const uint4& w, int p) {
+    const int row = p / ppr, col = p - (p / ppr) * ppr;
+    if (row >= nr) return;
+    const float pt = sc[t0 + row];
+    float x[EPV];
+    if constexpr (F16) {
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        x[2 * k] = f16_operand(static_cast<uint16_t>(u[k] & 0xffffu));
+        x[2 * k + 1] = f16_operand(static_cast<uint16_t>(u[k] >> 16));
+      }
+    } else {
+      x[0] = __uint_as_float(w.x);
+      x[1] = __uint_as_float(w.y);
+      x[2] = __uint_as_float(w.z);
+      x[3] = __uint_as_float(w.w);
+    }
+#pragma unroll
+    for (int k = 0; k < EPV; k++) prod[(col * EPV + k) * stride + row] = pt * x[k];
+  };
+  one(v.a, threadIdx.x);
+  one(v.b, threadIdx.x + kNT);
 }
 
 // Scores of rows 0..n into sc; returns the workgroup-wide max (every lane).
@@ -158,12 +172,14 @@ __device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, flo
   return mx;
 }
 
-template <bool F16>
-__device__ __forceinline__ void one_head(const HeadJob& J, int vec_hd, const Lds& L) {
+// SC_LDS: the probabilities live in LDS (sc is the LDS array), else in the
+// global scratch; the two bodies are separate so every access to sc compiles
+// to one address space.
+template <bool F16, bool SC_LDS>
+__device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, const Lds& L, float* __restrict__ sc) {
   using T = typename Elem<F16>::T;
   const int tid = threadIdx.x;
   const int n = J.pos + 1;
-  float* sc = n <= kScoreLds ? L.scores : J.gscores;
   for (int d = tid; d < J.hd; d += kNT) L.q[d] = J.q_row[J.h * J.hd + d];
   __syncthreads();
   float mx;
@@ -179,13 +195,11 @@ __device__ __forceinline__ void one_head(const HeadJob& J, int vec_hd, const Lds
 #pragma unroll
   for (int w = 0; w < kNT / 64; w++) mx = fmaxf(mx, L.red[w]);
   for (int t = tid; t < n; t += kNT) sc[t] = dev_expf(sc[t] - mx);
-  const bool in_lds = n <= kScoreLds;
-  if (in_lds)  // zero fill for the single-lane fold
+  if (SC_LDS)  // zero fill for the single-lane fold
     for (int t = n + tid; t < exact::lane_pad(n); t += kNT) sc[t] = 0.0f;
   __syncthreads();
   // softmax sum in the reference's left-to-right order (norms.rs:53)
-  const float sum = in_lds ? exact::block_seq_sum_nonneg<kNT, true>(sc, n)
-                           : exact::block_seq_sum_nonneg<kNT, false>(sc, n);
+  const float sum = exact::block_seq_sum_nonneg<kNT, SC_LDS>(sc, n);
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
   for (int t = tid; t < n; t += kNT) sc[t] = sc[t] * inv;
   __syncthreads();
@@ -195,38 +209,49 @@ __device__ __forceinline__ void one_head(const HeadJob& J, int vec_hd, const Lds
   const bool folder = d < J.dw;
   float acc = 0.0f;
   if (J.vec) {
-    const int rows_per_chunk = kVChunkBytes / (J.dw * static_cast<int>(sizeof(T)));
-    const T* s_vt = reinterpret_cast<const T*>(L.v);
-    int t0 = 0;
-    VRegs r = fetch_v<F16>(J, t0, min(rows_per_chunk, n - t0));
-    while (t0 < n) {
-      const int nr = min(rows_per_chunk, n - t0);
-      store_v<F16>(L.v, nr, J.dw, r);
-      __syncthreads();
-      const int t1 = t0 + nr;
-      if (t1 < n) r = fetch_v<F16>(J, t1, min(rows_per_chunk, n - t1));  // in flight during the fold
+    constexpr int EPV = 16 / sizeof(T);
+    const int ppr = J.dw / EPV;                 // pieces per row
+    const int ch = (kPieces / ppr) / 4 * 4;     // rows per chunk, a multiple of 4
+    const int stride = ch + 4;
+    const int n_chunks = (n + ch - 1) / ch;
+    VPieces v = fetch_v<F16>(J, 0, min(ch, n), ppr);
+    make_products<F16>(v, sc, 0, min(ch, n), ppr, ch, L.prod);
+    if (n_chunks > 1) v = fetch_v<F16>(J, ch, min(ch, n - ch), ppr);
+    __syncthreads();
+    for (int c = 0; c < n_chunks; c++) {
+      const int t0 = c * ch, nr = min(ch, n - t0);
       if (folder) {
+        const float* pr = L.prod + (c & 1) * kProdFloats + d * stride;
         int i = 0;
-        for (; i + 8 <= nr; i += 8) {
-          float vv[8], pp[8];
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            vv[j] = Elem<F16>::get(s_vt[(i + j) * J.dw + d]);
-            pp[j] = sc[t0 + i + j];
-          }
-#pragma unroll
-          for (int j = 0; j < 8; j++) acc += pp[j] * vv[j];
+        for (; i + 4 <= nr; i += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(pr + i);
+          acc += x.x;
+          acc += x.y;
+          acc += x.z;
+          acc += x.w;
         }
-        for (; i < nr; i++) acc += sc[t0 + i] * Elem<F16>::get(s_vt[i * J.dw + d]);
+        for (; i < nr; i++) acc += pr[i];
+      }
+      if (c + 1 < n_chunks) {
+        const int t1 = t0 + ch;
+        make_products<F16>(v, sc, t1, min(ch, n - t1), ppr, ch, L.prod + ((c + 1) & 1) * kProdFloats);
+        if (c + 2 < n_chunks) v = fetch_v<F16>(J, t1 + ch, min(ch, n - t1 - ch), ppr);
       }
       __syncthreads();
-      t0 = t1;
     }
   } else if (folder) {
     const T* vb = static_cast<const T*>(J.v) + (size_t)J.kvh * J.hd + J.d0 + d;
     for (int t = 0; t < n; t++) acc += sc[t] * Elem<F16>::get(vb[(size_t)t * J.kv_stride]);
   }
   if (folder) J.dst[J.h * J.hd + J.d0 + d] = acc;
+}
+
+template <bool F16>
+__device__ __forceinline__ void one_head(const HeadJob& J, int vec_hd, const Lds& L) {
+  if (J.pos + 1 <= kScoreLds)
+    one_head_body<F16, true>(J, vec_hd, L, L.scores);
+  else
+    one_head_body<F16, false>(J, vec_hd, L, J.gscores);
 }
 
 // blockIdx.x -> (head, dim slice). When the count divides by the 8 XCDs,
@@ -250,7 +275,7 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
   __shared__ float s_q[256];
   __shared__ float s_red[kNT / 64];
   __shared__ __align__(16) float s_scores[exact::lane_pad(kScoreLds)];
-  __shared__ uint4 s_v[kVChunkBytes / 16];
+  __shared__ __align__(16) float s_prod[2 * kProdFloats];
   const int lb = logical_block(n_heads * dsplit);
   const int h = lb / dsplit, ds = lb % dsplit, i = blockIdx.y;
   const int p0 = pos_dev ? *pos_dev : pos0;
@@ -268,7 +293,7 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
   J.dst = out + (size_t)i * n_heads * hd;
   J.gscores = scratch ? scratch + ((size_t)i * n_heads * dsplit + lb) * scratch_stride : nullptr;
   J.vec = mode != 0;
-  Lds L{s_q, s_red, s_scores, s_v};
+  Lds L{s_q, s_red, s_scores, s_prod};
   one_head<F16>(J, mode, L);
 }
 

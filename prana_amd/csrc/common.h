@@ -59,6 +59,13 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return nan ? __uint_as_float(nb) : hw;
 }
 
+// f16 bits -> f32 for a value that only feeds arithmetic (a dot product
+// operand). Identical to f16_to_f32 except that a signalling NaN comes out
+// quiet with the same sign and payload — which is what the first arithmetic
+// operation does to f16_to_f32's signalling result anyway, so every result
+// computed from it is unchanged. One instruction instead of five.
+__device__ __forceinline__ float f16_operand(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
 // f32 -> f16 bits, round-to-nearest-even, exactly as lib.rs:78-113 (NaN ->
 // sign | 0x7e00; hardware RNE matches every other input exhaustively).
 __device__ __forceinline__ uint16_t f32_to_f16(float x) {

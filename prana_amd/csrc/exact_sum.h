@@ -176,16 +176,18 @@ __device__ __forceinline__ float lane_seq_sum_padded(const float* a, int n) {
   return s;
 }
 
-// Below this length the single-lane chain (about 4-5 cycles per term) is
-// faster than the binade scan, whose cost is a few thousand cycles per binade.
+// Up to this length a padded sum is one lane's chain (about five cycles per
+// term); longer sums use the binade scan, whose steps cost a few thousand
+// cycles each but whose step count grows only with log2(n).
 constexpr int kSerialMax = 8192;
 
 // The sequential fold of a[0..n), a[i] >= 0, evaluated by an NT-lane
 // workgroup (blockDim.x == NT); every lane returns the same value. Must be
 // called by all lanes. a may live in LDS or global memory (read-only here,
 // visible to the whole workgroup). PADDED: a is an LDS buffer, 16-byte
-// aligned and zero-filled up to lane_pad(n) terms; short sums run on
-// one lane. Other sums use the binade scan, holding up to NT*CMAX terms in
+// aligned and zero-filled up to lane_pad(n) terms; sums of up to kSerialMax
+// terms are then folded by one lane. Other sums use the binade scan,
+// holding up to NT*CMAX terms in
 // registers (thread t owns the contiguous run [t*C, t*C + C),
 // C = ceil(n/NT)) and streaming longer sums from `a`. Sums with non-finite
 // terms run on one lane.
@@ -206,9 +208,10 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
         for (int i = 0; i < n; i++) s += a[i];
         s_sum = s;
       }
-    } else if (tid == 0) {
-      s_sum = lane_seq_sum_padded(a, n);
+      __syncthreads();
+      return s_sum;
     }
+    if (tid == 0) s_sum = lane_seq_sum_padded(a, n);
     __syncthreads();
     return s_sum;
   }

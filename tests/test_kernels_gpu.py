@@ -281,6 +281,26 @@ def test_attention_decode(nh, nkv, hd, pos):
     assert same_bits(P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd))
 
 
+def test_attention_decode_special_values():
+    # f16 K/V holding NaNs (quiet and signalling payloads), infinities, the
+    # largest finite f16 and subnormals: results must match bit for bit,
+    # NaN payloads included.
+    nh, nkv, hd, pos = 8, 2, 128, 300
+    kc, vc = _cache(pos + 1, nkv, hd, 11)
+    r = rng(12)
+    idx_v = r.choice(vc.size, 40, replace=False)
+    vc[idx_v[:10]] = 0x7E00          # quiet NaN
+    vc[idx_v[10:20]] = 0x7C01        # signalling NaN payload
+    vc[idx_v[20:25]] = 0xFC00        # -inf
+    vc[idx_v[25:30]] = 0x7C00        # +inf
+    vc[idx_v[30:]] = r.integers(1, 0x400, 10)  # subnormals
+    idx_k = r.choice(kc.size, 20, replace=False)
+    kc[idx_k[:10]] = 0x7BFF          # 65504
+    kc[idx_k[10:]] = r.integers(1, 0x400, 10)
+    q = rng(13).standard_normal(nh * hd).astype(np.float32)
+    assert same_bits(P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd))
+
+
 def test_attention_verify():
     nh, nkv, hd, pos0, seq = 32, 8, 128, 512, 9
     kc, vc = _cache(pos0 + seq, nkv, hd, 4)
