@@ -3,10 +3,14 @@
 
 A step is one decoded token: the full forward pass (32 layers, untied Q4_0 LM
 head) plus the device argmax feeding the next step, after a 512-token prefill.
-The weight GEMVs are also timed per launch with HIP events on their stream and
-reported against the 8 TB/s HBM roofline; the reference's CPU path (the C
-restatement of its scalar tier, row-parallel on the host cores) is timed on a
-bounded sample of the same workload.
+Inside the timed steps every 8th weight-GEMV dispatch records start/stop HIP
+events as part of the dispatch (on its stream); their average gives the
+roofline figure against the 8 TB/s HBM peak. The same number of steps is also
+timed without any events (reported beside). The
+HBM traffic per GEMV launch comes from the committed rocprofv3 counter
+summary (profiles/q4_0_gemv_7b_decode_traffic.json) when present. The
+reference's CPU path (the C restatement of its scalar tier, row-parallel on
+the host cores) is timed on a bounded sample of the same workload.
 
 Prints one JSON line. --gpus above 1 is not supported by this build.
 """
@@ -37,20 +41,18 @@ def main():
     ap.add_argument("--prefill", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers (not a valid benchmark)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 512 MiB device-to-device copy (the reference kernel for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the decode path shards by weight rows / KV heads as described in DESIGN.md but is not built "
-              "for more than one GPU.", file=sys.stderr)
+              "the decode path would shard by weight rows and KV heads, which is not built.", file=sys.stderr)
         sys.exit(2)
 
     import prana_amd as P
     from prana_amd import models as M
 
     cfg = dict(M.C4)
-    if args.layers:
-        cfg["n_layers"] = args.layers
     K, W, npre = args.steps, args.warmup, args.prefill
     t0 = time.time()
     tensors = M.synth_tensors(cfg, M.types_c4, 4)
@@ -60,10 +62,18 @@ def main():
     stream_bytes = model.stream_bytes()
     log(f"uploaded model in {time.time() - t0:.1f}s; {stream_bytes / 1e9:.4f} GB of weights streamed per token")
 
+    if args.copy_calibration:
+        nb = 512 << 20
+        a, b = P.DeviceArray(nb, np.uint8), P.DeviceArray(nb, np.uint8)
+        P.check(P.load().prana_memset_d(a.ptr, 1, nb))
+        P.check(P.load().prana_memcpy_d2d(b.ptr, a.ptr, nb))
+        a.free()
+        b.free()
+        log(f"calibration copy: {nb} bytes device to device")
+
     rng = np.random.default_rng(512)
     prompt = rng.integers(0, cfg["vocab_size"], npre).astype(np.uint32)
-    k_prof = min(K, 64)
-    cache = model.cache(npre + W + K + k_prof + 2)
+    cache = model.cache(npre + W + 2 * K + 2)
     t0 = time.perf_counter()
     cache.prefill(prompt[:-1])
     prefill_s = time.perf_counter() - t0
@@ -75,23 +85,37 @@ def main():
     last = int(toks[-1]) if W else int(prompt[-1])
     log(f"warmup {W} steps done")
 
+    # Timed region: K decode steps. Every 8th weight-GEMV dispatch carries
+    # start/stop HIP events (dispatch timestamps on its stream); 129 GEMV
+    # launches per token make the sampled launches rotate over all shapes.
+    P.gemv_profile(True, period=8)
+    P.gemv_profile_read(reset=True)
     P.check(P.load().prana_synchronize())
     t0 = time.perf_counter()
     toks = cache.decode(last, pos, K)
     P.check(P.load().prana_synchronize())
     dt = time.perf_counter() - t0
-    pos += K
-    tok_s = K / dt
-    log(f"timed {K} decode steps: {dt * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
-
-    # GEMV roofline: HIP events around every GEMV launch of k_prof more steps.
-    P.gemv_profile(True)
-    P.gemv_profile_read(reset=True)
-    cache.decode(int(toks[-1]), pos, k_prof)
     n_launch, gsec, gbytes = P.gemv_profile_read(reset=True)
     P.gemv_profile(False)
+    pos += K
+    tok_s = K / dt
     gemv_gbs = gbytes / gsec / 1e9 if gsec > 0 else 0.0
-    log(f"GEMV: {n_launch} launches, avg {gsec / max(n_launch, 1) * 1e6:.2f} us, {gemv_gbs:.1f} GB/s")
+    log(f"timed {K} decode steps: {dt * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
+    log(f"GEMV: {n_launch} timed launches, avg {gsec / max(n_launch, 1) * 1e6:.2f} us, {gemv_gbs:.1f} GB/s")
+
+    # The same number of steps again without any events.
+    P.check(P.load().prana_synchronize())
+    t0 = time.perf_counter()
+    cache.decode(int(toks[-1]), pos, K)
+    P.check(P.load().prana_synchronize())
+    dt_plain = time.perf_counter() - t0
+    log(f"run without events: {K / dt_plain:.1f} tok/s")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "q4_0_gemv_7b_decode_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
 
     cpu = None
     if not args.no_cpu:
@@ -130,12 +154,12 @@ def main():
         "data": "synthetic (seeded N(0,0.02) random-init weights, random prompt ids)",
         "config": {
             "workload": "7B-shape llama (dim 4096, 32 layers, 32/8 heads, FFN 14336, vocab 32000), all Q4_0, "
-                        f"untied Q4_0 head; greedy decode at batch 1 after a {npre}-token prefill"
-                        + (f" [DEBUG: {cfg['n_layers']} layers]" if args.layers else ""),
+                        f"untied Q4_0 head; greedy decode at batch 1 after a {npre}-token prefill",
             "prefill_tokens": npre,
             "weight_bytes_per_token": stream_bytes,
             "decode_weight_stream_gbs": round(stream_bytes * tok_s / 1e9, 2),
             "prefill_tok_s": round((npre - 1) / prefill_s, 2),
+            "tok_s_without_events": round(K / dt_plain, 3),
             "exact": "token-identical to the reference scalar path (bit-exact f32 order)",
         },
         "roofline": {
@@ -144,9 +168,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "Q4_0 GEMV (all decode projections + head)",
-            "launches": n_launch,
+            "timed_launches": n_launch,
             "avg_launch_us": round(gsec / max(n_launch, 1) * 1e6, 3),
             "bytes_per_launch": round(gbytes / max(n_launch, 1)),
         },

@@ -19,8 +19,7 @@
  *     buffers and synchronise before returning.
  *
  * Numerics: results are bit-identical to the reference's scalar tier
- * (integer block dots exact, f32 folds in the reference's order); the only
- * entry point with a different order is prana_attention_decode_splitk.
+ * (integer block dots exact, f32 folds in the reference's order).
  */
 #ifndef PRANA_HIP_H
 #define PRANA_HIP_H
@@ -52,6 +51,10 @@ int prana_device_alloc(size_t bytes, void **out);
 int prana_device_free(void *p);
 int prana_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int prana_memcpy_d2h(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy on the library stream (synchronous). No reference
+ * counterpart: a plain copy of known size, used to calibrate HBM traffic
+ * counters against the GEMVs. */
+int prana_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int prana_memset_d(void *dst, int value, size_t bytes);
 int prana_synchronize(void);
 
@@ -191,9 +194,11 @@ int prana_forward_batch(prana_model_t m, prana_cache_t c, const uint32_t *tokens
  * sampled ids at the end. No stop ids. */
 int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, size_t n_steps, uint32_t *out);
 
-/* GEMV launch profiling for roofline accounting: while on, every model GEMV is
- * bracketed by HIP events on its stream; read returns launches, summed kernel
- * seconds and summed algorithmic weight bytes since the last reset.
+/* GEMV launch profiling for roofline accounting: with on = P > 0, every P-th
+ * model decode-GEMV dispatch records start/stop HIP events as part of the
+ * dispatch itself (on its stream); on = 0 turns it off. read returns the timed
+ * launches, their summed kernel seconds and summed algorithmic weight bytes
+ * since the last reset.
  * No counterpart in the reference (its timing is PRANA_TIMING, infer.rs:81-130). */
 int prana_gemv_profile(int on);
 int prana_gemv_profile_read(size_t *launches, double *seconds, double *bytes, int reset);

@@ -322,8 +322,9 @@ class Model:
             pass
 
 
-def gemv_profile(on):
-    check(load().prana_gemv_profile(1 if on else 0))
+def gemv_profile(on, period=1):
+    """Time every `period`-th decode-GEMV dispatch while on (dispatch timestamps)."""
+    check(load().prana_gemv_profile(max(1, int(period)) if on else 0))
 
 
 def gemv_profile_read(reset=True):

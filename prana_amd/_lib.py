@@ -49,6 +49,7 @@ _SIGS = {
     "prana_device_free": (c_int, [c_void_p]),
     "prana_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size]),
     "prana_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size]),
+    "prana_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size]),
     "prana_memset_d": (c_int, [c_void_p, c_int, c_size]),
     "prana_synchronize": (c_int, []),
     "prana_mat_create": (c_int, [c_int, c_size, c_size, c_void_p, c_size, C.POINTER(c_void_p)]),

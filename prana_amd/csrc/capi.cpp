@@ -97,6 +97,15 @@ int prana_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   });
 }
 
+int prana_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    if (bytes) PRANA_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx().stream));
+    PRANA_HIP(hipStreamSynchronize(ctx().stream));
+    return static_cast<int>(kOk);
+  });
+}
+
 int prana_memset_d(void* dst, int value, size_t bytes) {
   return guard([&] {
     INIT_OR_RETURN();
@@ -506,7 +515,9 @@ int prana_gemv_profile(int on) {
     INIT_OR_RETURN();
     GemvProfile& gp = gemv_profile();
     int rc = gp.collect();
-    gp.on = on != 0;
+    gp.on = on > 0;
+    gp.period = on > 0 ? static_cast<size_t>(on) : 1;
+    gp.calls = 0;
     return rc;
   });
 }

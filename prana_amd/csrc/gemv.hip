@@ -7,6 +7,8 @@
 // block dot. The i32 dots are order-free and run 4-wide on v_dot4_i32_i8; the
 // f32 terms are computed in parallel; only the fold is sequential, one lane per
 // output, reading the terms back from LDS in block order.
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <type_traits>
 
@@ -14,6 +16,11 @@
 #include "kernels.h"
 
 namespace prana {
+
+LaunchEvents& launch_events() {
+  thread_local LaunchEvents ev;
+  return ev;
+}
 
 size_t devmat_bytes(const DevMat& m) {
   size_t n = m.rows * m.cols;
@@ -696,8 +703,15 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
       j.hsum += t0 * H / 32;
     }
     const size_t G = K / 32;
-    hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s, j, q + t0 * K,
-                       sa + t0 * G, sums + t0 * G, (int)nt);
+    LaunchEvents& le = launch_events();
+    if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
+      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s,
+                            le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      le = LaunchEvents{};
+    } else {
+      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s, j,
+                         q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+    }
     PRANA_LAUNCH_CHECK();
   }
   return kOk;

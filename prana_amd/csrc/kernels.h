@@ -49,6 +49,14 @@ int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStrea
 int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale, float* out, hipStream_t s);
 
 // ---- gemv.hip
+// Optional dispatch timestamps for the next decode GEMV launch on this
+// thread: when set, the launch records start/stop into these events as part
+// of the kernel dispatch itself (hipExtLaunchKernelGGL), then clears them.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents& launch_events();
+
 // out[t*ldo + r] (mode): 0 = store, 1 = store + bias[r], 2 = out += result
 // (the residual add x += o of infer.rs:186-188, 201-203).
 struct GemvOut {

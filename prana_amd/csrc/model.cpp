@@ -218,16 +218,20 @@ uint16_t* Cache::v(size_t l) const { return buf.as<uint16_t>() + (2 * l + 1) * l
 template <class F>
 int Model::timed(size_t bytes, size_t n, hipStream_t s, F&& launch) {
   GemvProfile& gp = gemv_profile();
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (gp.on) {
-    PRANA_HIP(hipEventCreate(&e0));
-    PRANA_HIP(hipEventCreate(&e1));
-    PRANA_HIP(hipEventRecord(e0, s));
+  size_t ev = 0;
+  const bool sample = gp.on && (gp.calls++ % gp.period == 0);
+  if (sample) {
+    if (int rc = gp.next_pair(&ev)) return rc;
+    launch_events() = LaunchEvents{gp.pool[ev], gp.pool[ev + 1]};
   }
   int rc = launch();
-  if (gp.on) {
-    PRANA_HIP(hipEventRecord(e1, s));
-    gp.pending.push_back({e0, e1, bytes, n});
+  if (sample) {
+    if (launch_events().start) {  // not a single timestamped decode launch: bracket on the stream
+      launch_events() = LaunchEvents{};
+      gp.skipped += 1;
+    } else {
+      gp.pending.push_back({ev, bytes, n});
+    }
   }
   return rc;
 }
@@ -287,18 +291,28 @@ GemvProfile& gemv_profile() {
   return p;
 }
 
+int GemvProfile::next_pair(size_t* ev) {
+  while (used + 2 > pool.size()) {
+    hipEvent_t e;
+    PRANA_HIP(hipEventCreate(&e));
+    pool.push_back(e);
+  }
+  *ev = used;
+  used += 2;
+  return kOk;
+}
+
 int GemvProfile::collect() {
   for (auto& r : pending) {
-    PRANA_HIP(hipEventSynchronize(r.e1));
+    PRANA_HIP(hipEventSynchronize(pool[r.ev + 1]));
     float ms = 0.0f;
-    PRANA_HIP(hipEventElapsedTime(&ms, r.e0, r.e1));
+    PRANA_HIP(hipEventElapsedTime(&ms, pool[r.ev], pool[r.ev + 1]));
     launches += 1;
     seconds += ms * 1e-3;
     bytes += static_cast<double>(r.bytes);
-    (void)hipEventDestroy(r.e0);
-    (void)hipEventDestroy(r.e1);
   }
   pending.clear();
+  used = 0;
   return kOk;
 }
 

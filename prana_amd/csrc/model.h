@@ -44,15 +44,26 @@ struct Workspace {
 
 // Optional per-launch timing of the model's GEMVs (HIP events on the stream
 // the GEMV runs on), for roofline accounting.
+// Each timed GEMV launch carries its own dispatch timestamps (no extra
+// markers on the stream); events come from a pool that grows on demand and
+// is reused across collections. Launches that are not a single decode-GEMV
+// dispatch are counted in `skipped` and not timed. With period P only every
+// P-th launch is timed (129 GEMV launches per 7B token, so the sampled
+// positions rotate over all shapes).
 struct GemvProfile {
   struct Rec {
-    hipEvent_t e0, e1;
+    size_t ev;  // index of the first of two pool events
     size_t bytes, n_tok;
   };
   bool on = false;
+  size_t period = 1;  // time every period-th GEMV launch
+  size_t calls = 0;
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
   std::vector<Rec> pending;
   double seconds = 0.0, bytes = 0.0;
-  size_t launches = 0;
+  size_t launches = 0, skipped = 0;
+  int next_pair(size_t* ev);
   int collect();
 };
 GemvProfile& gemv_profile();

@@ -165,6 +165,15 @@ def test_rmsnorm_adversarial(dim):
         assert same_bits(got[i], want[i]), i
 
 
+def test_sequential_order_closed_forms_on_device():
+    from tests.test_oracle import order_cases, pv_order_case
+    x_rms, y0, x_sm, p0 = order_cases()
+    assert P.rmsnorm(x_rms[None, :], np.ones(x_rms.size, np.float32), 0.0)[0, 0] == y0
+    assert P.softmax(x_sm[None, :])[0, 0] == p0
+    q, kc, vc, pos, nh, nkv, hd = pv_order_case()
+    assert P.attention_decode(q, kc, vc, pos, nh, nkv, hd)[0] == np.float32(0.25)
+
+
 def test_silu_and_expf():
     x = np.concatenate([rng(1).standard_normal(100000).astype(np.float32) * 10,
                         np.array([0.0, -0.0, 88.0, -88.0, 100.0, -104.0, -110.0, np.inf, -np.inf], np.float32)])

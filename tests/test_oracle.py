@@ -262,6 +262,45 @@ def test_rmsnorm_constant_row():  # norms.rs:66-74
     assert np.all(np.abs(y - 1.0) < 1e-5)
 
 
+def order_cases():
+    """Inputs whose left-to-right f32 fold has a closed form that any other
+    summation order misses (half-ulp ties against the running sum)."""
+    n = 37
+    # rmsnorm: squares 1, 2^-24, ... -> every add ties to the even 1.0
+    x_rms = np.full(n, 2.0 ** -12, np.float32)
+    x_rms[0] = 1.0
+    ss = np.float32(1.0)
+    y0 = np.float32(1.0) * (np.float32(1.0) / np.sqrt(ss / np.float32(n) + np.float32(0.0)))
+    # softmax: exps 1, ~1.5*2^-24, ... -> every add rounds up by exactly one ulp of [1, 2)
+    a = np.float32(math.log(1.5) - 24 * math.log(2.0))
+    x_sm = np.full(n, a, np.float32)
+    x_sm[0] = 0.0
+    p0 = np.float32(1.0) * (np.float32(1.0) / np.float32(1.0 + (n - 1) * 2.0 ** -23))
+    return x_rms, y0, x_sm, p0
+
+
+def pv_order_case():
+    """q = 0 gives p = 1/4 for 4 cache rows; v[dim 0] = 1, 2^-24, 2^-24, 2^-24
+    makes every later product a half-ulp tie against 0.25, so the sequential
+    fold stays exactly 0.25 (any regrouping gives 0.25 + 2^-24)."""
+    nh = nkv = 1
+    hd, pos = 16, 3
+    q = np.zeros(hd, np.float32)
+    kc = np.zeros((pos + 1) * hd, np.uint16)
+    vc = np.zeros((pos + 1) * hd, np.uint16)
+    vc[0] = 0x3C00  # 1.0
+    vc[hd::hd] = 0x0001  # 2^-24
+    return q, kc, vc, pos, nh, nkv, hd
+
+
+def test_sequential_order_closed_forms():
+    x_rms, y0, x_sm, p0 = order_cases()
+    assert O.rmsnorm(x_rms, np.ones(x_rms.size, np.float32), 0.0)[0, 0] == y0
+    assert O.softmax(x_sm)[0] == p0
+    q, kc, vc, pos, nh, nkv, hd = pv_order_case()
+    assert O.attention_decode(q, kc, vc, pos, nh, nkv, hd)[0] == np.float32(0.25)
+
+
 def test_softmax_props():  # norms.rs:77-106
     p = O.softmax(np.array([1.0, 2.0, 3.0], np.float32))
     assert abs(p.sum() - 1.0) < 1e-6 and p[0] < p[1] < p[2]
