@@ -423,7 +423,7 @@ struct DecodeJob {
 };
 
 constexpr int kDecMaxTok = 4;   // tokens per launch (LDS permitting)
-constexpr int kActRows = 32;    // act-mode rows per matrix: one quantization block
+constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: one quantization block
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
 // STAGED: more than one stage (double-buffered registers and terms);
@@ -458,16 +458,10 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
     qbase[j] = job.m[ACT ? j : mi].qs;
     sbase[j] = static_cast<const uint8_t*>(job.m[ACT ? j : mi].sc);
   }
-  // upk[i] = row << 16 | block offset of unit i (row < 64 + 64, offset < 16384)
-  int upk[U];
-#pragma unroll
-  for (int i = 0; i < U; i++) {
-    const int v = tid + NT * i;
-    const int row = v / SB;
-    upk[i] = (row << 16) | (v - row * SB);
-  }
-  auto unit_row = [&](int i) { return upk[i] >> 16; };
-  auto unit_off = [&](int i) { return upk[i] & 0xffff; };
+  // unit i of this lane: v = tid + NT*i -> (row, block offset) = divmod(v, SB),
+  // recomputed where needed (cheaper in registers than keeping U pairs).
+  auto unit_row = [&](int i) { return (tid + NT * i) / SB; };
+  auto unit_off = [&](int i) { return (tid + NT * i) % SB; };
   auto unit_up = [&](int i) { return ACT && unit_row(i) >= rt; };
   auto unit_lr = [&](int i) { return unit_up(i) ? unit_row(i) - rt : unit_row(i); };
   auto load_stage = [&](R* buf, int s) {
@@ -599,8 +593,10 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
     if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
     return;
   }
-  // act epilogue: gate lanes (row < 32) pair with up lanes (row + 32);
-  // h = act(g) * u, then quantize the 32-row block (one 32-lane group).
+  // act epilogue: gate lanes (row < rt) pair with up lanes (row + rt);
+  // h = act(g) * u. When the tile holds whole 32-row blocks (rt % 32 == 0),
+  // each block is quantized here by one 32-lane group; otherwise the caller
+  // quantizes h afterwards.
   __syncthreads();  // every fold read of the term buffers is done
   float* hx = terms;
   if (tid < n_tok * ROWS) hx[tid] = acc;
@@ -623,15 +619,17 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
       v = g * u;
       if (lv && job.h) job.h[fl_tok * H + r] = v;
     }
-    float scale;
-    int sum;
-    int qi = quantize_lane(lv ? v : 0.0f, &scale, &sum);
-    if (lv) {
-      size_t gi = fl_tok * H + r;
-      job.hq[gi] = static_cast<int8_t>(qi);
-      if ((gi & 31) == 0) {
-        job.hsa[gi >> 5] = scale;
-        job.hsum[gi >> 5] = sum;
+    if (rt % 32 == 0) {  // whole waves take part (ROWS = 2*rt is a multiple of 64)
+      float scale;
+      int sum;
+      int qi = quantize_lane(lv ? v : 0.0f, &scale, &sum);
+      if (lv) {
+        size_t gi = fl_tok * H + r;
+        job.hq[gi] = static_cast<int8_t>(qi);
+        if ((gi & 31) == 0) {
+          job.hsa[gi >> 5] = scale;
+          job.hsum[gi >> 5] = sum;
+        }
       }
     }
   }
@@ -648,12 +646,16 @@ TileGeom choose_geom(size_t K, bool act) {
   using R = RegUnit<KIND>;
   const int nb = static_cast<int>(K / R::kElems);
   const bool small_unit = R::kElems == 32;
-  if (act) {  // 32 rows of gate and of up: 64 rows x sb units = nt * u
-    if (small_unit && nb * 64 == 512 * 16) return TileGeom{16, kActRows, nb, 512};  // one stage
+  if (act) {  // rt rows of gate and of up: 2*rt rows x sb units = 256 * u
+    const int cand_act[] = {4, 2, 8, 7, 1};
+    for (int c = 0; small_unit && c < 5; c++) {  // one stage: whole rows per tile
+      const int u = cand_act[c];
+      if ((128 * u) % nb == 0 && 128 * u / nb <= kActRows) return TileGeom{u, 128 * u / nb, nb, 256};
+    }
     if (small_unit) return TileGeom{8, kActRows, 32, 256};
     return TileGeom{1, kActRows, 4, 256};
   }
-  const int cand_small[] = {2, 4, 1, 7, 8};
+  const int cand_small[] = {4, 2, 1, 7, 8};
   const int cand_k[] = {1, 2};
   const int* cand = small_unit ? cand_small : cand_k;
   const int nc = small_unit ? 5 : 2;
@@ -727,9 +729,15 @@ int launch_decode_t(const DecodeJob& job, const int8_t* q, const float* sa, cons
   const bool staged = g.sb < nb;
   if (act) {
     if constexpr (kSmall) {
-      if (g.nt == 512) return launch_tile_u<KIND, 16, true, false, 512>(job, g, q, sa, sums, n_tok, s);
-      if (!staged) return launch_tile_u<KIND, 8, true, false, 256>(job, g, q, sa, sums, n_tok, s);
-      return launch_tile_u<KIND, 8, true, true, 256>(job, g, q, sa, sums, n_tok, s);
+      if (staged) return launch_tile_u<KIND, 8, true, true, 256>(job, g, q, sa, sums, n_tok, s);
+      switch (g.u) {
+        case 1: return launch_tile_u<KIND, 1, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+        case 2: return launch_tile_u<KIND, 2, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+        case 4: return launch_tile_u<KIND, 4, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+        case 7: return launch_tile_u<KIND, 7, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+        case 8: return launch_tile_u<KIND, 8, true, false, 256>(job, g, q, sa, sums, n_tok, s);
+      }
+      return fail(kErrInvalid, "gemv: no act tile geometry");
     } else {
       if (!staged) return launch_tile_u<KIND, 1, true, false, 256>(job, g, q, sa, sums, n_tok, s);
       return launch_tile_u<KIND, 1, true, true, 256>(job, g, q, sa, sums, n_tok, s);
@@ -887,7 +895,15 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
   job.hq = hq;
   job.hsa = hsa;
   job.hsum = hsum;
-  return dispatch_kind(gate.kind, [&](auto k) { return launch_decode_t<decltype(k)::value>(job, q, sa, sums, n_tok, s); });
+  bool in_kernel = false;
+  int rc = dispatch_kind(gate.kind, [&](auto k) {
+    constexpr int KIND = decltype(k)::value;
+    in_kernel = choose_geom<KIND>(gate.cols, true).rt % 32 == 0;
+    if (!in_kernel && h == nullptr) return fail(kErrInvalid, "gemv_act: this shape needs the f32 h output");
+    return launch_decode_t<KIND>(job, q, sa, sums, n_tok, s);
+  });
+  if (rc || in_kernel) return rc;
+  return launch_quantize_acts(h, n_tok, gate.rows, hq, hsa, hsum, s);  // matmul.rs:105-127 on h
 }
 
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
