@@ -168,6 +168,32 @@ __device__ __forceinline__ int quantize_lane(float x, float* scale_out, int* sum
   return v;
 }
 
+// quantize_lane for B independent blocks at once (value b of this lane in
+// y[b]); the B cross-lane reductions are interleaved so that their latencies
+// overlap.
+template <int B>
+__device__ __forceinline__ void quantize_lanes(const float* y, int* q, float* scale, int* sum) {
+  float amax[B];
+#pragma unroll
+  for (int b = 0; b < B; b++) amax[b] = fabsf(y[b]);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+#pragma unroll
+    for (int b = 0; b < B; b++) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], o, 64));
+  }
+#pragma unroll
+  for (int b = 0; b < B; b++) {
+    scale[b] = amax[b] > 0.0f ? amax[b] / 127.0f : 1.0f;
+    q[b] = round_clamp127(y[b] * (1.0f / scale[b]));
+    sum[b] = q[b];
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+#pragma unroll
+    for (int b = 0; b < B; b++) sum[b] += __shfl_xor(sum[b], o, 64);
+  }
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }

@@ -47,40 +47,71 @@ int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, flo
 // left-to-right fold from -0.0, evaluated exactly by the whole workgroup; the
 // normalise + optional quantize is parallel.
 constexpr int kNormNT = 1024;
+constexpr int kNormMaxDim = 16320;  // row and weights staged in LDS (about 132 KB)
 __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                           int dim, float eps, float* __restrict__ out,
                                                           int8_t* __restrict__ q, float* __restrict__ sa,
                                                           int* __restrict__ sums) {
-  extern __shared__ float4 sq4[];  // dim squares, zero-filled up to lane_pad(dim)
-  float* sq = reinterpret_cast<float*>(sq4);
+  constexpr int kPer = (kNormMaxDim + kNormNT - 1) / kNormNT;
+  extern __shared__ float4 smem_n4[];
+  float* xs = reinterpret_cast<float*>(smem_n4);  // the row, at exact::run_pad(i)
+  float* wl = xs + exact::run_pad(dim);           // the weights
   const float* row = x + (size_t)blockIdx.x * dim;
-  const int padded = exact::lane_pad(dim);
-  for (int i = threadIdx.x; i < padded; i += kNormNT) {
-    float v = i < dim ? row[i] : 0.0f;
-    sq[i] = v * v;
+  const int tid = threadIdx.x;
+  {  // every load in flight at once
+    float xv[kPer], wv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      if (k * kNormNT >= dim) break;                  // uniform
+      const int i = min(tid + k * kNormNT, dim - 1);  // in bounds; stored only below dim
+      xv[k] = row[i];
+      wv[k] = w[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      if (k * kNormNT >= dim) break;
+      const int i = tid + k * kNormNT;
+      if (i < dim) {
+        xs[exact::run_pad(i)] = xv[k];
+        wl[i] = wv[k];
+      }
+    }
   }
   __syncthreads();
   // sum of squares in the reference's left-to-right order (norms.rs:15)
-  const float ss = exact::block_seq_sum_nonneg<kNormNT, true>(sq, dim);
+  const float ss = exact::block_seq_sum_short<kNormNT>(
+      [xs](int i) {
+        const float v = xs[exact::run_pad(i)];
+        return v * v;
+      },
+      dim);
   const float mean_sq = ss / static_cast<float>(dim);
   const float inv = 1.0f / sqrtf(mean_sq + eps);
-  // dim is a multiple of 32 whenever q != nullptr; round the loop up to a
-  // whole number of 32-lane groups so every group reduces together.
-  int span = q ? ((dim + kNormNT - 1) / kNormNT) * kNormNT : dim;
-  for (int i = threadIdx.x; i < span; i += kNormNT) {
-    bool live = i < dim;
-    float y = live ? row[i] * inv * w[i] : 0.0f;
-    if (live && out) out[(size_t)blockIdx.x * dim + i] = y;
+  // four elements per lane at a time; dim is a multiple of 32 whenever
+  // q != nullptr, so every 32-lane group is then all live or all past the end
+  // and reduces together.
+  for (int base = 0; base < dim; base += 4 * kNormNT) {
+    float y[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int i = base + b * kNormNT + tid;
+      y[b] = i < dim ? xs[exact::run_pad(i)] * inv * wl[i] : 0.0f;
+      if (i < dim && out) out[(size_t)blockIdx.x * dim + i] = y[b];
+    }
     if (q) {
-      float scale;
-      int sum;
-      int qi = quantize_lane(y, &scale, &sum);
-      if (live) {
-        size_t gi = (size_t)blockIdx.x * dim + i;
-        q[gi] = static_cast<int8_t>(qi);
-        if ((i & 31) == 0) {
-          sa[gi >> 5] = scale;
-          sums[gi >> 5] = sum;
+      float scale[4];
+      int qi[4], sum[4];
+      quantize_lanes<4>(y, qi, scale, sum);
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int i = base + b * kNormNT + tid;
+        if (i < dim) {
+          const size_t gi = (size_t)blockIdx.x * dim + i;
+          q[gi] = static_cast<int8_t>(qi[b]);
+          if ((i & 31) == 0) {
+            sa[gi >> 5] = scale[b];
+            sums[gi >> 5] = sum[b];
+          }
         }
       }
     }
@@ -91,8 +122,8 @@ int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, floa
                    float* sa, int* sums, hipStream_t s) {
   if (rows == 0) return kOk;
   PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
-  PRANA_CHECK(dim >= 1 && dim <= 16320, "rmsnorm: dim must be in 1..=16320");
-  const size_t lds = static_cast<size_t>(exact::lane_pad(static_cast<int>(dim))) * 4;
+  PRANA_CHECK(dim >= 1 && dim <= static_cast<size_t>(kNormMaxDim), "rmsnorm: dim must be in 1..=16320");
+  const size_t lds = (exact::run_pad(static_cast<int>(dim)) + dim) * 4;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormNT), lds, s, x, w, (int)dim, eps, out, q, sa, sums);
   PRANA_LAUNCH_CHECK();
   return kOk;

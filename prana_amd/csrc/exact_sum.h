@@ -10,12 +10,13 @@
 // choice that makes m' even — which depends only on the parity of m. So each
 // term is a pair of increments (for even / odd incoming m); pairs compose
 // associatively, and a workgroup scan gives every partial sum of the binade
-// exactly. The first step whose exact result reaches 2^24 ulps leaves the
-// binade: that one step is evaluated with an ordinary f32 add and the scan
-// restarts in the new binade. A sum of n comparable terms crosses about
-// log2(n) binades, so the whole fold costs a few dozen workgroup steps
-// instead of n dependent adds (used for long sums; short ones are cheaper as
-// one lane's chain). Non-finite terms fall back to a single-lane loop; a sum
+// exactly. A step that leaves the binade is evaluated with an ordinary f32
+// add. Two drivers place those steps: the predicted-binade scan guesses all
+// of them at once from approximate prefix sums and verifies the guess while
+// it walks the segments (one workgroup scan in total), and the adaptive scan
+// finds them one at a time (one workgroup scan per binade, for sums too long
+// for the first). Either replaces n dependent adds, each costing several
+// cycles of latency. Non-finite terms fall back to a single-lane loop; a sum
 // that overflows to +inf stays +inf.
 //
 // Terms are decoded from their bits with integer arithmetic only. The sign
@@ -100,6 +101,35 @@ __host__ __device__ inline int binade(float s) {
   return e;
 }
 
+// ---- predicted binades: one scan for the whole sum
+// The binade of every partial sum is predicted from approximate prefix sums
+// (ordinary f32 adds in any order, only used to choose grids). A step whose
+// predicted result binade differs from the predicted binade of its input is a
+// crossing; the steps between two crossings form a segment that stays on one
+// grid, so a single segmented workgroup scan of increment pairs gives every
+// segment's composed map. One lane then walks the K+1 segments: each crossing
+// step is an ordinary f32 add of the exact value before it, and each segment
+// applies its map to the exact value at its start. The walk also verifies the
+// prediction, which makes the result exact whenever it reports success:
+//   - a segment's start value must lie in the binade whose grid its pairs use;
+//   - its end value must still lie in that binade (< 2^24 grid units).
+// Increments are non-negative, so the sum never leaves a binade in the middle
+// of a segment without the end check seeing it, and inside the binade every
+// step's grid rounding is the f32 rounding. When a check fails (or there are
+// more than kPredMaxCross crossings) the caller folds serially instead.
+constexpr int kPredHead = 32;       // folded serially first (the sum grows fastest here)
+constexpr int kPredMaxCross = 63;   // crossings the walk accepts (one per lane of a wave)
+constexpr int kPredMaxPerLane = 64; // terms per lane of the predicted scan
+
+struct SegAcc {
+  Pair p;  // composed increments since the last crossing
+  int c;   // crossings so far (a crossing resets p to the identity)
+};
+
+__host__ __device__ inline SegAcc seg_combine(SegAcc a, SegAcc b) {
+  return SegAcc{b.c > 0 ? b.p : compose(a.p, b.p), a.c + b.c};
+}
+
 #if defined(__HIPCC__)
 // Workgroup-wide exclusive scan of Pair over NT lanes (NT/64 waves).
 // s_wave: LDS scratch of 2*NT/64 ints. *total gets the workgroup-wide
@@ -156,6 +186,7 @@ __device__ __forceinline__ float lane_seq_sum_padded(const float* a, int n) {
     const float4* q = p + 8 * b;
 #pragma unroll
     for (int j = 0; j < 8; j++) y[j] = q[8 + j];
+    __builtin_amdgcn_sched_barrier(0);  // keep the next batch's loads ahead of these adds
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       s += x[j].x;
@@ -165,6 +196,7 @@ __device__ __forceinline__ float lane_seq_sum_padded(const float* a, int n) {
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) x[j] = q[16 + j];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       s += y[j].x;
@@ -176,21 +208,329 @@ __device__ __forceinline__ float lane_seq_sum_padded(const float* a, int n) {
   return s;
 }
 
-// Up to this length a padded sum is one lane's chain (about five cycles per
-// term); longer sums use the binade scan, whose steps cost a few thousand
-// cycles each but whose step count grows only with log2(n).
-constexpr int kSerialMax = 8192;
+// LDS index of term i for buffers read as per-lane runs: one spare word per
+// 16 terms staggers the runs of neighbouring lanes across banks (a run length
+// of C words would otherwise put lanes C apart on the same bank). A buffer of
+// n terms needs run_pad(n - 1) + 1 words.
+__host__ __device__ constexpr int run_pad(int i) { return i + (i >> 4); }
+
+// Visit term(i0 + j), j = 0..nv-1, in order: f(j, value), in blocks of eight
+// fetched ahead of their use (about one fetch latency per eight terms). The
+// last block is padded with zero terms, which leave every pass below
+// unchanged, so the body needs no guards; fetches stay inside term(0..n).
+template <class Term, class F>
+__device__ __forceinline__ void for_each_run(Term a, int i0, int nv, int n, F&& f) {
+  for (int jb = 0; jb < nv; jb += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const float v = a(min(i0 + jb + u, n - 1));
+      t[u] = jb + u < nv ? v : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) f(jb + u, t[u]);
+  }
+}
+
+// Binade of a finite p >= 0 (the exponent field, subnormals and zero -> -126).
+__device__ __forceinline__ int binade_fast(float p) {
+  const int E = static_cast<int>((__float_as_uint(p) >> 23) & 0xffu);
+  return (E > 1 ? E : 1) - 127;
+}
+
+// term_pair_bits(bits(t), e) for finite t >= 0, from exact float operations
+// (scaling by a power of two, floor and the difference are exact here; a
+// scaled value small enough to lose bits is far below one half), without
+// branches.
+__device__ __forceinline__ Pair term_pair_fast(float t, int e) {
+  const float A = ldexpf(t, 23 - e);
+  const bool big = !(A < 268435456.0f);  // >= 2^28 (or +inf): leaves the binade
+  const float I = floorf(fminf(A, 268435456.0f));
+  const float f = A - I;
+  const int i = static_cast<int>(I);
+  const int v = i + (f > 0.5f ? 1 : 0);
+  const bool tie = f == 0.5f;
+  const int odd = i & 1;
+  return Pair{big ? kCap : (tie ? i + odd : v), big ? kCap : (tie ? i + 1 - odd : v)};
+}
+
+// One DPP step of a wave scan (bound_ctrl: lanes without a source read 0,
+// the identity of every operator scanned here).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_src(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xf, true);
+}
+// Inclusive wave-wide scan with an associative operator whose identity is
+// all-zero bits: shifts of 1, 2, 4, 8 inside 16-lane rows, then the row
+// broadcasts of lanes 15 and 31.
+template <class T, class Get, class Op>
+__device__ __forceinline__ T wave_scan_incl(T x, Get get, Op op) {
+  x = op(get([](int v) { return dpp_src<0x111, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x112, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x114, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x118, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x142, 0xa>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x143, 0xc>(v); }, x), x);
+  return x;
+}
+// The value of the previous lane (lane 0: all-zero bits).
+__device__ __forceinline__ int wave_shr1(int v) { return dpp_src<0x138, 0xf>(v); }
+
+__device__ __forceinline__ float scan_add_f32(float x) {
+  return wave_scan_incl(
+      x, [](auto mv, float v) { return __int_as_float(mv(__float_as_int(v))); },
+      [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ SegAcc scan_seg(SegAcc x) {
+  return wave_scan_incl(
+      x, [](auto mv, SegAcc v) { return SegAcc{Pair{mv(v.p.e), mv(v.p.o)}, mv(v.c)}; },
+      [](SegAcc a, SegAcc b) { return seg_combine(a, b); });
+}
+
+// Running composition of a lane's steps (a crossing resets it).
+__device__ __forceinline__ void seg_push(SegAcc& acc, bool cross, Pair pr) {
+  const Pair c = compose(acc.p, pr);
+  acc.p.e = cross ? 0 : c.e;
+  acc.p.o = cross ? 0 : c.o;
+  acc.c += cross ? 1 : 0;
+}
+
+// The fold of term(0..n) with n > kPredHead and n - kPredHead <= NT *
+// kPredMaxPerLane, terms >= 0; term(i) must return the same value in every
+// lane and every call (an LDS or global read, or a pure function of one).
+// Lane t owns positions [H + t*C, H + t*C + C): for LDS-backed terms, lay
+// them out so that runs of C consecutive positions in different lanes fall
+// in different banks. Returns the value in every lane and *ok; *ok is false
+// (value meaningless) when a term is not finite or the prediction failed.
+// Must be called by all NT lanes; contains five barriers.
+template <int NT, class Term>
+__device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
+  constexpr int W = NT / 64;
+  static_assert(kPredMaxCross < 64, "the walk keeps one segment per lane of wave 0");
+  __shared__ float s_fw[W];
+  __shared__ int s_epl[W], s_sw[3 * W];
+  __shared__ int s_tot[2 * (kPredMaxCross + 1)];
+  __shared__ float s_ct[kPredMaxCross + 1];
+  __shared__ int s_ce[kPredMaxCross + 1];
+  __shared__ float s_head, s_res;
+  __shared__ int s_ok;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = (n - kPredHead + NT - 1) / NT;
+  const int i0 = kPredHead + tid * C;
+  const int nv = max(0, min(C, n - i0));
+  bool bad = false;
+  if (tid == 0) {
+    float h[kPredHead];
+#pragma unroll
+    for (int i = 0; i < kPredHead; i++) h[i] = a(i);
+    float s = -0.0f;
+#pragma unroll
+    for (int i = 0; i < kPredHead; i++) s += h[i];
+    s_head = s;
+    bad = !(s <= 3.4028234663852886e38f);  // a head term is NaN or +inf
+  }
+  // pass 1: approximate prefix sums (any rounding; only the grids depend on
+  // them) and the finiteness check
+  float ls = 0.0f;
+  for_each_run(a, i0, nv, n, [&](int, float x) {
+    ls += x;
+    bad |= !(x <= 3.4028234663852886e38f);
+  });
+  const float inc = scan_add_f32(ls);
+  if (lane == 63) s_fw[wave] = inc;
+  if (__syncthreads_or(bad)) {
+    *ok = false;
+    return 0.0f;
+  }
+  float pre = 0.0f;
+#pragma unroll
+  for (int w = 0; w < W; w++)
+    if (w < wave) pre += s_fw[w];
+  const float sH = s_head;
+  const float P0 = sH + (pre + __int_as_float(wave_shr1(__float_as_int(inc))));
+  // pass 2: the predicted result binade of every owned step (P is recomputed
+  // identically in the fallback pass), the composition of steps 1..nv-1
+  // (their crossing flags are local; step 0's needs the previous lane's
+  // binade), and the first two local crossings: position, term, binade and
+  // the composition since the previous crossing (or since step 1).
+  int ep_first = 0, ep_last = 0, ncross = 0, e1 = 0, e2 = 0;
+  float x0 = 0.0f, x1 = 0.0f, x2 = 0.0f;
+  SegAcc rest{Pair{0, 0}, 0};
+  Pair pre1{0, 0}, pre2{0, 0};
+  {
+    float P = P0;
+    for_each_run(a, i0, nv, n, [&](int j, float x) {
+      P += x;
+      const int e = binade_fast(P);
+      if (j == 0) {
+        ep_first = e;
+        x0 = x;
+      } else {
+        const bool cross = e != ep_last;
+        // plain selects keep the records in registers
+        const bool r1 = cross && ncross == 0, r2 = cross && ncross == 1;
+        x1 = r1 ? x : x1;
+        e1 = r1 ? e : e1;
+        pre1.e = r1 ? rest.p.e : pre1.e;
+        pre1.o = r1 ? rest.p.o : pre1.o;
+        x2 = r2 ? x : x2;
+        e2 = r2 ? e : e2;
+        pre2.e = r2 ? rest.p.e : pre2.e;
+        pre2.o = r2 ? rest.p.o : pre2.o;
+        ncross += cross ? 1 : 0;
+        seg_push(rest, cross, term_pair_fast(x, e));
+      }
+      ep_last = e;
+    });
+  }
+  int prev_last = wave_shr1(ep_last);
+  if (lane == 63) s_epl[wave] = ep_last;
+  __syncthreads();
+  if (lane == 0) prev_last = wave > 0 ? s_epl[wave - 1] : binade_fast(sH);
+  int next_first = __shfl_down(ep_first, 1, 64);
+  const bool cross0 = ep_first != prev_last;
+  const SegAcc el0 = cross0 ? SegAcc{Pair{0, 0}, 1} : SegAcc{term_pair_fast(x0, ep_first), 0};
+  const SegAcc loc = nv > 0 ? seg_combine(el0, rest) : SegAcc{Pair{0, 0}, 0};
+  // workgroup exclusive segmented scan of the lanes' compositions
+  const SegAcc incs = scan_seg(loc);
+  if (lane == 63) {
+    s_sw[3 * wave] = incs.p.e;
+    s_sw[3 * wave + 1] = incs.p.o;
+    s_sw[3 * wave + 2] = incs.c;
+  }
+  // the first lane of each wave needs the next wave's first binade
+  __shared__ int s_epf[W];
+  if (lane == 0) s_epf[wave] = ep_first;
+  __syncthreads();
+  if (lane == 63) next_first = wave + 1 < W ? s_epf[wave + 1] : 0;
+  SegAcc run{Pair{0, 0}, 0}, all{Pair{0, 0}, 0};
+#pragma unroll
+  for (int w = 0; w < W; w++) {
+    const SegAcc t{Pair{s_sw[3 * w], s_sw[3 * w + 1]}, s_sw[3 * w + 2]};
+    if (w < wave) run = seg_combine(run, t);
+    all = seg_combine(all, t);
+  }
+  run = seg_combine(run, SegAcc{Pair{wave_shr1(incs.p.e), wave_shr1(incs.p.o)}, wave_shr1(incs.c)});
+  // pass 3: segment totals and crossing terms, indexed by segment, from the
+  // records of pass 2 (a lane with more crossings walks its run again)
+  if (all.c <= kPredMaxCross && nv > 0) {
+    const SegAcc r0 = seg_combine(run, el0);  // after step 0
+    if (cross0) {
+      s_ct[r0.c] = x0;
+      s_ce[r0.c] = ep_first;
+      if (r0.c == 1 && i0 == kPredHead) {  // segment 0 is empty
+        s_tot[0] = 0;
+        s_tot[1] = 0;
+      }
+    }
+    if (ncross <= 2) {
+      if (ncross >= 1) {
+        const Pair t1 = compose(r0.p, pre1);  // the segment ending at step j1-1
+        s_tot[2 * r0.c] = t1.e;
+        s_tot[2 * r0.c + 1] = t1.o;
+        s_ct[r0.c + 1] = x1;
+        s_ce[r0.c + 1] = e1;
+      }
+      if (ncross == 2) {
+        s_tot[2 * (r0.c + 1)] = pre2.e;
+        s_tot[2 * (r0.c + 1) + 1] = pre2.o;
+        s_ct[r0.c + 2] = x2;
+        s_ce[r0.c + 2] = e2;
+      }
+    } else {
+      SegAcc r = r0;
+      float P = P0;
+      int ein = prev_last;
+      for_each_run(a, i0, nv, n, [&](int j, float x) {
+        P += x;
+        const int e = binade_fast(P);
+        if (j > 0) {
+          const bool cross = e != ein;
+          if (cross) {  // step j-1 ends its segment
+            s_tot[2 * r.c] = r.p.e;
+            s_tot[2 * r.c + 1] = r.p.o;
+          }
+          seg_push(r, cross, term_pair_fast(x, e));
+          if (cross) {
+            s_ct[r.c] = x;
+            s_ce[r.c] = e;
+          }
+        }
+        ein = e;
+      });
+    }
+    if (i0 + nv == n || next_first != ep_last) {  // the lane's last step ends its segment
+      const SegAcc fin = seg_combine(run, loc);
+      s_tot[2 * fin.c] = fin.p.e;
+      s_tot[2 * fin.c + 1] = fin.p.o;
+    }
+  }
+  __syncthreads();
+  // the walk: wave 0 holds segment j in lane j and carries the exact value
+  // from segment to segment
+  if (wave == 0) {
+    const int K = all.c;
+    bool good = K <= kPredMaxCross;
+    const int jl = min(lane, kPredMaxCross);
+    const int te = s_tot[2 * jl], to = s_tot[2 * jl + 1], ce = s_ce[jl];
+    const float ct = s_ct[jl];
+    float val = sH;
+    int E = binade_fast(sH);
+    for (int j = 0; good && j <= K; j++) {
+      if (j > 0) {
+        val = val + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct), j));
+        E = __builtin_amdgcn_readlane(ce, j);
+        good = val <= 3.4028234663852886e38f;
+      }
+      int e;
+      int32_t m;
+      decompose(val, &e, &m);
+      const int32_t me = apply(Pair{__builtin_amdgcn_readlane(te, j), __builtin_amdgcn_readlane(to, j)}, m);
+      good = good && e == E && me < (1 << 24);
+      val = static_cast<float>(me) * ldexpf(1.0f, E - 23);
+    }
+    if (lane == 0) {
+      s_res = val;
+      s_ok = good;
+    }
+  }
+  __syncthreads();
+  *ok = s_ok != 0;
+  return s_res;
+}
+
 
 // The sequential fold of a[0..n), a[i] >= 0, evaluated by an NT-lane
 // workgroup (blockDim.x == NT); every lane returns the same value. Must be
 // called by all lanes. a may live in LDS or global memory (read-only here,
-// visible to the whole workgroup). PADDED: a is an LDS buffer, 16-byte
-// aligned and zero-filled up to lane_pad(n) terms; sums of up to kSerialMax
-// terms are then folded by one lane. Other sums use the binade scan,
-// holding up to NT*CMAX terms in
-// registers (thread t owns the contiguous run [t*C, t*C + C),
-// C = ceil(n/NT)) and streaming longer sums from `a`. Sums with non-finite
-// terms run on one lane.
+// visible to the whole workgroup). Sums of up to kPredHead + NT *
+// kPredMaxPerLane terms use the predicted-binade scan, falling back to one
+// lane's chain for non-finite terms, very short sums and failed predictions
+// (PADDED: a is an LDS buffer, 16-byte aligned and zero-filled up to
+// lane_pad(n) terms, so the chain runs on 16-byte loads). Longer sums use the
+// adaptive binade scan, holding up to NT*CMAX terms in registers (thread t
+// owns the contiguous run [t*C, t*C + C), C = ceil(n/NT)) and streaming
+// longer sums from `a`; non-finite terms again run on one lane.
+// The same fold for sums of at most kPredHead + NT * kPredMaxPerLane terms
+// given by a term function (see block_seq_sum_pred): the predicted-binade scan
+// with a one-lane fallback.
+template <int NT, class Term>
+__device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
+  __shared__ float s_short;
+  if (n > kPredHead) {
+    bool ok;
+    const float v = block_seq_sum_pred<NT>(term, n, &ok);
+    if (ok) return v;
+  }
+  if (threadIdx.x == 0) {
+    float s = -0.0f;
+    for (int i = 0; i < n; i++) s += term(i);
+    s_short = s;
+  }
+  __syncthreads();
+  return s_short;
+}
+
 template <int NT, bool PADDED, int CMAX = 16>
 __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
   static_assert(NT % 64 == 0 && NT <= 1024, "whole waves");
@@ -199,19 +539,22 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
   __shared__ int s_k, s_first;
   const int tid = threadIdx.x;
   if (n <= 0) return -0.0f;
-  if (PADDED && n <= kSerialMax) {
-    bool bad = false;
-    for (int j = tid; j < n; j += NT) bad |= !(a[j] <= 3.4028234663852886e38f);
-    if (__syncthreads_or(bad)) {
-      if (tid == 0) {
+  if (n <= kPredHead + NT * kPredMaxPerLane) {
+    if (n > kPredHead) {
+      bool ok;
+      const float v = block_seq_sum_pred<NT>([a](int i) { return a[i]; }, n, &ok);
+      if (ok) return v;
+    }
+    // non-finite terms, short sums and failed predictions: one lane's chain
+    if (tid == 0) {
+      if (PADDED) {
+        s_sum = lane_seq_sum_padded(a, n);
+      } else {
         float s = -0.0f;
         for (int i = 0; i < n; i++) s += a[i];
         s_sum = s;
       }
-      __syncthreads();
-      return s_sum;
     }
-    if (tid == 0) s_sum = lane_seq_sum_padded(a, n);
     __syncthreads();
     return s_sum;
   }
