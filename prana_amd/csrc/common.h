@@ -144,14 +144,28 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
-// Reductions over aligned groups of 32 lanes (one quantization block).
+// Reductions over aligned groups of 32 lanes (one quantization block), every
+// lane getting the result: within quads (DPP quad_perm), then with the
+// mirrored half-row and row partners (DPP, so each lane meets the other
+// quad / half-row), then across the two 16-lane rows. Max and integer sums
+// do not depend on the combination order.
+template <int CTRL>
+__device__ __forceinline__ int dpp_lane_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
 __device__ __forceinline__ float half_wave_max_f32(float v) {
-  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, __int_as_float(dpp_lane_mov<0xB1>(__float_as_int(v))));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, __int_as_float(dpp_lane_mov<0x4E>(__float_as_int(v))));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, __int_as_float(dpp_lane_mov<0x141>(__float_as_int(v))));  // row_half_mirror
+  v = fmaxf(v, __int_as_float(dpp_lane_mov<0x140>(__float_as_int(v))));  // row_mirror
+  return fmaxf(v, __shfl_xor(v, 16, 64));
 }
 __device__ __forceinline__ int half_wave_sum_i32(int v) {
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_lane_mov<0xB1>(v);
+  v += dpp_lane_mov<0x4E>(v);
+  v += dpp_lane_mov<0x141>(v);
+  v += dpp_lane_mov<0x140>(v);
+  return v + __shfl_xor(v, 16, 64);
 }
 
 // Quantize one 32-element activation block held one value per lane of an
@@ -175,12 +189,7 @@ template <int B>
 __device__ __forceinline__ void quantize_lanes(const float* y, int* q, float* scale, int* sum) {
   float amax[B];
 #pragma unroll
-  for (int b = 0; b < B; b++) amax[b] = fabsf(y[b]);
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) {
-#pragma unroll
-    for (int b = 0; b < B; b++) amax[b] = fmaxf(amax[b], __shfl_xor(amax[b], o, 64));
-  }
+  for (int b = 0; b < B; b++) amax[b] = half_wave_max_f32(fabsf(y[b]));
 #pragma unroll
   for (int b = 0; b < B; b++) {
     scale[b] = amax[b] > 0.0f ? amax[b] / 127.0f : 1.0f;
@@ -188,10 +197,7 @@ __device__ __forceinline__ void quantize_lanes(const float* y, int* q, float* sc
     sum[b] = q[b];
   }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) {
-#pragma unroll
-    for (int b = 0; b < B; b++) sum[b] += __shfl_xor(sum[b], o, 64);
-  }
+  for (int b = 0; b < B; b++) sum[b] = half_wave_sum_i32(sum[b]);
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) {

@@ -214,21 +214,23 @@ __device__ __forceinline__ float lane_seq_sum_padded(const float* a, int n) {
 // n terms needs run_pad(n - 1) + 1 words.
 __host__ __device__ constexpr int run_pad(int i) { return i + (i >> 4); }
 
-// Visit term(i0 + j), j = 0..nv-1, in order: f(j, value), in blocks of eight
-// fetched ahead of their use (about one fetch latency per eight terms). The
-// last block is padded with zero terms, which leave every pass below
-// unchanged, so the body needs no guards; fetches stay inside term(0..n).
+// Visit term(i0 + j), j = 0..nv-1, in order: f(j, value), in blocks of four
+// whose fetches are issued one block ahead. The last block is padded with
+// zero terms, which leave every pass below unchanged, so the body needs no
+// guards; fetches stay inside term(0..n).
 template <class Term, class F>
 __device__ __forceinline__ void for_each_run(Term a, int i0, int nv, int n, F&& f) {
-  for (int jb = 0; jb < nv; jb += 8) {
-    float t[8];
+  if (nv <= 0) return;
+  float t[4], u[4];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const float v = a(min(i0 + jb + u, n - 1));
-      t[u] = jb + u < nv ? v : 0.0f;
-    }
+  for (int k = 0; k < 4; k++) t[k] = a(min(i0 + k, n - 1));
+  for (int jb = 0; jb < nv; jb += 4) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) f(jb + u, t[u]);
+    for (int k = 0; k < 4; k++) u[k] = a(min(i0 + jb + 4 + k, n - 1));
+#pragma unroll
+    for (int k = 0; k < 4; k++) f(jb + k, jb + k < nv ? t[k] : 0.0f);
+#pragma unroll
+    for (int k = 0; k < 4; k++) t[k] = u[k];
   }
 }
 
@@ -358,30 +360,79 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   SegAcc rest{Pair{0, 0}, 0};
   Pair pre1{0, 0}, pre2{0, 0};
   {
+    // Blocks of four steps. The common block has no crossing and no tie:
+    // four symmetric increments, added at once (the increments are >= 0, so
+    // one saturating add equals four). Other blocks take the steps one by one.
     float P = P0;
-    for_each_run(a, i0, nv, n, [&](int j, float x) {
-      P += x;
-      const int e = binade_fast(P);
-      if (j == 0) {
-        ep_first = e;
-        x0 = x;
-      } else {
-        const bool cross = e != ep_last;
-        // plain selects keep the records in registers
-        const bool r1 = cross && ncross == 0, r2 = cross && ncross == 1;
-        x1 = r1 ? x : x1;
-        e1 = r1 ? e : e1;
-        pre1.e = r1 ? rest.p.e : pre1.e;
-        pre1.o = r1 ? rest.p.o : pre1.o;
-        x2 = r2 ? x : x2;
-        e2 = r2 ? e : e2;
-        pre2.e = r2 ? rest.p.e : pre2.e;
-        pre2.o = r2 ? rest.p.o : pre2.o;
-        ncross += cross ? 1 : 0;
-        seg_push(rest, cross, term_pair_fast(x, e));
+    int elast = 0;
+    float t[4], u[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) t[k] = a(min(i0 + k, n - 1));
+    for (int jb = 0; jb < nv; jb += 4) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) u[k] = a(min(i0 + jb + 4 + k, n - 1));
+      float x[4], fr[4];
+      int e[4], v[4], ii[4];
+      bool slow = false;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        x[k] = jb + k < nv ? t[k] : 0.0f;  // zero padding: no change to any state
+        P += x[k];
+        e[k] = binade_fast(P);
       }
-      ep_last = e;
-    });
+      if (jb == 0) {
+        ep_first = e[0];
+        x0 = x[0];
+        elast = e[0];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float A = ldexpf(x[k], 23 - e[k]);
+        const float I = floorf(fminf(A, 268435456.0f));
+        fr[k] = A - I;
+        ii[k] = static_cast<int>(I);
+        const bool step = !(jb == 0 && k == 0);  // step 0 is combined after the exchange
+        const int ein = k == 0 ? elast : e[k - 1];
+        slow |= step && (e[k] != ein || fr[k] == 0.5f);
+        v[k] = step ? min(ii[k] + (fr[k] > 0.5f ? 1 : 0), kCap) : 0;
+      }
+      if (slow) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          if (jb == 0 && k == 0) continue;
+          const int ein = k == 0 ? elast : e[k - 1];
+          if (e[k] != ein) {
+            // plain selects keep the records in registers
+            const bool r1 = ncross == 0, r2 = ncross == 1;
+            x1 = r1 ? x[k] : x1;
+            e1 = r1 ? e[k] : e1;
+            pre1.e = r1 ? rest.p.e : pre1.e;
+            pre1.o = r1 ? rest.p.o : pre1.o;
+            x2 = r2 ? x[k] : x2;
+            e2 = r2 ? e[k] : e2;
+            pre2.e = r2 ? rest.p.e : pre2.e;
+            pre2.o = r2 ? rest.p.o : pre2.o;
+            ncross++;
+            rest.p = Pair{0, 0};
+            rest.c++;
+          } else if (fr[k] == 0.5f) {
+            const int i = ii[k];
+            rest.p = compose(rest.p, Pair{i + (i & 1), i + 1 - (i & 1)});
+          } else {
+            rest.p.e = min(rest.p.e + v[k], kCap);
+            rest.p.o = min(rest.p.o + v[k], kCap);
+          }
+        }
+      } else {
+        const int s4 = (v[0] + v[1]) + (v[2] + v[3]);  // each <= 2^28: no overflow
+        rest.p.e = min(rest.p.e + s4, kCap);
+        rest.p.o = min(rest.p.o + s4, kCap);
+      }
+      elast = e[3];
+#pragma unroll
+      for (int k = 0; k < 4; k++) t[k] = u[k];
+    }
+    ep_last = elast;
   }
   int prev_last = wave_shr1(ep_last);
   if (lane == 63) s_epl[wave] = ep_last;

@@ -13,7 +13,6 @@
 #include <type_traits>
 
 #include "common.h"
-#include "exact_sum.h"
 #include "kernels.h"
 
 namespace prana {
@@ -228,15 +227,14 @@ __device__ __forceinline__ Acts stage_acts(int* smem, const int8_t* q, const flo
   return Acts{aw, as, am};
 }
 
-__device__ __forceinline__ float store_out(const GemvOut& o, int tok, size_t r, float acc) {
+__device__ __forceinline__ void store_out(const GemvOut& o, int tok, size_t r, float acc) {
   float* dst = o.out + (size_t)tok * o.ldo + r;
-  float v = acc;
   if (o.residual)
-    v = *dst + acc;
+    *dst = *dst + acc;
   else if (o.bias)
-    v = acc + o.bias[r];
-  *dst = v;
-  return v;
+    *dst = acc + o.bias[r];
+  else
+    *dst = acc;
 }
 
 // grid: (ceil(rows/rt), n_tok). LDS: acts + rt x (T+1) terms.
@@ -422,99 +420,10 @@ struct DecodeJob {
   int8_t* hq;
   float* hsa;
   int* hsum;
-  NormFollow nf;  // tags != nullptr: one extra workgroup (the first) runs norm_follow
 };
 
 constexpr int kDecMaxTok = 4;   // tokens per launch (LDS permitting)
 constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: one quantization block
-
-// ---- rmsnorm follower (one token)
-// The first workgroup of a residual GEMV launch computes rmsnorm (norms.rs:9-23)
-// of the rows the other workgroups produce. A producing lane publishes each
-// final row value together with the launch's epoch as one 64-bit word
-// (tags[row]); one load then tells the follower both that the row is final
-// and its value. The follower's waves poll those words a chunk of 256 rows at
-// a time and stage the values and their squares in LDS; once every row is in,
-// the workgroup folds the squares exactly in row order (the reference's
-// sequential sum) and normalises and quantizes from LDS. Producers never wait
-// on anything, so every poll ends; a spin bound still guards the loop and
-// records a give-up in status.
-constexpr int kFollowChunk = 256;
-constexpr int kFollowMaxSpins = 1 << 16;
-
-__host__ __device__ constexpr size_t follow_lds_bytes(size_t dim) {
-  return (exact::run_pad(static_cast<int>(dim)) + dim) * 4;
-}
-
-template <int NT>
-__device__ void norm_follow(const NormFollow& nf, int dim, uint8_t* sm8) {
-  const int nch = (dim + kFollowChunk - 1) / kFollowChunk;
-  float* xs = reinterpret_cast<float*>(sm8);  // row values, at exact::run_pad(row)
-  float* wl = xs + exact::run_pad(dim);       // norm weights
-  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-  for (int i = tid; i < dim; i += NT) wl[i] = nf.w[i];
-  for (int c = wave; c < nch; c += NT / 64) {
-    // All four words are (re)loaded every round, so a round costs one memory
-    // round trip; a final row never changes within the launch.
-    unsigned long long v[4];
-    for (int spins = 0;; spins++) {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        v[j] = __hip_atomic_load(nf.tags + min(c * kFollowChunk + 64 * j + lane, dim - 1), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-      bool all = true;
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        all = all && (c * kFollowChunk + 64 * j + lane >= dim || static_cast<unsigned>(v[j] >> 32) == nf.epoch);
-      if (__all(all)) break;
-      if (spins >= kFollowMaxSpins) {
-        if (nf.status && lane == 0) nf.status[0] = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int r = c * kFollowChunk + 64 * j + lane;
-      if (r < dim) xs[exact::run_pad(r)] = __uint_as_float(static_cast<unsigned>(v[j]));
-    }
-  }
-  __syncthreads();
-  // sum of squares in the reference's left-to-right order (norms.rs:15)
-  const float ss = exact::block_seq_sum_short<NT>(
-      [xs](int i) {
-        const float v = xs[exact::run_pad(i)];
-        return v * v;
-      },
-      dim);
-  // the epilogue of rmsnorm_kernel, from the staged rows
-  const float mean_sq = ss / static_cast<float>(dim);
-  const float inv = 1.0f / sqrtf(mean_sq + nf.eps);
-  // four 32-element blocks per lane group at a time (dim % 32 == 0, so every
-  // 32-lane group is either all live or all past the end)
-  for (int base = 0; base < dim; base += 4 * NT) {
-    float y[4], scale[4];
-    int qi[4], sum[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const int i = base + b * NT + tid;
-      y[b] = i < dim ? xs[exact::run_pad(i)] * inv * wl[i] : 0.0f;
-    }
-    quantize_lanes<4>(y, qi, scale, sum);
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const int i = base + b * NT + tid;
-      if (i < dim) {
-        if (nf.out) nf.out[i] = y[b];
-        nf.q[i] = static_cast<int8_t>(qi[b]);
-        if ((i & 31) == 0) {
-          nf.sa[i >> 5] = scale[b];
-          nf.sums[i >> 5] = sum[b];
-        }
-      }
-    }
-  }
-}
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
 // STAGED: more than one stage (double-buffered registers and terms);
@@ -527,16 +436,9 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   using R = RegUnit<KIND>;
   constexpr int TPU = R::kTpu;
   const int tid = threadIdx.x;
-  if constexpr (!ACT) {
-    if (job.nf.tags && blockIdx.x == 0) {  // dispatched first, so it polls while the rows are produced
-      norm_follow<NT>(job.nf, static_cast<int>(job.m[0].rows), reinterpret_cast<uint8_t*>(smem4));
-      return;
-    }
-  }
 
   int mi = 0, tile = blockIdx.x;
   if (!ACT) {
-    if (job.nf.tags) tile -= 1;  // workgroup 0 is the norm follower
     while (mi < job.n_mats - 1 && tile >= job.tiles[mi]) tile -= job.tiles[mi++];
   }
   const int rt = job.rt, SB = job.sb;
@@ -688,13 +590,7 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   }
 
   if (!ACT) {
-    if (folder) {
-      const float v = store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
-      if (job.nf.tags)
-        __hip_atomic_store(job.nf.tags + r0 + fl_lr,
-                           (static_cast<unsigned long long>(job.nf.epoch) << 32) | __float_as_uint(v),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
     return;
   }
   // act epilogue: gate lanes (row < rt) pair with up lanes (row + rt);
@@ -796,13 +692,6 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   PRANA_CHECK(K <= 16384, "gemv: decode kernel supports cols <= 16384");
   PRANA_CHECK(rows_wg * g.sb == NT * U, "gemv: tile geometry mismatch");
   PRANA_CHECK(group >= 1, "gemv: decode tile exceeds LDS");
-  size_t lds_min = 0;
-  if (job.nf.tags) {
-    PRANA_CHECK(!ACT && job.n_mats == 1 && n_tok == 1 && job.o[0].residual, "gemv: norm follower shape");
-    PRANA_CHECK(job.m[0].rows % 32 == 0 && job.m[0].rows <= kNormFollowMaxDim, "gemv: norm follower dim");
-    total += 1;
-    lds_min = follow_lds_bytes(job.m[0].rows);
-  }
   for (size_t t0 = 0; t0 < n_tok; t0 += group) {
     const size_t nt = std::min<size_t>(group, n_tok - t0);
     DecodeJob j = job;
@@ -816,14 +705,13 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
       j.hsum += t0 * H / 32;
     }
     const size_t G = K / 32;
-    const size_t lds = std::max(nt * per_tok, lds_min);
     LaunchEvents& le = launch_events();
     if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
-      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), lds, s,
+      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s,
                             le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
       le = LaunchEvents{};
     } else {
-      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), lds, s, j,
+      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s, j,
                          q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     }
     PRANA_LAUNCH_CHECK();
@@ -1016,18 +904,6 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
   });
   if (rc || in_kernel) return rc;
   return launch_quantize_acts(h, n_tok, gate.rows, hq, hsa, hsum, s);  // matmul.rs:105-127 on h
-}
-
-int launch_gemv_norm(const DevMat& m, const int8_t* q, const float* sa, const int* sums, const GemvOut& o,
-                     const NormFollow& nf, hipStream_t s) {
-  PRANA_CHECK(m.kind != kKindF32 && o.residual && nf.tags && nf.w && nf.q && nf.sa && nf.sums,
-              "gemv_norm: quantized residual GEMV with a complete norm target");
-  DecodeJob job{};
-  job.m[0] = m;
-  job.o[0] = o;
-  job.n_mats = 1;
-  job.nf = nf;
-  return dispatch_kind(m.kind, [&](auto k) { return launch_decode_t<decltype(k)::value>(job, q, sa, sums, 1, s); });
 }
 
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,

@@ -71,29 +71,6 @@ constexpr size_t kGemvDecodeMaxTokens = 16;
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s);
-// rmsnorm (norms.rs:9-23) of the rows a one-token residual GEMV writes,
-// computed inside the same launch by one extra workgroup (the first) that follows the
-// rows as they land. Every producing lane also publishes {bits(row value),
-// epoch} as one 64-bit word in tags[row]; tags holds dim words, zeroed at
-// allocation, and epoch must differ from every value a previous launch left
-// there (a per-buffer counter that skips 0). out (f32, optional), q/sa/sums:
-// the normalised row and its 32-block quantization, as launch_rmsnorm writes
-// them. status (optional) is set to 1 if the follower ever gives up waiting.
-struct NormFollow {
-  const float* w = nullptr;
-  float eps = 0.0f;
-  float* out = nullptr;
-  int8_t* q = nullptr;
-  float* sa = nullptr;
-  int* sums = nullptr;
-  unsigned long long* tags = nullptr;
-  unsigned epoch = 0;
-  int* status = nullptr;
-};
-constexpr size_t kNormFollowMaxDim = 8192;
-// m.rows == dim, o.residual set, one token, quantized kind, dim % 32 == 0.
-int launch_gemv_norm(const DevMat& m, const int8_t* q, const float* sa, const int* sums, const GemvOut& o,
-                     const NormFollow& nf, hipStream_t s);
 // Up to three quantized matrices of one kind sharing the input (fused
 // Q|K|V), one launch.
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,

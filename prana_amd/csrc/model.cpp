@@ -193,11 +193,6 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
       return rc;
     ws.cap_tok = n;
   }
-  if (!ws.norm_tags.p) {
-    if ((rc = ws.norm_tags.alloc(c.dim * 8)) || (rc = ws.status.alloc(4))) return rc;
-    PRANA_HIP(hipMemset(ws.norm_tags.p, 0, c.dim * 8));
-    PRANA_HIP(hipMemset(ws.status.p, 0, 4));
-  }
   size_t need = std::max(attention_scratch_floats(n_tok, c.n_heads, ctx_cap),
                          prefill_attn ? attention_scratch_floats(n_tok, c.n_heads, n_tok) : 0) * 4;
   if ((rc = ws.scratch.ensure(std::max<size_t>(need, 4)))) return rc;
@@ -339,38 +334,6 @@ int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint
   }
   if (out && n_steps) PRANA_HIP(hipMemcpyAsync(out, ids + 1, n_steps * 4, hipMemcpyDeviceToHost, s));
   PRANA_HIP(hipStreamSynchronize(s));
-  return check_status();
-}
-
-bool Model::can_follow(const Mat& w) const {
-  return w.d.kind != kKindF32 && w.d.rows == c.dim && c.dim % 32 == 0 && c.dim <= kNormFollowMaxDim;
-}
-
-int Model::apply_norm(const Mat& w, const GemvOut& o, const DevBuf& nw, hipStream_t s, bool hset) {
-  NormFollow nf;
-  nf.w = nw.as<float>();
-  nf.eps = c.norm_eps;
-  nf.out = ws.xb.as<float>();
-  nf.q = ws.qa.as<int8_t>();
-  nf.sa = ws.sa.as<float>();
-  nf.sums = ws.sums.as<int>();
-  nf.tags = ws.norm_tags.as<unsigned long long>();
-  if (++norm_epoch == 0) norm_epoch = 1;
-  nf.epoch = norm_epoch;
-  nf.status = ws.status.as<int>();
-  // The follower writes ws.qa only after every row is final, i.e. after each
-  // workgroup has consumed its own activations, so qa may also be the input.
-  return timed(w.stream_bytes, 1, s, [&] {
-    if (hset) return launch_gemv_norm(w.d, ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), o, nf, s);
-    return launch_gemv_norm(w.d, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), o, nf, s);
-  });
-}
-
-int Model::check_status() {
-  if (!ws.status.p) return kOk;
-  int st = 0;
-  PRANA_HIP(hipMemcpy(&st, ws.status.p, 4, hipMemcpyDeviceToHost));
-  PRANA_CHECK(st == 0, "norm follower timed out waiting for its rows (device status set)");
   return kOk;
 }
 
@@ -382,23 +345,17 @@ int Model::norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s) 
 // The layer stack shared by forward (n = 1), prefill and forward_batch.
 // mode: 0 decode (pos0 = pos), 1 prefill (f32-K/V attention over the window,
 // positions 0..n), 2 verify (cache attention at pos0..pos0+n).
-int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s, bool* final_normed) {
+int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s) {
   size_t hd = c.head_dim, q_dim = c.n_heads * hd, kv_dim = c.n_kv_heads * hd;
   float* x = ws.x.as<float>();
   const float2* tab = rope.as<float2>();
   int rc;
-  // One token: each residual GEMV (wo, down) also computes the norm that
-  // follows it, inside its own launch.
-  const bool follow = n == 1;
-  bool normed = false;  // ws.xb / ws.qa already hold the attention norm of x
-  if (final_normed) *final_normed = false;
   for (size_t l = 0; l < layers.size(); l++) {
     Layer& L = layers[l];
     uint16_t* kc = cache.k(l);
     uint16_t* vc = cache.v(l);
     // --- attention block (infer.rs:163-188)
-    if (!normed && (rc = norm_quant(x, L.vec[kRmsAtt], n, s))) return rc;
-    normed = false;
+    if ((rc = norm_quant(x, L.vec[kRmsAtt], n, s))) return rc;
     GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
     GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
     GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
@@ -431,31 +388,19 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
                                    ws.sums.as<int>(), s)))
       return rc;
     GemvOut ores{x, c.dim, nullptr, 1};
-    if (follow && can_follow(*L.w[kWo])) {
-      if ((rc = apply_norm(*L.w[kWo], ores, L.vec[kRmsFfn], s, false))) return rc;
-    } else {
-      if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
-      // --- gated MLP block (infer.rs:191-203)
-      if ((rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
-    }
+    if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
+    // --- gated MLP block (infer.rs:191-203)
+    if ((rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
     if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s))) return rc;
-    const bool last = l + 1 == layers.size();
-    const DevBuf* next = last ? (final_normed ? &rms_final : nullptr) : &layers[l + 1].vec[kRmsAtt];
-    if (follow && next && can_follow(*L.w[kW2])) {
-      if ((rc = apply_norm(*L.w[kW2], ores, *next, s, true))) return rc;
-      normed = true;
-      if (last) *final_normed = true;
-    } else {
-      if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s, true))) return rc;
-    }
+    if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s, true))) return rc;
   }
   return kOk;
 }
 
 // Model::logits / logits_batch (checkpoint.rs:239-265): final norm, then the
 // head over n rows into ws.logits.
-int Model::logits_pass(size_t n, hipStream_t s, bool normed) {
-  int rc = normed ? kOk : norm_quant(ws.x.as<float>(), rms_final, n, s);
+int Model::logits_pass(size_t n, hipStream_t s) {
+  int rc = norm_quant(ws.x.as<float>(), rms_final, n, s);
   if (rc) return rc;
   GemvOut o{ws.logits.as<float>(), c.vocab_size, nullptr, 0};
   return apply(head(), n, ws.xb.as<float>(), o, s);
@@ -482,9 +427,8 @@ int Model::forward_dev(Cache& cache, const uint32_t* host_token, const uint32_t*
     PRANA_HIP(hipMemcpyAsync(ws.tokens.p, host_token, 4, hipMemcpyHostToDevice, s));
   }
   if ((rc = embed_tokens(dev_token ? dev_token : ws.tokens.as<uint32_t>(), 1, s))) return rc;
-  bool normed = false;
-  if ((rc = layers_pass(cache, 1, pos, 0, s, need_logits ? &normed : nullptr))) return rc;
-  if (need_logits && (rc = logits_pass(1, s, normed))) return rc;
+  if ((rc = layers_pass(cache, 1, pos, 0, s))) return rc;
+  if (need_logits && (rc = logits_pass(1, s))) return rc;
   return kOk;
 }
 
@@ -495,7 +439,7 @@ int Model::forward(Cache& cache, uint32_t token, size_t pos, bool need_logits, f
   if (need_logits && logits_host)
     PRANA_HIP(hipMemcpyAsync(logits_host, ws.logits.p, c.vocab_size * 4, hipMemcpyDeviceToHost, s));
   PRANA_HIP(hipStreamSynchronize(s));
-  return check_status();
+  return kOk;
 }
 
 int Model::batch_dev(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, int mode, hipStream_t s) {
@@ -582,7 +526,6 @@ int Model::generate(const uint32_t* prompt, size_t p, size_t steps, const uint32
     token = next;
   }
   PRANA_HIP(hipStreamSynchronize(s));
-  if ((rc = check_status())) return rc;
   double t2 = now_s();
   if (n_out) *n_out = generated;
   if (st) {
@@ -656,7 +599,6 @@ int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, si
       if (i == budget || tn != drafts[i]) break;
     }
   }
-  if ((rc = target.check_status()) || (rc = draft.check_status())) return rc;
   double t2 = now_s();
   if (n_out) *n_out = generated;
   if (st) {

@@ -40,8 +40,6 @@ struct Workspace {
   DevBuf scratch;       // attention scores
   DevBuf tokens, argmax;
   DevBuf stream_out;  // device-side token stream of decode()
-  DevBuf norm_tags;   // [dim] {row bits, epoch} words of the rmsnorm follower (zeroed once)
-  DevBuf status;      // int: set on the device if a norm follower gave up waiting
 };
 
 // Optional per-launch timing of the model's GEMVs (HIP events on the stream
@@ -80,7 +78,6 @@ struct Model {
   DevBuf rope;                // float2 [seq_len][head_dim/2] (cos, sin)
   bool finalized = false;
   Workspace ws;
-  unsigned norm_epoch = 0;  // last epoch handed to a norm follower (never 0)
 
   int set_tensor(const std::string& name, int ggml_type, const uint64_t* dims, int n_dims, const void* bytes,
                  size_t nbytes);
@@ -101,17 +98,9 @@ struct Model {
   template <class F>
   int timed(size_t bytes, size_t n, hipStream_t s, F&& launch);
   int norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s);
-  // One-token residual GEMV x += w * acts whose launch also computes
-  // rmsnorm(x) with weights nw into ws.xb and ws.qa/sa/sums (what norm_quant
-  // writes). can_follow: w's shape and kind allow it.
-  bool can_follow(const Mat& w) const;
-  int apply_norm(const Mat& w, const GemvOut& o, const DevBuf& nw, hipStream_t s, bool hset);
-  int check_status();
   int embed_tokens(const uint32_t* dev_ids, size_t n, hipStream_t s);
-  // final_normed != nullptr (one token): the last layer's down projection may
-  // also apply the final norm; *final_normed tells whether it did.
-  int layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s, bool* final_normed = nullptr);
-  int logits_pass(size_t n, hipStream_t s, bool normed = false);
+  int layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_t s);
+  int logits_pass(size_t n, hipStream_t s);
 
   // The token comes from host_token when given, else from dev_token (a
   // device id), else from ws.tokens[0].
