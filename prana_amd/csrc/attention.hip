@@ -92,6 +92,11 @@ struct HeadJob {
   float* dst;        // output row (n_heads*hd)
   float* gscores;    // global scratch of >= pos+1 floats (used beyond kScoreLds)
   bool vec;          // 16-byte aligned rows: V streams through LDS chunks
+  // optional: the output row quantized in 32-element blocks (quantize_acts,
+  // matmul.rs:105-127) for the next projection; set only when dw % 32 == 0
+  int8_t* qd;
+  float* qsa;
+  int* qsum;
 };
 
 struct Lds {
@@ -244,6 +249,17 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
     for (int t = 0; t < n; t++) acc += sc[t] * Elem<F16>::get(vb[(size_t)t * J.kv_stride]);
   }
   if (folder) J.dst[J.h * J.hd + J.d0 + d] = acc;
+  if (J.qd && folder) {  // the folders are whole 32-lane groups here
+    float scale;
+    int sum;
+    const int qi = quantize_lane(acc, &scale, &sum);
+    const int gi = J.h * J.hd + J.d0 + d;
+    J.qd[gi] = static_cast<int8_t>(qi);
+    if ((gi & 31) == 0) {
+      J.qsa[gi >> 5] = scale;
+      J.qsum[gi >> 5] = sum;
+    }
+  }
 }
 
 template <bool F16>
@@ -271,7 +287,8 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
                                                    const void* __restrict__ v, int pos0,
                                                    const int* __restrict__ pos_dev, int n_heads, int group, int hd,
                                                    int dsplit, float* __restrict__ out, float* __restrict__ scratch,
-                                                   int scratch_stride, int mode) {
+                                                   int scratch_stride, int mode, int8_t* __restrict__ qd,
+                                                   float* __restrict__ qsa, int* __restrict__ qsum) {
   __shared__ float s_q[256];
   __shared__ float s_red[kNT / 64];
   __shared__ __align__(16) float s_scores[exact::lane_pad(kScoreLds)];
@@ -293,6 +310,10 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
   J.dst = out + (size_t)i * n_heads * hd;
   J.gscores = scratch ? scratch + ((size_t)i * n_heads * dsplit + lb) * scratch_stride : nullptr;
   J.vec = mode != 0;
+  const size_t row_len = (size_t)n_heads * hd;
+  J.qd = qd ? qd + i * row_len : nullptr;
+  J.qsa = qd ? qsa + i * row_len / 32 : nullptr;
+  J.qsum = qd ? qsum + i * row_len / 32 : nullptr;
   Lds L{s_q, s_red, s_scores, s_prod};
   one_head<F16>(J, mode, L);
 }
@@ -300,7 +321,7 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
 template <bool F16>
 int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const int* pos_dev, size_t n_q,
                 size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
-                hipStream_t s) {
+                const ActQuant* aq, bool* quantized, hipStream_t s) {
   const size_t elem = F16 ? 2 : 4;
   const bool aligned = reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                        (hd * elem) % 16 == 0;
@@ -312,8 +333,12 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
   const int ds = attention_dim_slices(n_q, n_heads, hd, elem, aligned);
   PRANA_CHECK(ctx_cap <= static_cast<size_t>(kScoreLds) || scratch != nullptr,
               "attention: contexts beyond 4096 positions need score scratch");
+  // fused quantization needs every workgroup's dims to be whole 32-blocks
+  const bool fuse_q = aq && aq->q && (hd / ds) % 32 == 0;
+  if (quantized) *quantized = fuse_q;
   hipLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, q, k, v, (int)pos0, pos_dev,
-                     (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode);
+                     (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode,
+                     fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -339,21 +364,23 @@ size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap) {
 
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
-                           const int* pos_dev, hipStream_t s) {
+                           const int* pos_dev, hipStream_t s, const ActQuant* aq, bool* quantized) {
   if (n_q == 0) return kOk;
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "attention: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
   if (ctx_cap == 0) ctx_cap = pos0 + n_q;
   PRANA_CHECK(pos_dev || pos0 + n_q <= ctx_cap, "attention: scratch capacity below pos0 + n_q");
-  return launch_attn<true>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, hd, out, scratch, ctx_cap, s);
+  return launch_attn<true>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, hd, out, scratch, ctx_cap, aq, quantized,
+                           s);
 }
 
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
-                             size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s) {
+                             size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s,
+                             const ActQuant* aq, bool* quantized) {
   if (seq == 0) return kOk;
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "attention: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
-  return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, s);
+  return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, aq, quantized, s);
 }
 
 }  // namespace prana

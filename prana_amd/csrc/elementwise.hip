@@ -365,47 +365,55 @@ int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s) {
 // ---------------------------------------------------------------- argmax
 // infer.rs:560-568: strict `>` scan, first max wins. A NaN at index 0 pins the
 // result to 0; later NaNs never win. Parallel form: per-lane strided scans
-// (increasing index, strict >), then a (value, lowest index) reduction.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ v, int n, uint32_t* __restrict__ out) {
-  __shared__ float s_v[256];
-  __shared__ int s_i[256];
+// (increasing index, strict >, sixteen loads in flight per lane), then a
+// (value, lowest index) reduction across the workgroup.
+constexpr int kArgNT = 1024;
+
+__device__ __forceinline__ void argmax_merge(float& av, int& aj, float bv, int bj, int n) {
+  if (bj < n && (aj >= n || bv > av || (bv == av && bj < aj))) {
+    av = bv;
+    aj = bj;
+  }
+}
+
+__global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict__ v, int n, uint32_t* __restrict__ out) {
+  __shared__ float s_v[kArgNT / 64];
+  __shared__ int s_i[kArgNT / 64];
   const float* row = v + (size_t)blockIdx.x * n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float best = -INFINITY;
   int bi = n;  // none
-  for (int i = threadIdx.x; i < n; i += 256) {
-    float x = row[i];
-    if (x > best) {
-      best = x;
-      bi = i;
-    }
-  }
-  s_v[threadIdx.x] = best;
-  s_i[threadIdx.x] = bi;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o) {
-      float bv = s_v[threadIdx.x + o];
-      int bj = s_i[threadIdx.x + o];
-      float av = s_v[threadIdx.x];
-      int aj = s_i[threadIdx.x];
-      if (bj < n && (aj >= n || bv > av || (bv == av && bj < aj))) {
-        s_v[threadIdx.x] = bv;
-        s_i[threadIdx.x] = bj;
+  for (int base = 0; base < n; base += 16 * kArgNT) {
+    float x[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) x[u] = row[min(base + u * kArgNT + tid, n - 1)];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+      const int i = base + u * kArgNT + tid;
+      if (i < n && x[u] > best) {
+        best = x[u];
+        bi = i;
       }
     }
-    __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    int r = s_i[0];
-    if (r >= n || row[0] != row[0]) r = 0;  // all -inf / NaN at index 0
-    out[blockIdx.x] = static_cast<uint32_t>(r);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) argmax_merge(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64), n);
+  if (lane == 0) {
+    s_v[wave] = best;
+    s_i[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgNT / 64; w++) argmax_merge(best, bi, s_v[w], s_i[w], n);
+    if (bi >= n || row[0] != row[0]) bi = 0;  // all -inf / NaN, or a NaN at index 0
+    out[blockIdx.x] = static_cast<uint32_t>(bi);
   }
 }
 
 int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStream_t s) {
   if (rows == 0) return kOk;
-  PRANA_CHECK(n > 0, "argmax: empty row");
-  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, v, (int)n, out);
+  PRANA_CHECK(n > 0 && n <= 0x7fffffff, "argmax: row length out of range");
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(kArgNT), 0, s, v, (int)n, out);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }

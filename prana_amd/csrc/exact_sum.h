@@ -275,6 +275,16 @@ __device__ __forceinline__ T wave_scan_incl(T x, Get get, Op op) {
   x = op(get([](int v) { return dpp_src<0x143, 0xc>(v); }, x), x);
   return x;
 }
+// The same inside each 16-lane row only (enough for the per-wave totals of
+// a workgroup of up to 16 waves).
+template <class T, class Get, class Op>
+__device__ __forceinline__ T row_scan_incl(T x, Get get, Op op) {
+  x = op(get([](int v) { return dpp_src<0x111, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x112, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x114, 0xf>(v); }, x), x);
+  x = op(get([](int v) { return dpp_src<0x118, 0xf>(v); }, x), x);
+  return x;
+}
 // The value of the previous lane (lane 0: all-zero bits).
 __device__ __forceinline__ int wave_shr1(int v) { return dpp_src<0x138, 0xf>(v); }
 
@@ -285,6 +295,16 @@ __device__ __forceinline__ float scan_add_f32(float x) {
 }
 __device__ __forceinline__ SegAcc scan_seg(SegAcc x) {
   return wave_scan_incl(
+      x, [](auto mv, SegAcc v) { return SegAcc{Pair{mv(v.p.e), mv(v.p.o)}, mv(v.c)}; },
+      [](SegAcc a, SegAcc b) { return seg_combine(a, b); });
+}
+__device__ __forceinline__ float row_scan_add_f32(float x) {
+  return row_scan_incl(
+      x, [](auto mv, float v) { return __int_as_float(mv(__float_as_int(v))); },
+      [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ SegAcc row_scan_seg(SegAcc x) {
+  return row_scan_incl(
       x, [](auto mv, SegAcc v) { return SegAcc{Pair{mv(v.p.e), mv(v.p.o)}, mv(v.c)}; },
       [](SegAcc a, SegAcc b) { return seg_combine(a, b); });
 }
@@ -344,10 +364,10 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
     *ok = false;
     return 0.0f;
   }
-  float pre = 0.0f;
-#pragma unroll
-  for (int w = 0; w < W; w++)
-    if (w < wave) pre += s_fw[w];
+  static_assert(W <= 16, "wave totals are scanned inside one 16-lane row");
+  // every wave scans the wave totals in its first row and picks its prefix
+  const float tw = row_scan_add_f32(lane < W ? s_fw[lane] : 0.0f);
+  const float pre = wave > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), wave - 1)) : 0.0f;
   const float sH = s_head;
   const float P0 = sH + (pre + __int_as_float(wave_shr1(__float_as_int(inc))));
   // pass 2: the predicted result binade of every owned step (P is recomputed
@@ -454,12 +474,16 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   if (lane == 0) s_epf[wave] = ep_first;
   __syncthreads();
   if (lane == 63) next_first = wave + 1 < W ? s_epf[wave + 1] : 0;
-  SegAcc run{Pair{0, 0}, 0}, all{Pair{0, 0}, 0};
-#pragma unroll
-  for (int w = 0; w < W; w++) {
-    const SegAcc t{Pair{s_sw[3 * w], s_sw[3 * w + 1]}, s_sw[3 * w + 2]};
-    if (w < wave) run = seg_combine(run, t);
-    all = seg_combine(all, t);
+  SegAcc run{Pair{0, 0}, 0}, all;
+  {
+    const SegAcc tw = row_scan_seg(lane < W ? SegAcc{Pair{s_sw[3 * lane], s_sw[3 * lane + 1]}, s_sw[3 * lane + 2]}
+                                            : SegAcc{Pair{0, 0}, 0});
+    auto pick = [&](int w) {
+      return SegAcc{Pair{__builtin_amdgcn_readlane(tw.p.e, w), __builtin_amdgcn_readlane(tw.p.o, w)},
+                    __builtin_amdgcn_readlane(tw.c, w)};
+    };
+    if (wave > 0) run = pick(wave - 1);
+    all = pick(W - 1);
   }
   run = seg_combine(run, SegAcc{Pair{wave_shr1(incs.p.e), wave_shr1(incs.p.o)}, wave_shr1(incs.c)});
   // pass 3: segment totals and crossing terms, indexed by segment, from the

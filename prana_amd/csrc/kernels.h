@@ -91,9 +91,19 @@ size_t terms_per_row(const DevMat& m);
 // non-null). scratch >= attention_scratch_floats(n_q, n_heads, ctx_cap)
 // floats (none up to 4096 positions), ctx_cap >= pos0+n_q (0 = exactly
 // pos0+n_q).
+// Optional quantized copy of an attention output (quantize_acts layout, one
+// row of n_heads*hd per query). The launchers fill it in the same pass when
+// every workgroup's output dims are whole 32-element blocks and report that
+// through *quantized; otherwise the caller quantizes.
+struct ActQuant {
+  int8_t* q;
+  float* sa;
+  int* sums;
+};
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
-                           const int* pos_dev, hipStream_t s);
+                           const int* pos_dev, hipStream_t s, const ActQuant* aq = nullptr,
+                           bool* quantized = nullptr);
 // attention (prefill, attention.rs:236-284) over f32 K/V of the window.
 // scratch >= attention_scratch_floats(seq, n_heads, seq) floats.
 // Score scratch a launch needs (probabilities beyond 4096 positions spill
@@ -101,6 +111,7 @@ int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* v
 size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap);
 int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, bool aligned);
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
-                             size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s);
+                             size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s,
+                             const ActQuant* aq = nullptr, bool* quantized = nullptr);
 
 }  // namespace prana

@@ -364,12 +364,15 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
       const GemvOut o[3] = {oq, ok, ov};
       if ((rc = apply_multi(w, o, 3, n, ws.xb.as<float>(), s))) return rc;
     }
+    const ActQuant aq{ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>()};
+    bool quantized = false;
     if (mode == 0) {
       if ((rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd, tab,
                                c.rope_neox, kc, vc, nullptr, pos0, s)))
         return rc;
       if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
-                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s)))
+                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s, &aq,
+                                       &quantized)))
         return rc;
     } else {
       if ((rc = launch_rope(ws.q.as<float>(), n, q_dim, q_dim, hd, tab, pos0, c.rope_neox, s))) return rc;
@@ -378,14 +381,16 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
       if ((rc = launch_kv_write(vc, pos0, kv_dim, ws.v.as<float>(), n * kv_dim, s))) return rc;
       if (mode == 1)
         rc = launch_attention_prefill(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, c.n_heads,
-                                      c.n_kv_heads, hd, ws.attn.as<float>(), ws.scratch.as<float>(), s);
+                                      c.n_kv_heads, hd, ws.attn.as<float>(), ws.scratch.as<float>(), s, &aq,
+                                      &quantized);
       else
         rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, n, c.n_heads, c.n_kv_heads, hd,
-                                    ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s);
+                                    ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s, &aq,
+                                    &quantized);
       if (rc) return rc;
     }
-    if ((rc = launch_quantize_acts(ws.attn.as<float>(), n, q_dim, ws.qa.as<int8_t>(), ws.sa.as<float>(),
-                                   ws.sums.as<int>(), s)))
+    if (!quantized && (rc = launch_quantize_acts(ws.attn.as<float>(), n, q_dim, ws.qa.as<int8_t>(),
+                                                 ws.sa.as<float>(), ws.sums.as<int>(), s)))
       return rc;
     GemvOut ores{x, c.dim, nullptr, 1};
     if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;

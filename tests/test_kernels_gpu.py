@@ -342,5 +342,6 @@ def test_argmax_semantics():
         assert P.argmax(r)[0] == O.argmax(r), r
     big = rng(2).standard_normal((5, 151936)).astype(np.float32)
     big[3, 1000] = big[3, 2000] = 100.0
+    big[4, 10] = big[4, 10 + 1024] = 100.0                      # tie inside one lane's stride
     got = P.argmax(big)
     assert [int(v) for v in got] == [O.argmax(b) for b in big]
