@@ -116,6 +116,12 @@ int prana_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float
 /* silu in place (norms.rs:27-31); gelu_tanh in place (norms.rs:35-41). */
 int prana_silu(float *x, size_t n, prana_stream_t stream);
 int prana_gelu_tanh(float *x, size_t n, prana_stream_t stream);
+/* The gated-MLP step of forward_impl (infer.rs:193-199): g = act(g) * u
+ * elementwise over n values, act = silu / gelu_tanh. */
+int prana_silu_mul(float *g, const float *u, size_t n, prana_stream_t stream);
+int prana_gelu_tanh_mul(float *g, const float *u, size_t n, prana_stream_t stream);
+/* add_bias (infer.rs:73-79) on each of `rows` rows of n: x[r*n + i] += bias[i]. */
+int prana_add_bias(float *x, const float *bias, size_t rows, size_t n, prana_stream_t stream);
 /* softmax (norms.rs:44-56) over each of `rows` rows of n. */
 int prana_softmax(const float *in, size_t rows, size_t n, float *out, prana_stream_t stream);
 /* rope_interleaved (attention.rs:90-101) / rope_neox (107-121) in place on

@@ -194,6 +194,27 @@ def gelu_tanh(x):
     return _inplace(load().prana_gelu_tanh, x)
 
 
+def act_mul(g, u, gelu=False):
+    """g = act(g) * u (infer.rs:193-199), act = silu or gelu_tanh."""
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    assert g.shape == u.shape
+    dg, du = DeviceArray.from_host(g), DeviceArray.from_host(u)
+    fn = load().prana_gelu_tanh_mul if gelu else load().prana_silu_mul
+    check(fn(dg.ptr, du.ptr, g.size, None))
+    return dg.to_host()
+
+
+def add_bias(x, bias):
+    """add_bias (infer.rs:73-79) on every row of x."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    b = np.ascontiguousarray(bias, np.float32)
+    assert b.shape == (x.shape[1],)
+    dx, db = DeviceArray.from_host(x), DeviceArray.from_host(b)
+    check(load().prana_add_bias(dx.ptr, db.ptr, x.shape[0], x.shape[1], None))
+    return dx.to_host()
+
+
 def softmax(x):
     x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
     d, o = DeviceArray.from_host(x), DeviceArray(x.shape, np.float32)

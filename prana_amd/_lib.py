@@ -64,6 +64,9 @@ _SIGS = {
     "prana_rmsnorm": (c_int, [c_void_p, c_void_p, c_size, c_size, c_float, c_void_p, c_void_p]),
     "prana_silu": (c_int, [c_void_p, c_size, c_void_p]),
     "prana_gelu_tanh": (c_int, [c_void_p, c_size, c_void_p]),
+    "prana_silu_mul": (c_int, [c_void_p, c_void_p, c_size, c_void_p]),
+    "prana_gelu_tanh_mul": (c_int, [c_void_p, c_void_p, c_size, c_void_p]),
+    "prana_add_bias": (c_int, [c_void_p, c_void_p, c_size, c_size, c_void_p]),
     "prana_softmax": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p]),
     "prana_rope_interleaved": (c_int, [c_void_p, c_size, c_size, c_size, c_size, c_float, c_void_p]),
     "prana_rope_neox": (c_int, [c_void_p, c_size, c_size, c_size, c_size, c_float, c_void_p]),

@@ -258,6 +258,30 @@ int prana_gelu_tanh(float* x, size_t n, prana_stream_t stream) {
   });
 }
 
+int prana_silu_mul(float* g, const float* u, size_t n, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && u, "silu_mul: null buffer");
+    return launch_act_mul(g, u, n, 0, nullptr, nullptr, nullptr, pick_stream(stream));
+  });
+}
+
+int prana_gelu_tanh_mul(float* g, const float* u, size_t n, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && u, "gelu_tanh_mul: null buffer");
+    return launch_act_mul(g, u, n, 1, nullptr, nullptr, nullptr, pick_stream(stream));
+  });
+}
+
+int prana_add_bias(float* x, const float* bias, size_t rows, size_t n, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(x && bias && n > 0, "add_bias: null buffer or empty row");
+    return launch_add(x, bias, rows * n, n, pick_stream(stream));
+  });
+}
+
 int prana_softmax(const float* in, size_t rows, size_t n, float* out, prana_stream_t stream) {
   return guard([&] {
     INIT_OR_RETURN();

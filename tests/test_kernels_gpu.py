@@ -207,6 +207,17 @@ def test_expf_exhaustive():
         dx.free()
 
 
+def test_act_mul_and_add_bias():
+    # g = silu(g) * u and x += bias: the oracle's silu, then one IEEE f32
+    # multiply / add per element (numpy float32 arithmetic rounds the same way)
+    g = rng(31).standard_normal(14336 + 7).astype(np.float32) * 4
+    u = rng(32).standard_normal(g.size).astype(np.float32)
+    assert same_bits(P.act_mul(g, u), O.silu(g) * u)
+    x = rng(33).standard_normal((5, 896)).astype(np.float32)
+    b = rng(34).standard_normal(896).astype(np.float32)
+    assert same_bits(P.add_bias(x, b), x + b[None, :])
+
+
 def test_gelu_tanh_tolerance():
     # gelu_tanh is Gemma-only; device tanhf vs glibc tanhf is the libm
     # boundary, so this is a tolerance check (1e-6 relative + 1e-7).
