@@ -813,6 +813,110 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(DevMat m, const float* __
   }
 }
 
+// ===================================================================
+// Batched matmul on the int8 matrix cores (prefill / verify, N > 16 tokens).
+//
+// One v_mfma_i32_32x32x16_i8 pair gives the exact i32 block dots of one
+// 32-element block for a 32-token x 32-row tile; the f32 term of each
+// (token, row) is then formed with the decode kernels' expression and added
+// to that output's accumulator, block after block, so every output is the
+// same left-to-right fold as in the decode path (bitwise equal per element,
+// as matmul_q8_prefill / matmul_kquant_prefill are to their decode forms).
+// Lane layout (checked on the device): A[i][k] i = lane%32, k = 8*(lane/32)
+// + byte; B[k][j] j = lane%32; D[i][j] j = lane%32, i = 8*(v/4) +
+// 4*(lane/32) + v%4 for the 16 values v of a lane.
+// A = activations (i = token), B = weights (j = row): each lane owns one
+// weight row and sixteen tokens of its wave's tile.
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+constexpr int kMmaRows = 128;  // weight rows per workgroup (32 per wave)
+constexpr int kMmaToks = 32;   // tokens per workgroup
+
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ sa, const int* __restrict__ sums,
+                                                        int n_tok, GemvOut o) {
+  static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
+  constexpr int kChunk = 32;  // blocks whose activation scales / sums are staged at a time
+  __shared__ __align__(16) float s_sa[kChunk][kMmaToks];
+  __shared__ __align__(16) int s_sm[kChunk][kMmaToks];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
+  const int K = static_cast<int>(m.cols), G = K / 32;
+  const int R = static_cast<int>(m.rows);
+  const int n_row = blockIdx.x * kMmaRows + wave * 32 + (lane & 31);  // this lane's weight row (B column)
+  const int row = min(n_row, R - 1);
+  const int m0 = blockIdx.y * kMmaToks;
+  const int tok_a = min(m0 + (lane & 31), n_tok - 1);  // this lane's A row
+  const int8_t* qa = q + (size_t)tok_a * K + 8 * h;
+  float acc[16];
+#pragma unroll
+  for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+  for (int b0 = 0; b0 < G; b0 += kChunk) {
+    // stage the tile's per-block activation scales and sums, [block][token]
+    __syncthreads();  // the previous chunk has been read
+    for (int e = threadIdx.x; e < kChunk * kMmaToks; e += 256) {
+      const int tt = e / kChunk, bb = e % kChunk;  // consecutive lanes: consecutive blocks of one token
+      const size_t gi = (size_t)min(m0 + tt, n_tok - 1) * G + min(b0 + bb, G - 1);
+      s_sa[bb][tt] = sa[gi];
+      s_sm[bb][tt] = sums[gi];
+    }
+    __syncthreads();
+    const int cb = min(kChunk, G - b0);
+    for (int bb = 0; bb < cb; bb++) {
+      const int b = b0 + bb;
+      const long a1 = *reinterpret_cast<const long*>(qa + 32 * b);
+      const long a2 = *reinterpret_cast<const long*>(qa + 32 * b + 16);
+      long b1, b2;
+      float d;
+      if constexpr (KIND == kKindQ4_0) {
+        const long w = *reinterpret_cast<const long*>(m.qs + ((size_t)row * G + b) * 16 + 8 * h);
+        b1 = w & 0x0F0F0F0F0F0F0F0FL;
+        b2 = (w >> 4) & 0x0F0F0F0F0F0F0F0FL;
+        d = ld_f16(m.sc, (size_t)row * G + b);
+      } else {
+        const int8_t* wr = reinterpret_cast<const int8_t*>(m.qs) + (size_t)row * K + 32 * b + 8 * h;
+        b1 = *reinterpret_cast<const long*>(wr);
+        b2 = *reinterpret_cast<const long*>(wr + 16);
+        d = KIND == kKindQ8F ? reinterpret_cast<const float*>(m.sc)[(size_t)row * G + b]
+                             : ld_f16(m.sc, (size_t)row * G + b);
+      }
+      v16i_t c = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a2, b2, c, 0, 0, 0);
+#pragma unroll
+      for (int g = 0; g < 4; g++) {  // tokens 8g + 4h + e of the tile hold values v = 4g + e
+        const float4 s4 = *reinterpret_cast<const float4*>(&s_sa[bb][8 * g + 4 * h]);
+        const int4 m4 = *reinterpret_cast<const int4*>(&s_sm[bb][8 * g + 4 * h]);
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        const int mv[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          int isum = c[4 * g + e];
+          if constexpr (KIND == kKindQ4_0) isum -= 8 * mv[e];
+          acc[4 * g + e] += d * sv[e] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
+        }
+      }
+    }
+  }
+  if (n_row < R) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int t = m0 + 8 * (v / 4) + 4 * h + (v % 4);
+      if (t < n_tok) store_out(o, t, n_row, acc[v]);
+    }
+  }
+}
+
+template <int KIND>
+int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                     const GemvOut& o, hipStream_t s) {
+  PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30), "gemm: shape out of range");
+  dim3 grid((m.rows + kMmaRows - 1) / kMmaRows, (n_tok + kMmaToks - 1) / kMmaToks);
+  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), 0, s, m, q, sa, sums, (int)n_tok, o);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 template <int KIND>
 int launch_q(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok, const GemvOut& o,
              hipStream_t s) {
@@ -924,9 +1028,9 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
       PRANA_LAUNCH_CHECK();
       return kOk;
     }
-    case kKindQ8F: return launch_q<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ8_0: return launch_q<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ4_0: return launch_q<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
     case kKindQ4_K: return launch_q<kKindQ4_K>(m, q, sa, sums, n_tok, o, s);
     case kKindQ6_K: return launch_q<kKindQ6_K>(m, q, sa, sums, n_tok, o, s);
   }
