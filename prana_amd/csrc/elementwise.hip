@@ -43,16 +43,19 @@ int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, flo
 
 // ---------------------------------------------------------------- rmsnorm
 // norms.rs:9-23: ms = (sum_seq x*x)/dim; inv = 1/sqrt(ms+eps); y = (x*inv)*w.
-// One 1024-lane workgroup per row. The sum of squares is the reference's
+// One workgroup per row: 1024 lanes for long rows, 256 for rows up to
+// kNormSmallDim (the exact scan's fixed costs grow with the wave count, its
+// per-term work shrinks with it). The sum of squares is the reference's
 // left-to-right fold from -0.0, evaluated exactly by the whole workgroup; the
 // normalise + optional quantize is parallel.
-constexpr int kNormNT = 1024;
 constexpr int kNormMaxDim = 16320;  // row and weights staged in LDS (about 132 KB)
+constexpr int kNormSmallDim = 2048;
+template <int kNormNT>
 __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                           int dim, float eps, float* __restrict__ out,
                                                           int8_t* __restrict__ q, float* __restrict__ sa,
                                                           int* __restrict__ sums) {
-  constexpr int kPer = (kNormMaxDim + kNormNT - 1) / kNormNT;
+  constexpr int kPer = ((kNormNT == 1024 ? kNormMaxDim : kNormSmallDim) + kNormNT - 1) / kNormNT;
   extern __shared__ float4 smem_n4[];
   float* xs = reinterpret_cast<float*>(smem_n4);  // the row, at exact::run_pad(i)
   float* wl = xs + exact::run_pad(dim);           // the weights
@@ -124,7 +127,10 @@ int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, floa
   PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
   PRANA_CHECK(dim >= 1 && dim <= static_cast<size_t>(kNormMaxDim), "rmsnorm: dim must be in 1..=16320");
   const size_t lds = (exact::run_pad(static_cast<int>(dim)) + dim) * 4;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormNT), lds, s, x, w, (int)dim, eps, out, q, sa, sums);
+  if (dim <= static_cast<size_t>(kNormSmallDim))
+    hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(rows), dim3(256), lds, s, x, w, (int)dim, eps, out, q, sa, sums);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<1024>, dim3(rows), dim3(1024), lds, s, x, w, (int)dim, eps, out, q, sa, sums);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }

@@ -1,0 +1,140 @@
+#!/usr/bin/env python3
+"""Kernel microbenchmarks for the configurations beside the headline decode.
+
+C1: the Q8_0 matmul sweep (R x K in {4096x4096, 14336x4096, 4096x14336,
+32000x4096}, N in {1, 4, 16, 64} tokens). Weight copies rotate so that the
+bytes touched per case exceed twice the 256 MB MALL.
+C3: attention over an f16 cache (32 query / 8 KV heads, head_dim 128) at
+contexts 1024, 4096, 16384 and 32768, for one query row (decode) and for
+eight query rows over one cache (the verify form).
+
+Timing comes from a rocprofv3 kernel trace, so there is no host overhead in
+the figures. Run
+
+    rocprofv3 --kernel-trace -d OUT -o run -- python3 -m prana_amd.microbench
+    python3 -m prana_amd.microbench --summarize OUT/.../run_results.db
+
+The run writes a case manifest (JSON). In the trace, each case is bracketed
+by small fill-kernel markers: one before its warmup calls, one before its
+timed calls and one after them, so set-up work (uploads, repacking) never
+lands in a timed group. The summary sums every non-runtime kernel between
+the second and third marker of a case, activation quantization included.
+"""
+import argparse
+import json
+import os
+import sqlite3
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+Q8_0 = 8
+MALL = 256 << 20
+C1_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]
+C1_TOKENS = [1, 4, 16, 64]
+C3_CTX = [1024, 4096, 16384, 32768]
+WARMUP, TIMED = 3, 20
+
+
+def _marker(P, buf):
+    P.check(P.load().prana_memset_d(buf.ptr, 0, 256))
+
+
+def run(manifest_path):
+    import prana_amd as P
+
+    P.init()
+    marker = P.DeviceArray((256,), np.uint8)
+    cases = []
+    rng = np.random.default_rng(0)
+
+    for rows, cols in C1_SHAPES:
+        raw = P.synth_tensor(Q8_0, rows, cols, rows * 7 + cols, 0.02)
+        copies = max(3, -(-2 * MALL // raw.nbytes))
+        mats = [P.Matrix(Q8_0, rows, cols, raw) for _ in range(copies)]
+        print(f"C1 Q8_0 {rows}x{cols}: {copies} copies", file=sys.stderr, flush=True)
+        for n in C1_TOKENS:
+            x = P.DeviceArray.from_host(rng.standard_normal((n, cols)).astype(np.float32))
+            out = P.DeviceArray((n, rows), np.float32)
+            for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
+                _marker(P, marker)
+                for i in range(calls):
+                    P.check(P.load().prana_matmul(mats[i % copies].h, x.ptr, n, out.ptr, None))
+            _marker(P, marker)
+            P.check(P.load().prana_synchronize())
+            cases.append({"config": "C1", "case": f"Q8_0 {rows}x{cols} N={n}", "calls": TIMED,
+                          "bytes": rows * cols // 32 * 34 + n * cols * 4 + n * rows * 4, "copies": copies})
+        del mats
+
+    nh, nkv, hd = 32, 8, 128
+    kv = nkv * hd
+    for ctx in C3_CTX:
+        print(f"C3 ctx={ctx}", file=sys.stderr, flush=True)
+        for b in (1, 8):
+            rows = ctx + b
+            k = P.DeviceArray.from_host(rng.standard_normal(rows * kv).astype(np.float16).view(np.uint16))
+            v = P.DeviceArray.from_host(rng.standard_normal(rows * kv).astype(np.float16).view(np.uint16))
+            q = P.DeviceArray.from_host(rng.standard_normal(b * nh * hd).astype(np.float32))
+            out = P.DeviceArray((b * nh * hd,), np.float32)
+            for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
+                _marker(P, marker)
+                for _ in range(calls):
+                    if b == 1:
+                        rc = P.load().prana_attention_decode(q.ptr, k.ptr, v.ptr, ctx, nh, nkv, hd, out.ptr, None)
+                    else:
+                        rc = P.load().prana_attention_verify(q.ptr, k.ptr, v.ptr, ctx, b, nh, nkv, hd, out.ptr, None)
+                    P.check(rc)
+            _marker(P, marker)
+            P.check(P.load().prana_synchronize())
+            form = "decode" if b == 1 else f"{b} query rows at ctx..ctx+{b - 1} (verify form)"
+            cases.append({"config": "C3", "case": f"ctx={ctx} {form}", "calls": TIMED,
+                          "bytes": 2 * rows * kv * 2 + b * nh * hd * 8})
+    with open(manifest_path, "w") as f:
+        json.dump(cases, f, indent=1)
+    print(f"wrote {len(cases)} cases to {manifest_path}", file=sys.stderr)
+
+
+def summarize(db, manifest_path):
+    cases = json.load(open(manifest_path))
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, duration from kernels order by start").fetchall()
+    segs, cur = [], None
+    for name, dur in rows:
+        if "fillBuffer" in name:
+            if cur is not None:
+                segs.append(cur)
+            cur = []
+        elif cur is not None:
+            cur.append((name, dur))
+    if cur is not None:
+        segs.append(cur)
+    # three segments per case: warmup, timed, then set-up of the next case
+    out = ["| config | case | kernels per call | us per call | GB/s | % of 8 TB/s |", "|---|---|---|---:|---:|---:|"]
+    for i, cs in enumerate(cases):
+        seg = segs[3 * i + 1]
+        work = [(n, d) for n, d in seg if "__amd_rocclr" not in n]
+        names = sorted({n.replace("void ", "").replace("(anonymous namespace)::", "").replace("prana::", "").split("(")[0]
+                        for n, _ in work})
+        us = sum(d for _, d in work) / 1000.0 / cs["calls"]
+        gbs = cs["bytes"] / (us * 1e-6) / 1e9
+        out.append(f"| {cs['config']} | {cs['case']} | {', '.join('`' + n + '`' for n in names)} | {us:.2f} | {gbs:.0f} "
+                   f"| {100 * gbs / 8000:.1f}% |")
+    print("\n".join(out))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--summarize", metavar="DB")
+    ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
+    args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize, args.manifest)
+    else:
+        run(args.manifest)
+
+
+if __name__ == "__main__":
+    main()
