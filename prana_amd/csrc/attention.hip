@@ -11,6 +11,8 @@
 // slices and the heads of one KV group are placed on the same XCD) and then
 // folds its own dims; V rows of the slice stream through LDS in chunks that
 // are fetched with 16-byte loads one chunk ahead of the fold.
+#include <algorithm>
+
 #include "common.h"
 #include "exact_sum.h"
 #include "kernels.h"
@@ -279,6 +281,312 @@ __device__ __forceinline__ int logical_block(int nb) {
   return (b % 8) * (nb / 8) + b / 8;
 }
 
+// ---------------------------------------------------------------- split path
+// The same arithmetic in three launches, for the f16 cache with 64- or
+// 128-wide heads: every phase then gets the parallelism it can use instead of
+// the one fixed by a workgroup per head.
+//   scores : one lane per (K row, KV head); the group's query heads are folded
+//            side by side (independent chains), scores -> scratch
+//   softmax: one 1024-lane workgroup per (query row, head): max, expf, the
+//            exact left-to-right sum, probabilities -> scratch (in place)
+//   PV     : one workgroup per (query row, head, 64-dim slice): one folder
+//            wave adds the products of its dims in row order while four
+//            producer waves stream V and form the products of the next chunk
+// Scratch rows are (query row, head) major with a stride of
+// split_stride(ctx_cap) floats.
+constexpr int kSplitRows = 256;     // K rows per scores workgroup
+constexpr int kSmNT = 1024;         // softmax lanes
+constexpr int kPvProd = 256;        // producer lanes
+constexpr int kPvNT = 64 + kPvProd; // one folder wave + producers
+// cache windows from this many rows on take the split path
+constexpr size_t kSplitMinRows = 2048;
+
+__host__ __device__ constexpr size_t split_stride(size_t ctx_cap) {
+  return (ctx_cap + kSplitRows - 1) / kSplitRows * kSplitRows;
+}
+
+// grid: (ceil(rows / kSplitRows), n_q * n_kv * ceil(group / 4)). Lane t of
+// block x scores K row x*kSplitRows + t against a block of up to four query
+// heads of one KV group (side-by-side chains) for query row i; rows past that
+// row's position are skipped. A short head block repeats its first head in
+// the spare chains (computed, not stored) so the body has no branches.
+template <int HD>
+__global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __restrict__ q,
+                                                                const uint16_t* __restrict__ k, int pos0,
+                                                                int n_heads, int group, int n_kv,
+                                                                float* __restrict__ sc, int sc_stride) {
+  __shared__ __align__(16) float s_q[4 * HD];
+  const int nhb = (group + 3) / 4;
+  const int hb = blockIdx.y % nhb, ik = blockIdx.y / nhb;
+  const int i = ik / n_kv, kvh = ik % n_kv;
+  const int n = pos0 + i + 1;
+  const int row0 = blockIdx.x * kSplitRows;
+  if (row0 >= n) return;  // uniform, before the barrier
+  const int h0 = kvh * group + 4 * hb;  // first head of the block
+  const int nh = min(4, group - 4 * hb);
+  const float* qh = q + (size_t)i * n_heads * HD + (size_t)h0 * HD;
+  for (int e = threadIdx.x; e < 4 * HD; e += kSplitRows) s_q[e] = qh[e / HD < nh ? e : e % HD];
+  __syncthreads();
+  const int t = row0 + threadIdx.x;
+  if (t >= n) return;
+  const int kv_stride = n_kv * HD;
+  const uint4* kp = reinterpret_cast<const uint4*>(k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  uint4 raw[HD / 8];
+#pragma unroll
+  for (int e = 0; e < HD / 8; e++) raw[e] = kp[e];
+  const float4* qv = reinterpret_cast<const float4*>(s_q);
+  float dot[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
+  // q of step e+1 is read while step e computes. The empty asm after each
+  // step consumes that step's partial dots and orders memory, so the reads
+  // of later steps cannot be hoisted above it (all of them at once would
+  // need 4*HD registers).
+  float4 qa[4][2], qn[4][2];
+#pragma unroll
+  for (int hh = 0; hh < 4; hh++) qa[hh][0] = qv[hh * (HD / 4)], qa[hh][1] = qv[hh * (HD / 4) + 1];
+#pragma unroll
+  for (int e = 0; e < HD / 8; e++) {
+    if (e + 1 < HD / 8) {
+#pragma unroll
+      for (int hh = 0; hh < 4; hh++)
+        qn[hh][0] = qv[hh * (HD / 4) + 2 * e + 2], qn[hh][1] = qv[hh * (HD / 4) + 2 * e + 3];
+    }
+    const uint32_t w[4] = {raw[e].x, raw[e].y, raw[e].z, raw[e].w};
+    float kf[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      kf[j] = f16_operand(static_cast<uint16_t>(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu));
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+      const float4 a = qa[hh][0], b = qa[hh][1];
+      dot[hh] += a.x * kf[0];
+      dot[hh] += a.y * kf[1];
+      dot[hh] += a.z * kf[2];
+      dot[hh] += a.w * kf[3];
+      dot[hh] += b.x * kf[4];
+      dot[hh] += b.y * kf[5];
+      dot[hh] += b.z * kf[6];
+      dot[hh] += b.w * kf[7];
+    }
+    asm volatile("" ::"v"(dot[0]), "v"(dot[1]), "v"(dot[2]), "v"(dot[3]) : "memory");
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) qa[hh][0] = qn[hh][0], qa[hh][1] = qn[hh][1];
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  float* dst = sc + ((size_t)i * n_heads + h0) * sc_stride + t;
+#pragma unroll
+  for (int hh = 0; hh < 4; hh++)
+    if (hh < nh) dst[(size_t)hh * sc_stride] = dot[hh] * scale;
+}
+
+// grid: (n_heads, n_q). Softmax of the row's scores in place. Rows of up to
+// kSmNT*kSmPer scores are held in registers (every load in flight at once);
+// longer rows stream. IN_LDS: the exponentials are staged in LDS
+// (exact::run_pad layout) for the exact sum; otherwise the sum reads them
+// back from the scratch row.
+constexpr int kSmPer = 36;
+template <bool IN_LDS>
+__global__ __launch_bounds__(kSmNT) void attn_split_softmax(float* __restrict__ sc, int sc_stride, int pos0,
+                                                            int n_heads) {
+  extern __shared__ float4 smem_e4[];
+  float* e = reinterpret_cast<float*>(smem_e4);
+  __shared__ float s_red[kSmNT / 64];
+  const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+  const int n = pos0 + i + 1;
+  float* row = sc + ((size_t)i * n_heads + h) * sc_stride;
+  const bool in_regs = n <= kSmNT * kSmPer;
+  float vals[kSmPer];
+  float mx = -INFINITY;
+  if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kSmPer; k++) {
+      if (k * kSmNT >= n) break;  // uniform
+      vals[k] = row[min(tid + k * kSmNT, n - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kSmPer; k++) {
+      if (k * kSmNT >= n) break;
+      if (tid + k * kSmNT < n) mx = fmaxf(mx, vals[k]);
+    }
+  } else {
+    for (int t = tid; t < n; t += kSmNT) mx = fmaxf(mx, row[t]);
+  }
+  mx = wave_max_f32(mx);
+  if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kSmNT / 64; w++) mx = fmaxf(mx, s_red[w]);
+  auto put = [&](int t, float v) {
+    if constexpr (IN_LDS)
+      e[exact::run_pad(t)] = v;
+    else
+      row[t] = v;
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kSmPer; k++) {
+      if (k * kSmNT >= n) break;
+      const int t = tid + k * kSmNT;
+      vals[k] = dev_expf(vals[k] - mx);
+      if (t < n) put(t, vals[k]);
+    }
+  } else {
+    for (int t = tid; t < n; t += kSmNT) put(t, dev_expf(row[t] - mx));
+  }
+  __syncthreads();
+  // softmax sum in the reference's left-to-right order (norms.rs:53)
+  float sum;
+  if constexpr (IN_LDS)
+    sum = exact::block_seq_sum_short<kSmNT>([e](int t) { return e[exact::run_pad(t)]; }, n);
+  else if (n <= exact::kPredHead + kSmNT * exact::kPredMaxPerLane)
+    sum = exact::block_seq_sum_short<kSmNT>([row](int t) { return row[t]; }, n);
+  else
+    sum = exact::block_seq_sum_nonneg<kSmNT, false>(row, n);
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kSmPer; k++) {
+      if (k * kSmNT >= n) break;
+      const int t = tid + k * kSmNT;
+      if (t < n) row[t] = vals[k] * inv;
+    }
+  } else {
+    for (int t = tid; t < n; t += kSmNT) {
+      if constexpr (IN_LDS)
+        row[t] = e[exact::run_pad(t)] * inv;
+      else
+        row[t] = row[t] * inv;
+    }
+  }
+}
+
+// grid: (n_heads * HD/64, n_q). Folder lane d (wave 0) owns dim 64*slice + d;
+// producer lane (waves 1..4) tasks = (row quad, dim pair). Products of a
+// chunk of CH rows sit in LDS as [row/4][dim][row%4] so the folder reads four
+// rows of its dim with one 16-byte load. Rows past n are zero products, which
+// leave the fold (started from +0.0) unchanged.
+template <int HD, int CH>
+__global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__ prob, int sc_stride,
+                                                       const uint16_t* __restrict__ v, int pos0, int n_heads,
+                                                       int group, float* __restrict__ out,
+                                                       int8_t* __restrict__ qd, float* __restrict__ qsa,
+                                                       int* __restrict__ qsum) {
+  constexpr int NS = HD / 64;
+  constexpr int kTasks = CH / 4 * 32;  // (row quad, dim pair) per chunk
+  constexpr int kPer = kTasks / kPvProd;
+  constexpr int kQuadStep = kPvProd / 32;  // row quads between a lane's tasks
+  static_assert(kTasks % kPvProd == 0, "whole tasks per producer lane");
+  static_assert(kSplitRows % CH == 0, "probability reads of the last chunk stay inside the scratch row");
+  __shared__ __align__(16) float s_prod[2][CH * 64];
+  const int lb = logical_block(n_heads * NS);
+  const int h = lb / NS, slice = lb % NS, i = blockIdx.y;
+  const int n = pos0 + i + 1;
+  const int kvh = h / group;
+  const int kv_words = (n_heads / group) * HD / 2;  // a cache row in 32-bit words
+  const int tid = threadIdx.x;
+  const int n_chunks = (n + CH - 1) / CH;
+  const bool folder = tid < 64;
+  const int pl = tid - 64;
+  const int dp = pl & 31, rq0 = pl >> 5;
+  // this lane's dim pair in row 0, and its probabilities
+  const uint32_t* vlane = reinterpret_cast<const uint32_t*>(v + (size_t)kvh * HD + slice * 64) + dp;
+  const float* plane = prob + ((size_t)i * n_heads + h) * sc_stride + 4 * rq0;
+
+  uint32_t vr[kPer][4];
+  float4 pr[kPer];
+  auto fetch = [&](int c) {
+    const int tq = c * CH + 4 * rq0;  // first row of task 0
+    if (c * CH + CH <= n) {           // whole chunk: no clamping
+#pragma unroll
+      for (int k = 0; k < kPer; k++) {
+        const uint32_t* r0 = vlane + (size_t)(tq + 4 * kQuadStep * k) * kv_words;
+        pr[k] = *reinterpret_cast<const float4*>(plane + c * CH + 4 * kQuadStep * k);
+#pragma unroll
+        for (int r = 0; r < 4; r++) vr[k][r] = r0[(size_t)r * kv_words];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kPer; k++) {
+        const int t = tq + 4 * kQuadStep * k;
+        pr[k] = *reinterpret_cast<const float4*>(plane + c * CH + 4 * kQuadStep * k);  // t + 3 < sc_stride
+#pragma unroll
+        for (int r = 0; r < 4; r++) vr[k][r] = vlane[(size_t)min(t + r, n - 1) * kv_words];  // rows past n: unused
+      }
+    }
+  };
+  auto produce = [&](int c, float* buf) {
+    const int tq = c * CH + 4 * rq0;
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int t = tq + 4 * kQuadStep * k;
+      const float pv[4] = {pr[k].x, pr[k].y, pr[k].z, pr[k].w};
+      float a[4], b[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const bool live = t + r < n;
+        a[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(vr[k][r] & 0xffffu)) : 0.0f;
+        b[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(vr[k][r] >> 16)) : 0.0f;
+      }
+      float4* dst = reinterpret_cast<float4*>(buf) + (rq0 + kQuadStep * k) * 64 + 2 * dp;
+      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+      dst[1] = make_float4(b[0], b[1], b[2], b[3]);
+    }
+  };
+
+  float acc = 0.0f;
+  if (!folder) {
+    fetch(0);
+    produce(0, s_prod[0]);
+    if (n_chunks > 1) fetch(1);
+  }
+  __syncthreads();
+  for (int c = 0; c < n_chunks; c++) {
+    if (folder) {
+      // groups of 8 row quads; the next group's reads are issued before this
+      // group's adds, and the empty asm (consuming acc, ordering memory)
+      // keeps later reads from being hoisted further
+      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid;
+      float4 x[8], y[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] = src[j * 64];
+#pragma unroll
+      for (int g = 0; g < CH / 32; g++) {
+        if (g + 1 < CH / 32) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) y[j] = src[((g + 1) * 8 + j) * 64];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          acc += x[j].x;
+          acc += x[j].y;
+          acc += x[j].z;
+          acc += x[j].w;
+        }
+        asm volatile("" ::"v"(acc) : "memory");
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = y[j];
+      }
+    } else if (c + 1 < n_chunks) {
+      produce(c + 1, s_prod[(c + 1) & 1]);
+      if (c + 2 < n_chunks) fetch(c + 2);
+    }
+    __syncthreads();
+  }
+  if (folder) {
+    const size_t gi = (size_t)i * n_heads * HD + (size_t)h * HD + slice * 64 + tid;
+    out[gi] = acc;
+    if (qd) {
+      float scale;
+      int sum;
+      const int qi = quantize_lane(acc, &scale, &sum);
+      qd[gi] = static_cast<int8_t>(qi);
+      if ((gi & 31) == 0) {
+        qsa[gi >> 5] = scale;
+        qsum[gi >> 5] = sum;
+      }
+    }
+  }
+}
+
 // grid: (n_heads*dsplit, n_q). Query row i sits at position p0 + i.
 // mode: 0 scalar rows; -1 vector V chunks with a runtime head width;
 // 48/64/128 vector K and V loads with that compiled head width.
@@ -318,6 +626,63 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
   one_head<F16>(J, mode, L);
 }
 
+// Largest dynamic LDS a launch may request on this device (queried once).
+size_t max_dyn_lds() {
+  static const size_t v = [] {
+    int dev = 0, b = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return size_t{65536};
+    return static_cast<size_t>(b);
+  }();
+  return v;
+}
+
+template <int HD>
+int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, size_t n_q, size_t n_heads,
+                 size_t n_kv_heads, float* out, float* scratch, size_t ctx_cap, const ActQuant* aq, bool* quantized,
+                 hipStream_t s) {
+  const int group = static_cast<int>(n_heads / n_kv_heads);
+  const int stride = static_cast<int>(split_stride(ctx_cap));
+  const size_t rows = pos0 + n_q;
+  hipLaunchKernelGGL(attn_split_scores<HD>,
+                     dim3((rows + kSplitRows - 1) / kSplitRows, n_q * n_kv_heads * ((group + 3) / 4)),
+                     dim3(kSplitRows), 0, s, q, k, (int)pos0, (int)n_heads, group,
+                     (int)n_kv_heads, scratch, stride);
+  PRANA_LAUNCH_CHECK();
+  // the softmax stages the longest row's exponentials in LDS when they fit
+  const size_t lds = (exact::run_pad(static_cast<int>(rows) - 1) + 1) * sizeof(float);
+  static const size_t lds_cap = [] {
+    const size_t cap = max_dyn_lds() > 16384 ? max_dyn_lds() - 16384 : 0;  // static LDS of the sum
+    if (cap > 65536)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_split_softmax<true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap));
+    return cap;
+  }();
+  if (lds <= lds_cap)
+    hipLaunchKernelGGL(attn_split_softmax<true>, dim3(n_heads, n_q), dim3(kSmNT), lds, s, scratch, stride,
+                       (int)pos0, (int)n_heads);
+  else
+    hipLaunchKernelGGL(attn_split_softmax<false>, dim3(n_heads, n_q), dim3(kSmNT), 0, s, scratch, stride,
+                       (int)pos0, (int)n_heads);
+  PRANA_LAUNCH_CHECK();
+  const bool fuse_q = aq && aq->q;  // 64-dim slices are whole 32-blocks
+  if (quantized) *quantized = fuse_q;
+  // long chunks amortize the per-chunk barrier; short ones keep two
+  // workgroups per CU when there are many
+  int8_t* qd = fuse_q ? aq->q : nullptr;
+  float* qsa = fuse_q ? aq->sa : nullptr;
+  int* qsum = fuse_q ? aq->sums : nullptr;
+  if (n_heads * (HD / 64) * n_q <= 256)
+    hipLaunchKernelGGL((attn_split_pv<HD, 256>), dim3(n_heads * (HD / 64), n_q), dim3(kPvNT), 0, s, scratch, stride,
+                       v, (int)pos0, (int)n_heads, group, out, qd, qsa, qsum);
+  else
+    hipLaunchKernelGGL((attn_split_pv<HD, 128>), dim3(n_heads * (HD / 64), n_q), dim3(kPvNT), 0, s, scratch, stride,
+                       v, (int)pos0, (int)n_heads, group, out, qd, qsa, qsum);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 template <bool F16>
 int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const int* pos_dev, size_t n_q,
                 size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
@@ -325,6 +690,14 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
   const size_t elem = F16 ? 2 : 4;
   const bool aligned = reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                        (hd * elem) % 16 == 0;
+  if (F16 && aligned && !pos_dev && scratch && pos0 + n_q >= kSplitMinRows && (hd == 64 || hd == 128)) {
+    const uint16_t* kc = static_cast<const uint16_t*>(k);
+    const uint16_t* vc = static_cast<const uint16_t*>(v);
+    return hd == 64 ? launch_split<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap, aq,
+                                       quantized, s)
+                    : launch_split<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap, aq,
+                                        quantized, s);
+  }
   int mode = 0;
   if (aligned) {
     const bool compiled = (hd == 48 || hd == 64 || hd == 128) && (F16 || hd % 16 == 0);
@@ -355,11 +728,15 @@ int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, boo
   return ds;
 }
 
-size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap) {
-  if (ctx_cap <= static_cast<size_t>(kScoreLds)) return 0;
-  size_t ds = 1;  // upper bound of attention_dim_slices
-  while (n_q * n_heads * ds < 128 && ds < 4) ds *= 2;
-  return n_q * n_heads * ds * ctx_cap;
+size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap, bool cache) {
+  // split path (cache windows): scores / probabilities of every (query row, head)
+  size_t need = cache ? n_q * n_heads * split_stride(ctx_cap) : 0;
+  if (ctx_cap > static_cast<size_t>(kScoreLds)) {
+    size_t ds = 1;  // upper bound of attention_dim_slices
+    while (n_q * n_heads * ds < 128 && ds < 4) ds *= 2;
+    need = std::max(need, n_q * n_heads * ds * ctx_cap);
+  }
+  return need;
 }
 
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,

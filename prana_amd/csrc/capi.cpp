@@ -371,7 +371,7 @@ int prana_attention_prefill(const float* q, const float* k, const float* v, size
     INIT_OR_RETURN();
     Scratch& sc = scratch();
     std::lock_guard<std::mutex> lk(sc.mu);
-    const size_t need = attention_scratch_floats(seq, n_heads, seq);
+    const size_t need = attention_scratch_floats(seq, n_heads, seq, false);
     int rc = sc.att.ensure(need * 4);
     if (rc) return rc;
     hipStream_t s = pick_stream(stream);

@@ -117,7 +117,15 @@ __host__ __device__ inline int binade(float s) {
 // of a segment without the end check seeing it, and inside the binade every
 // step's grid rounding is the f32 rounding. When a check fails (or there are
 // more than kPredMaxCross crossings) the caller folds serially instead.
+// The exact partial sums drift from the approximate ones by their rounding
+// errors (random-walk-like, ~sqrt(n) units at most in practice). A step whose
+// approximate result lies within pred_margin(n) units of a binade boundary is
+// "ambiguous": it is made a crossing (a plain add in the walk) and so is the
+// step after it, so no segment starts or ends on a guessed binade. Such
+// crossings carry the binade code kPredAmb; the walk skips the (empty)
+// segment that follows them.
 constexpr int kPredHead = 32;       // folded serially first (the sum grows fastest here)
+constexpr int kPredAmb = 1000;      // binade code of an ambiguous step
 constexpr int kPredMaxCross = 63;   // crossings the walk accepts (one per lane of a wave)
 constexpr int kPredMaxPerLane = 64; // terms per lane of the predicted scan
 
@@ -240,6 +248,21 @@ __device__ __forceinline__ int binade_fast(float p) {
   return (E > 1 ? E : 1) - 127;
 }
 
+// Margin, in units of the last place, around binade boundaries inside which
+// an approximate partial sum of an n-term fold does not decide the binade.
+__host__ __device__ inline int pred_margin(int n) { return 8 * static_cast<int>(sqrtf(static_cast<float>(n))) + 16; }
+
+// The binade code of an approximate partial sum p >= 0: its binade, or
+// kPredAmb when p > 0 lies within r units of either boundary of its binade.
+__device__ __forceinline__ int binade_code(float p, int r) {
+  const uint32_t f = __float_as_uint(p) & 0x7fffffu;
+  const bool amb = p > 0.0f && (f < static_cast<uint32_t>(r) || f > 0x7fffffu - static_cast<uint32_t>(r));
+  return amb ? kPredAmb : binade_fast(p);
+}
+
+// A step with binade code ec after a step with code ein starts a new segment.
+__device__ __forceinline__ bool seg_break(int ec, int ein) { return ec != ein || ec == kPredAmb; }
+
 // term_pair_bits(bits(t), e) for finite t >= 0, from exact float operations
 // (scaling by a power of two, floor and the difference are exact here; a
 // scaled value small enough to lose bits is far below one half), without
@@ -340,6 +363,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   const int C = (n - kPredHead + NT - 1) / NT;
   const int i0 = kPredHead + tid * C;
   const int nv = max(0, min(C, n - i0));
+  const int R = pred_margin(n);
   bool bad = false;
   if (tid == 0) {
     float h[kPredHead];
@@ -392,18 +416,19 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
 #pragma unroll
       for (int k = 0; k < 4; k++) u[k] = a(min(i0 + jb + 4 + k, n - 1));
       float x[4], fr[4];
-      int e[4], v[4], ii[4];
+      int e[4], ec[4], v[4], ii[4];
       bool slow = false;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         x[k] = jb + k < nv ? t[k] : 0.0f;  // zero padding: no change to any state
         P += x[k];
         e[k] = binade_fast(P);
+        ec[k] = binade_code(P, R);
       }
       if (jb == 0) {
-        ep_first = e[0];
+        ep_first = ec[0];
         x0 = x[0];
-        elast = e[0];
+        elast = ec[0];
       }
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -412,24 +437,24 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
         fr[k] = A - I;
         ii[k] = static_cast<int>(I);
         const bool step = !(jb == 0 && k == 0);  // step 0 is combined after the exchange
-        const int ein = k == 0 ? elast : e[k - 1];
-        slow |= step && (e[k] != ein || fr[k] == 0.5f);
+        const int ein = k == 0 ? elast : ec[k - 1];
+        slow |= step && (seg_break(ec[k], ein) || fr[k] == 0.5f);
         v[k] = step ? min(ii[k] + (fr[k] > 0.5f ? 1 : 0), kCap) : 0;
       }
       if (slow) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
           if (jb == 0 && k == 0) continue;
-          const int ein = k == 0 ? elast : e[k - 1];
-          if (e[k] != ein) {
+          const int ein = k == 0 ? elast : ec[k - 1];
+          if (seg_break(ec[k], ein)) {
             // plain selects keep the records in registers
             const bool r1 = ncross == 0, r2 = ncross == 1;
             x1 = r1 ? x[k] : x1;
-            e1 = r1 ? e[k] : e1;
+            e1 = r1 ? ec[k] : e1;
             pre1.e = r1 ? rest.p.e : pre1.e;
             pre1.o = r1 ? rest.p.o : pre1.o;
             x2 = r2 ? x[k] : x2;
-            e2 = r2 ? e[k] : e2;
+            e2 = r2 ? ec[k] : e2;
             pre2.e = r2 ? rest.p.e : pre2.e;
             pre2.o = r2 ? rest.p.o : pre2.o;
             ncross++;
@@ -448,7 +473,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
         rest.p.e = min(rest.p.e + s4, kCap);
         rest.p.o = min(rest.p.o + s4, kCap);
       }
-      elast = e[3];
+      elast = ec[3];
 #pragma unroll
       for (int k = 0; k < 4; k++) t[k] = u[k];
     }
@@ -457,9 +482,9 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   int prev_last = wave_shr1(ep_last);
   if (lane == 63) s_epl[wave] = ep_last;
   __syncthreads();
-  if (lane == 0) prev_last = wave > 0 ? s_epl[wave - 1] : binade_fast(sH);
+  if (lane == 0) prev_last = wave > 0 ? s_epl[wave - 1] : binade_code(sH, R);
   int next_first = __shfl_down(ep_first, 1, 64);
-  const bool cross0 = ep_first != prev_last;
+  const bool cross0 = seg_break(ep_first, prev_last);
   const SegAcc el0 = cross0 ? SegAcc{Pair{0, 0}, 1} : SegAcc{term_pair_fast(x0, ep_first), 0};
   const SegAcc loc = nv > 0 ? seg_combine(el0, rest) : SegAcc{Pair{0, 0}, 0};
   // workgroup exclusive segmented scan of the lanes' compositions
@@ -518,9 +543,9 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
       int ein = prev_last;
       for_each_run(a, i0, nv, n, [&](int j, float x) {
         P += x;
-        const int e = binade_fast(P);
+        const int e = binade_code(P, R);
         if (j > 0) {
-          const bool cross = e != ein;
+          const bool cross = seg_break(e, ein);
           if (cross) {  // step j-1 ends its segment
             s_tot[2 * r.c] = r.p.e;
             s_tot[2 * r.c + 1] = r.p.o;
@@ -534,7 +559,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
         ein = e;
       });
     }
-    if (i0 + nv == n || next_first != ep_last) {  // the lane's last step ends its segment
+    if (i0 + nv == n || seg_break(next_first, ep_last)) {  // the lane's last step ends its segment
       const SegAcc fin = seg_combine(run, loc);
       s_tot[2 * fin.c] = fin.p.e;
       s_tot[2 * fin.c + 1] = fin.p.o;
@@ -557,6 +582,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
         E = __builtin_amdgcn_readlane(ce, j);
         good = val <= 3.4028234663852886e38f;
       }
+      if (E == kPredAmb) continue;  // an ambiguous crossing: its segment is empty
       int e;
       int32_t m;
       decompose(val, &e, &m);

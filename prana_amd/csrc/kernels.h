@@ -89,8 +89,9 @@ size_t terms_per_row(const DevMat& m);
 // attention_decode / attention_verify (attention.rs:129-160, 296-333) over the
 // f16 cache: n_q query rows at positions pos0 + i (pos0 read from pos_dev when
 // non-null). scratch >= attention_scratch_floats(n_q, n_heads, ctx_cap)
-// floats (none up to 4096 positions), ctx_cap >= pos0+n_q (0 = exactly
-// pos0+n_q).
+// floats, ctx_cap >= pos0+n_q (0 = exactly pos0+n_q). Windows of at least
+// 2048 rows with 64- or 128-wide heads and a host-side position take the
+// three-launch split path.
 // Optional quantized copy of an attention output (quantize_acts layout, one
 // row of n_heads*hd per query). The launchers fill it in the same pass when
 // every workgroup's output dims are whole 32-element blocks and report that
@@ -105,10 +106,12 @@ int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* v
                            const int* pos_dev, hipStream_t s, const ActQuant* aq = nullptr,
                            bool* quantized = nullptr);
 // attention (prefill, attention.rs:236-284) over f32 K/V of the window.
-// scratch >= attention_scratch_floats(seq, n_heads, seq) floats.
-// Score scratch a launch needs (probabilities beyond 4096 positions spill
-// from LDS to it), and the dim slices per head a launch uses.
-size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap);
+// scratch >= attention_scratch_floats(seq, n_heads, seq, false) floats.
+// Score scratch a launch needs: cache windows (cache = true) keep the scores
+// of every (query row, head) there on the split path; probabilities beyond
+// 4096 positions spill from LDS to it on the one-launch path. Also the dim
+// slices per head a launch uses.
+size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap, bool cache = true);
 int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, bool aligned);
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
                              size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s,

@@ -193,8 +193,8 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
       return rc;
     ws.cap_tok = n;
   }
-  size_t need = std::max(attention_scratch_floats(n_tok, c.n_heads, ctx_cap),
-                         prefill_attn ? attention_scratch_floats(n_tok, c.n_heads, n_tok) : 0) * 4;
+  size_t need = (prefill_attn ? attention_scratch_floats(n_tok, c.n_heads, n_tok, false)
+                              : attention_scratch_floats(n_tok, c.n_heads, ctx_cap)) * 4;
   if ((rc = ws.scratch.ensure(std::max<size_t>(need, 4)))) return rc;
   return kOk;
 }

@@ -76,6 +76,27 @@ def test_tiny_speculative_equals_greedy_and_oracle(draft_arch):
     assert list(spec)[: len(plain)] == list(plain)[: len(spec)]
 
 
+def test_long_window_split_attention_bitexact():
+    # Decode and verify steps past 2048 cached rows run the split attention
+    # path, whose PV launch also quantizes the output for the wo projection.
+    cfg = M.config(256, 512, 2, 4, 1, 512, 2200, head_dim=64, rope_neox=1)
+    t = M.synth_tensors(cfg, M.types_c0, 7)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(2200), o.cache(2200)
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab_size"], 2050).astype(np.uint32)
+    gc.prefill(prompt[:2045])
+    oc.prefill(prompt[:2045])
+    tok = int(prompt[2045])
+    for pos in range(2045, 2049):  # windows of 2046..2049 rows: both paths
+        lg, lo = gc.forward(tok, pos), oc.forward(tok, pos)
+        assert same_bits(lg, lo), pos
+        tok = int(np.argmax(lo))
+    batch = [int(x) for x in prompt[:5]]
+    assert same_bits(gc.forward_batch(batch, 2049), oc.forward_batch(batch, 2049))
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(gc.read(layer, 1, 2054), oc.read(layer, 1, 2054))
+
+
 # ------------------------------------------------------------------ config 0: 15M shape, Q8_0, 256-step greedy decode
 @pytest.fixture(scope="module")
 def c0():
