@@ -917,6 +917,234 @@ int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const in
   return kOk;
 }
 
+// ---- skinny batches (a few tokens) on the 16x16x32 int8 matrix cores
+// v_mfma_i32_16x16x32_i8 takes one whole 32-element block per instruction:
+// A[i][k] = activation k of token i, B[k][j] = quant k of weight row j; lane
+// (j = lane%16, kg = lane/16) supplies elements 8kg..8kg+7 of token / row j
+// and receives D for tokens 4kg+v, row j (v = 0..3). A wave owns 16 rows x
+// 16 tokens; a workgroup's RW*TT waves cover 16*RW rows x 16*TT tokens.
+// Weights, activations and both scale sets stream through LDS in chunks of
+// kSkCB blocks: every lane fetches its share of chunk c+3 into registers
+// while chunk c is multiplied, so two chunks of loads are in flight behind
+// the one being used. Every output folds its block terms (d*sa)*float(isum)
+// in block order, as the decode kernels do.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+constexpr int kSkCB = 16;  // blocks per staged chunk
+
+template <int KIND, int RW, int TT>
+struct SkLayout {
+  static constexpr int NT = 64 * RW * TT;
+  static constexpr int QB = KIND == kKindQ4_0 ? 16 : 32;  // quant bytes per block
+  static constexpr int ROWS = 16 * RW, TOKS = 16 * TT;
+  // padded rows: 16 consecutive rows / tokens start 4 banks apart
+  static constexpr int WSTR = kSkCB * QB + 16;  // bytes per staged weight row
+  static constexpr int ASTR = kSkCB * 32 + 16;  // bytes per staged activation row
+  static constexpr int DSTR = kSkCB + 1;        // words per staged weight-scale row
+  // one buffer: W [ROWS][WSTR] | A [TOKS][ASTR] | D [ROWS][DSTR] | SA [kSkCB][TOKS] | SM [kSkCB][TOKS]
+  static constexpr int A_OFF = ROWS * WSTR;
+  static constexpr int D_OFF = A_OFF + TOKS * ASTR;
+  static constexpr int SA_OFF = D_OFF + ROWS * DSTR * 4;
+  static constexpr int SM_OFF = SA_OFF + kSkCB * TOKS * 4;
+  static constexpr int BYTES = SM_OFF + kSkCB * TOKS * 4;
+  // pieces of a chunk and their share per lane
+  static constexpr int WPR = kSkCB * QB / 16;  // 16-byte weight pieces per row
+  static constexpr int WP = ROWS * WPR, AP = TOKS * kSkCB * 2, DP = ROWS * kSkCB, SP = TOKS * kSkCB;
+  static constexpr int WPL = (WP + NT - 1) / NT, APL = (AP + NT - 1) / NT;
+  static constexpr int DPL = (DP + NT - 1) / NT, SPL = (SP + NT - 1) / NT;
+};
+
+typedef int sk_i4 __attribute__((ext_vector_type(4)));  // plain vector: stays in registers
+
+template <int KIND, int RW, int TT>
+struct SkRegs {
+  using L = SkLayout<KIND, RW, TT>;
+  sk_i4 w[L::WPL], a[L::APL];
+  uint32_t d[L::DPL];
+  float sa[L::SPL];
+  int sm[L::SPL];
+};
+
+template <int KIND, int RW, int TT>
+__global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, const int8_t* __restrict__ q,
+                                                                   const float* __restrict__ sa,
+                                                                   const int* __restrict__ sums, int n_tok,
+                                                                   GemvOut o) {
+  static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
+  using L = SkLayout<KIND, RW, TT>;
+  extern __shared__ int4 sk_smem[];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(sk_smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rtile = wave % RW, ttile = wave / RW;
+  const int j = lane & 15, kg = lane >> 4;
+  const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
+  const int row0 = static_cast<int>(blockIdx.x) * L::ROWS;
+  const int n_chunks = (G + kSkCB - 1) / kSkCB;
+
+  auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
+    SkRegs<KIND, RW, TT> r;
+    const int cb0 = c * kSkCB;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = min(tid + L::NT * i, L::WP - 1);
+      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int blk = min(cb0 + pr / (L::QB / 16), G - 1);
+      const uint8_t* src = m.qs + (size_t)rr * G * L::QB + (size_t)blk * L::QB + (pr % (L::QB / 16)) * 16;
+      r.w[i] = *reinterpret_cast<const sk_i4*>(src);
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = min(tid + L::NT * i, L::AP - 1);
+      const int t = min(p / (2 * kSkCB), n_tok - 1), pr = p % (2 * kSkCB);
+      const int blk = min(cb0 + pr / 2, G - 1);
+      r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = min(tid + L::NT * i, L::DP - 1);
+      const size_t gi = (size_t)min(row0 + p / kSkCB, R - 1) * G + min(cb0 + p % kSkCB, G - 1);
+      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
+                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = min(tid + L::NT * i, L::SP - 1);
+      const size_t gi = (size_t)min(p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
+      r.sa[i] = sa[gi];
+      r.sm[i] = sums[gi];
+    }
+    return r;
+  };
+  auto store = [&](const SkRegs<KIND, RW, TT>& r, int buf) __attribute__((always_inline)) {
+    uint8_t* b = lds + buf * L::BYTES;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::WP) *reinterpret_cast<sk_i4*>(b + (p / L::WPR) * L::WSTR + (p % L::WPR) * 16) = r.w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::AP)
+        *reinterpret_cast<sk_i4*>(b + L::A_OFF + (p / (2 * kSkCB)) * L::ASTR + (p % (2 * kSkCB)) * 16) = r.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::DP) reinterpret_cast<uint32_t*>(b + L::D_OFF)[(p / kSkCB) * L::DSTR + p % kSkCB] = r.d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::SP) {
+        reinterpret_cast<float*>(b + L::SA_OFF)[(p % kSkCB) * L::TOKS + p / kSkCB] = r.sa[i];
+        reinterpret_cast<int*>(b + L::SM_OFF)[(p % kSkCB) * L::TOKS + p / kSkCB] = r.sm[i];
+      }
+    }
+  };
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int buf, int c) __attribute__((always_inline)) {
+    const uint8_t* b = lds + buf * L::BYTES;
+    const uint8_t* arow = b + L::A_OFF + (ttile * 16 + j) * L::ASTR + 8 * kg;
+    const uint8_t* wrow = b + (rtile * 16 + j) * L::WSTR + (KIND == kKindQ4_0 ? 8 * (kg & 1) : 8 * kg);
+    const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + (rtile * 16 + j) * L::DSTR;
+    const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + ttile * 16 + 4 * kg;
+    const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + ttile * 16 + 4 * kg;
+    const int nlive = min(kSkCB, G - c * kSkCB);  // uniform
+#pragma unroll
+    for (int bb = 0; bb < kSkCB; bb++) {
+      const long av = *reinterpret_cast<const long*>(arow + bb * 32);
+      long wb = *reinterpret_cast<const long*>(wrow + bb * L::QB);
+      if constexpr (KIND == kKindQ4_0)
+        wb = kg < 2 ? (wb & 0x0F0F0F0F0F0F0F0FL) : ((wb >> 4) & 0x0F0F0F0F0F0F0F0FL);
+      const v4i_t z = {0, 0, 0, 0};
+      const v4i_t cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wb, z, 0, 0, 0);
+      const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
+      const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * L::TOKS);
+      const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      int mv[4] = {0, 0, 0, 0};
+      if constexpr (KIND == kKindQ4_0) {
+        const int4 m4 = *reinterpret_cast<const int4*>(smb + bb * L::TOKS);
+        mv[0] = m4.x, mv[1] = m4.y, mv[2] = m4.z, mv[3] = m4.w;
+      }
+      const bool live = bb < nlive;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        int isum = cc[v];
+        if constexpr (KIND == kKindQ4_0) isum -= 8 * mv[v];
+        const float t = acc[v] + d * sv[v] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
+        acc[v] = live ? t : acc[v];
+      }
+      // every fourth block: the LDS reads of later blocks may not be hoisted
+      // above this point (registers)
+      if (bb % 4 == 3) asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]) : "memory");
+    }
+  };
+
+  SkRegs<KIND, RW, TT> r0 = load(0), r1;
+  store(r0, 0);
+  if (n_chunks > 1) r0 = load(1);
+  if (n_chunks > 2) r1 = load(2);
+  __syncthreads();
+  // chunk c+1 sits in r0 when c is even, in r1 when c is odd
+  for (int c = 0; c < n_chunks; c += 2) {
+    compute(0, c);
+    if (c + 1 < n_chunks) store(r0, 1);
+    if (c + 3 < n_chunks) r0 = load(c + 3);
+    __syncthreads();
+    if (c + 1 >= n_chunks) break;
+    compute(1, c + 1);
+    if (c + 2 < n_chunks) store(r1, 0);
+    if (c + 4 < n_chunks) r1 = load(c + 4);
+    __syncthreads();
+  }
+  const int n_row = row0 + rtile * 16 + j;
+  if (n_row < R) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int t = 16 * ttile + 4 * kg + v;
+      if (t < n_tok) store_out(o, t, n_row, acc[v]);
+    }
+  }
+}
+
+template <int KIND, int RW, int TT>
+int launch_skinny_t(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                    const GemvOut& o, hipStream_t s) {
+  using L = SkLayout<KIND, RW, TT>;
+  static const bool attr_ok = [] {
+    return L::BYTES * 2 <= 65536 ||
+           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_skinny_kernel<KIND, RW, TT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+  }();
+  PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
+  hipLaunchKernelGGL((gemm_skinny_kernel<KIND, RW, TT>), dim3((m.rows + L::ROWS - 1) / L::ROWS), dim3(L::NT),
+                     L::BYTES * 2, s, m, q, sa, sums, (int)n_tok, o);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+template <int KIND, int TT>
+int launch_skinny_tt(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                     const GemvOut& o, hipStream_t s) {
+  // rows per workgroup: grow while at least 256 workgroups remain (bigger
+  // tiles share each staged activation chunk among more rows)
+  int rw = 1;
+  while (rw < 4 && (m.rows + 32 * rw - 1) / (32 * rw) >= 256) rw *= 2;
+  if (rw == 1) return launch_skinny_t<KIND, 1, TT>(m, q, sa, sums, n_tok, o, s);
+  if (rw == 2) return launch_skinny_t<KIND, 2, TT>(m, q, sa, sums, n_tok, o, s);
+  return launch_skinny_t<KIND, 4, TT>(m, q, sa, sums, n_tok, o, s);
+}
+
+template <int KIND>
+int launch_gemm_skinny(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                       const GemvOut& o, hipStream_t s) {
+  PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30) && n_tok >= 1 && n_tok <= 64,
+              "gemm_skinny: shape out of range");
+  if (n_tok <= 16) return launch_skinny_tt<KIND, 1>(m, q, sa, sums, n_tok, o, s);
+  if (n_tok <= 32) return launch_skinny_tt<KIND, 2>(m, q, sa, sums, n_tok, o, s);
+  return launch_skinny_tt<KIND, 4>(m, q, sa, sums, n_tok, o, s);
+}
+
 template <int KIND>
 int launch_q(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok, const GemvOut& o,
              hipStream_t s) {
@@ -968,7 +1196,7 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
   if (n_tok == 0) return kOk;
   for (int i = 1; i < n; i++)
     PRANA_CHECK(ms[i].kind == ms[0].kind && ms[i].cols == ms[0].cols, "gemv_multi: matrices must share kind and cols");
-  if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens) {
+  if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens || gemv_skinny(ms[0].kind, n_tok)) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
       if (rc) return rc;
@@ -1013,6 +1241,13 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s) {
   if (n_tok == 0 || m.rows == 0) return kOk;
+  if (gemv_skinny(m.kind, n_tok)) {
+    switch (m.kind) {
+      case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
+      case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
+      case kKindQ4_0: return launch_gemm_skinny<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
+    }
+  }
   if (m.kind != kKindF32 && n_tok <= kDecodeMaxTokens) {
     DecodeJob job{};
     job.m[0] = m;

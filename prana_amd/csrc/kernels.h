@@ -68,6 +68,15 @@ struct GemvOut {
 // Token counts up to this use the weight-streaming decode kernel (and
 // launch_gemv_act); larger batches use the tiled kernel.
 constexpr size_t kGemvDecodeMaxTokens = 16;
+// launch_gemv over block-32 kinds (Q8F, Q8_0, Q4_0) takes batches of this
+// many tokens to the skinny matrix-core kernel (launch_gemv_multi runs such
+// batches matrix by matrix).
+constexpr size_t kGemvSkinnyMinTokens = 5;
+constexpr size_t kGemvSkinnyMaxTokens = 64;
+inline bool gemv_skinny(int kind, size_t n_tok) {
+  return (kind == kKindQ8F || kind == kKindQ8_0 || kind == kKindQ4_0) && n_tok >= kGemvSkinnyMinTokens &&
+         n_tok <= kGemvSkinnyMaxTokens;
+}
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s);

@@ -90,28 +90,34 @@ def test_matmul_prefill_rows_equal_decode():
 
 
 @pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0, fx.Q4_K, fx.Q6_K])
-@pytest.mark.parametrize("rows,cols,n_tok", [(37, 512, 17), (300, 1024, 33), (129, 256, 70)])
+@pytest.mark.parametrize("rows,cols,n_tok", [(37, 512, 17), (300, 1024, 33), (129, 256, 70), (37, 512, 5),
+                                             (300, 1024, 9), (129, 768, 16), (1000, 512, 48), (64, 1280, 64),
+                                             (70, 256, 31)])
 def test_matmul_batched(ty, rows, cols, n_tok):
-    # N > 16 tokens: the int8 matrix-core path for block-32 kinds (ragged
-    # row and token tiles), the row-outer kernel for K-quants
+    # Batches of 5..64 tokens: the skinny int8 matrix-core kernel for
+    # block-32 kinds (ragged row and token tiles, block counts that are not
+    # whole fetch groups); more than 64: the tiled matrix-core kernel; K-quants
+    # the row-outer kernel
     raw, g, o = _mat_pair(ty, rows, cols, 41 + n_tok, real=True)
     a = rng(n_tok).standard_normal((n_tok, cols)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
 
 
+@pytest.mark.parametrize("n_tok", [16, 64])
 @pytest.mark.parametrize("shape", [(4096, 4096), (4096, 14336)])
-def test_matmul_batched_config1(shape):
+def test_matmul_batched_config1(shape, n_tok):
     rows, cols = shape
     raw, g, o = _mat_pair(fx.Q8_0, rows, cols, 200 + cols, real=True)
-    a = rng(64).standard_normal((64, cols)).astype(np.float32)
+    a = rng(n_tok).standard_normal((n_tok, cols)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
 
 
-def test_q8_f32_scales_parts_batched():
+@pytest.mark.parametrize("n_tok", [40, 7, 100])
+def test_q8_f32_scales_parts_batched(n_tok):
     w = rng(12).standard_normal((96, 256)).astype(np.float32)
     q, s = O.quantize_q8(w)
     g, o = P.Matrix.q8_parts(q, s), O.Mat.q8_parts(q, s)
-    a = rng(18).standard_normal((40, 256)).astype(np.float32)
+    a = rng(18).standard_normal((n_tok, 256)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
 
 
