@@ -161,7 +161,40 @@ __device__ __forceinline__ void make_products(const VPieces& v, const float* sc,
   one(v.b, threadIdx.x + kNT);
 }
 
+// Dots of q with two f16 K rows of a compiled head width, as two
+// side-by-side chains (each folded left to right from -0.0, as row_dot): the
+// second chain fills the first's dependent-add latency.
+template <int HD>
+__device__ __forceinline__ void row_dot2_f16(const float* s_q, const uint16_t* ka, const uint16_t* kb, float* da,
+                                             float* db) {
+  static_assert(HD % 8 == 0, "f16 rows load 8 halves at a time");
+  uint4 ra[HD / 8], rb[HD / 8];
+  const uint4* pa = reinterpret_cast<const uint4*>(ka);
+  const uint4* pb = reinterpret_cast<const uint4*>(kb);
+#pragma unroll
+  for (int i = 0; i < HD / 8; i++) ra[i] = pa[i];
+#pragma unroll
+  for (int i = 0; i < HD / 8; i++) rb[i] = pb[i];
+  float a = -0.0f, b = -0.0f;
+#pragma unroll
+  for (int i = 0; i < HD / 8; i++) {
+    const uint32_t wa[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+    const uint32_t wb[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float q0 = s_q[8 * i + 2 * j], q1 = s_q[8 * i + 2 * j + 1];
+      a += q0 * f16_operand(static_cast<uint16_t>(wa[j] & 0xffffu));
+      b += q0 * f16_operand(static_cast<uint16_t>(wb[j] & 0xffffu));
+      a += q1 * f16_operand(static_cast<uint16_t>(wa[j] >> 16));
+      b += q1 * f16_operand(static_cast<uint16_t>(wb[j] >> 16));
+    }
+  }
+  *da = a;
+  *db = b;
+}
+
 // Scores of rows 0..n into sc; returns the workgroup-wide max (every lane).
+// Compiled f16 widths take a lane's rows two at a time.
 template <int HD, bool F16>
 __device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, float* sc) {
   using T = typename Elem<F16>::T;
@@ -171,6 +204,22 @@ __device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, flo
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));
   const T* kb = static_cast<const T*>(J.k) + (size_t)J.kvh * hd;
   float mx = -INFINITY;
+  if constexpr (HD > 0 && F16) {
+    for (int t = tid; t < n; t += 2 * kNT) {
+      const int t2 = t + kNT;
+      float da, db;
+      row_dot2_f16<HD>(L.q, kb + (size_t)t * J.kv_stride, kb + (size_t)min(t2, n - 1) * J.kv_stride, &da, &db);
+      const float s = da * scale;
+      sc[t] = s;
+      mx = fmaxf(mx, s);
+      if (t2 < n) {
+        const float s2 = db * scale;
+        sc[t2] = s2;
+        mx = fmaxf(mx, s2);
+      }
+    }
+    return mx;
+  }
   for (int t = tid; t < n; t += kNT) {
     float s = row_dot<HD, F16>(L.q, kb + (size_t)t * J.kv_stride, hd) * scale;
     sc[t] = s;

@@ -1196,7 +1196,7 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
   if (n_tok == 0) return kOk;
   for (int i = 1; i < n; i++)
     PRANA_CHECK(ms[i].kind == ms[0].kind && ms[i].cols == ms[0].cols, "gemv_multi: matrices must share kind and cols");
-  if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens || gemv_skinny(ms[0].kind, n_tok)) {
+  if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
       if (rc) return rc;

@@ -68,10 +68,11 @@ struct GemvOut {
 // Token counts up to this use the weight-streaming decode kernel (and
 // launch_gemv_act); larger batches use the tiled kernel.
 constexpr size_t kGemvDecodeMaxTokens = 16;
-// launch_gemv over block-32 kinds (Q8F, Q8_0, Q4_0) takes batches of this
-// many tokens to the skinny matrix-core kernel (launch_gemv_multi runs such
-// batches matrix by matrix).
-constexpr size_t kGemvSkinnyMinTokens = 5;
+// launch_gemv over block-32 kinds (Q8F, Q8_0, Q4_0) takes batches of
+// kGemvSkinnyMinTokens..kGemvSkinnyMaxTokens tokens to the skinny
+// matrix-core kernel; smaller batches stay on the decode kernel, which also
+// keeps the fused Q|K|V and gate|up launches up to kGemvDecodeMaxTokens.
+constexpr size_t kGemvSkinnyMinTokens = 9;
 constexpr size_t kGemvSkinnyMaxTokens = 64;
 inline bool gemv_skinny(int kind, size_t n_tok) {
   return (kind == kKindQ8F || kind == kKindQ8_0 || kind == kKindQ4_0) && n_tok >= kGemvSkinnyMinTokens &&

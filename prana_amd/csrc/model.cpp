@@ -270,8 +270,7 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
 
 int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s) {
   const size_t H = c.hidden_dim;
-  const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens &&
-                    !gemv_skinny(gate.d.kind, n);
+  const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens;
   if (fuse) {
     return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {
       return launch_gemv_act(gate.d, up.d, c.act, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n,

@@ -97,6 +97,64 @@ def run(manifest_path):
     print(f"wrote {len(cases)} cases to {manifest_path}", file=sys.stderr)
 
 
+def run_models():
+    """End-to-end passes of the model configurations (wall clock of the
+    library's own prefill / decode timers; weights random-init, synthetic
+    prompts): C0 greedy decode, C2 2048-token prefill + 512-token decode, C4
+    plain and speculative (k = 4, 8) decode after a 512-token prefill."""
+    import prana_amd as P
+    from prana_amd import models as M
+
+    rng = np.random.default_rng(20261202)
+    rows = []
+
+    def rec(config, case, st, extra=None):
+        r = {"config": config, "case": case, "prompt_tokens": st.prompt_tokens,
+             "generated_tokens": st.generated_tokens,
+             "prefill_tok_s": round((st.prompt_tokens - 1) / st.prefill_seconds, 1) if st.prefill_seconds > 0 else None,
+             "decode_tok_s": round(st.generated_tokens / st.decode_seconds, 1) if st.decode_seconds > 0 else None}
+        r.update(extra or {})
+        rows.append(r)
+        print(json.dumps(r), file=sys.stderr, flush=True)
+
+    g = P.Model(M.C0, M.c0_tensors(seed=1))
+    prompt = rng.integers(0, M.C0["vocab_size"], 5).astype(np.uint32)
+    g.generate(prompt, 16)
+    _, st = g.generate(prompt, 256)
+    rec("C0", "15M shape, Q8_0, 5-token prompt, greedy to position 256", st)
+    del g
+
+    g = P.Model(M.C2, M.c2_tensors(seed=2))
+    prompt = rng.integers(0, M.C2["vocab_size"], 2048).astype(np.uint32)
+    g.generate(prompt[:64], 8)
+    _, st = g.generate(prompt, 512)
+    rec("C2", "qwen2-0.5B shape, Q4_K/Q6_K mix, 2048-token prefill + 512 greedy tokens", st)
+    del g
+
+    g = P.Model(M.C4, M.c4_tensors(seed=4))
+    dcfg = M.c4_draft_config()
+    draft = P.Model(dcfg, M.synth_tensors(dcfg, M.types_c0, 1))
+    prompt = rng.integers(0, M.C4["vocab_size"], 512).astype(np.uint32)
+    g.generate(prompt[:16], 4)
+    plain, st = g.generate(prompt, 128)
+    rec("C4", "7B shape, Q4_0, 512-token prefill + 128 greedy tokens", st)
+    for k in (4, 8):
+        spec, st = P.generate_speculative(g, draft, prompt, 128, k)
+        rec("C4", f"speculative, 15M-shape draft, k={k}", st,
+            {"proposed": st.proposed, "accepted": st.accepted, "equals_plain": bool(list(spec) == list(plain))})
+    return rows
+
+
+def models_table(rows):
+    out = ["| config | case | prefill tok/s | decode tok/s | note |", "|---|---|---:|---:|---|"]
+    for r in rows:
+        note = ""
+        if "proposed" in r:
+            note = f"accepted {r['accepted']}/{r['proposed']} drafts; stream equals plain greedy: {r['equals_plain']}"
+        out.append(f"| {r['config']} | {r['case']} | {r['prefill_tok_s']} | {r['decode_tok_s']} | {note} |")
+    return "\n".join(out)
+
+
 def summarize(db, manifest_path):
     cases = json.load(open(manifest_path))
     c = sqlite3.connect(db)
@@ -128,9 +186,12 @@ def summarize(db, manifest_path):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--summarize", metavar="DB")
+    ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
-    if args.summarize:
+    if args.models:
+        print(models_table(run_models()))
+    elif args.summarize:
         summarize(args.summarize, args.manifest)
     else:
         run(args.manifest)
