@@ -1145,6 +1145,246 @@ int launch_gemm_skinny(const DevMat& m, const int8_t* q, const float* sa, const 
   return launch_skinny_tt<KIND, 4>(m, q, sa, sums, n_tok, o, s);
 }
 
+// ---- K-quant batches (Q4_K, Q6_K) on the 16x16x32 int8 matrix cores
+// The same tiling and LDS staging as the skinny kernel, with chunks of two
+// 256-element super-blocks. One MFMA step is one 32-element group:
+//   Q4_K: s = sum a*q over the group's nibbles (unsigned, one MFMA), then
+//         term = sa*((d*sc)*float(s) - (dmin*m)*float(sum_a))   (kquant.rs:257-282)
+//   Q6_K: q - 32 as signed bytes; the group's two 16-element sub-blocks are
+//         two MFMAs whose activation operands zero the other half, then
+//         term = ((d*sa)*float(sc))*float(isum16), sub-block 0 first   (kquant.rs:287-318)
+// Every output folds its terms in element order.
+constexpr int kKqCS = 2;  // super-blocks per staged chunk
+
+template <int KIND, int RW, int TT>
+struct KqLayout {
+  static constexpr int NT = 64 * RW * TT;
+  static constexpr int ROWS = 16 * RW, TOKS = 16 * TT;
+  static constexpr int UB = KIND == kKindQ4_K ? 144 : 208;  // quant-array bytes per super-block
+  static constexpr int WSTR = kKqCS * UB + 16;               // padded staged weight row
+  static constexpr int ASTR = kKqCS * 256 + 16;              // padded staged activation row
+  static constexpr int DSTR = kKqCS + 1;                     // Q6_K d words per staged row
+  static constexpr int NG = kKqCS * 8;                       // 32-element groups per chunk
+  static constexpr int A_OFF = ROWS * WSTR;
+  static constexpr int D_OFF = A_OFF + TOKS * ASTR;
+  static constexpr int SA_OFF = D_OFF + ROWS * DSTR * 4;
+  static constexpr int SM_OFF = SA_OFF + NG * TOKS * 4;
+  static constexpr int BYTES = SM_OFF + NG * TOKS * 4;
+  static constexpr int WPR = kKqCS * UB / 16;  // 16-byte pieces per row
+  static constexpr int WP = ROWS * WPR, AP = TOKS * kKqCS * 16, DP = ROWS * kKqCS, SP = TOKS * NG;
+  static constexpr int WPL = (WP + NT - 1) / NT, APL = (AP + NT - 1) / NT;
+  static constexpr int DPL = (DP + NT - 1) / NT, SPL = (SP + NT - 1) / NT;
+};
+
+template <int KIND, int RW, int TT>
+struct KqRegs {
+  using L = KqLayout<KIND, RW, TT>;
+  sk_i4 w[L::WPL], a[L::APL];
+  uint32_t d[L::DPL];
+  float sa[L::SPL];
+  int sm[L::SPL];
+};
+
+template <int KIND, int RW, int TT>
+__global__ __launch_bounds__(64 * RW * TT) void gemm_kq_kernel(DevMat m, const int8_t* __restrict__ q,
+                                                               const float* __restrict__ sa,
+                                                               const int* __restrict__ sums, int n_tok, GemvOut o) {
+  static_assert(KIND == kKindQ4_K || KIND == kKindQ6_K, "K-quant kinds");
+  using L = KqLayout<KIND, RW, TT>;
+  {  // blockIdx.y: this workgroup's group of TOKS tokens
+    const size_t t0 = (size_t)blockIdx.y * L::TOKS;
+    q += t0 * m.cols;
+    sa += t0 * (m.cols / 32);
+    sums += t0 * (m.cols / 32);
+    o.out += t0 * o.ldo;
+    n_tok = min(n_tok - static_cast<int>(t0), L::TOKS);
+  }
+  extern __shared__ int4 kq_smem[];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(kq_smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rtile = wave % RW, ttile = wave / RW;
+  const int j = lane & 15, kg = lane >> 4;
+  const int K = static_cast<int>(m.cols), G = K / 32, NB = K / 256, R = static_cast<int>(m.rows);
+  const int row0 = static_cast<int>(blockIdx.x) * L::ROWS;
+  const int n_chunks = (NB + kKqCS - 1) / kKqCS;
+
+  auto load = [&](int c) __attribute__((always_inline)) {
+    KqRegs<KIND, RW, TT> r;
+    const int sb0 = c * kKqCS;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = min(tid + L::NT * i, L::WP - 1);
+      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int sb = min(sb0 + pr / (L::UB / 16), NB - 1);
+      r.w[i] = *reinterpret_cast<const sk_i4*>(m.qs + ((size_t)rr * NB + sb) * L::UB + (pr % (L::UB / 16)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = min(tid + L::NT * i, L::AP - 1);
+      const int t = min(p / (kKqCS * 16), n_tok - 1), pr = p % (kKqCS * 16);
+      const int sb = min(sb0 + pr / 16, NB - 1);
+      r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)sb * 256 + (pr % 16) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = min(tid + L::NT * i, L::DP - 1);
+      const size_t gi = (size_t)min(row0 + p / kKqCS, R - 1) * NB + min(sb0 + p % kKqCS, NB - 1);
+      r.d[i] = KIND == kKindQ6_K ? reinterpret_cast<const uint16_t*>(m.sc)[gi] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = min(tid + L::NT * i, L::SP - 1);
+      const size_t gi = (size_t)min(p / L::NG, n_tok - 1) * G + min(sb0 * 8 + p % L::NG, G - 1);
+      r.sa[i] = sa[gi];
+      r.sm[i] = sums[gi];
+    }
+    return r;
+  };
+  auto store = [&](const KqRegs<KIND, RW, TT>& r, int buf) __attribute__((always_inline)) {
+    uint8_t* b = lds + buf * L::BYTES;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::WP) *reinterpret_cast<sk_i4*>(b + (p / L::WPR) * L::WSTR + (p % L::WPR) * 16) = r.w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::AP)
+        *reinterpret_cast<sk_i4*>(b + L::A_OFF + (p / (kKqCS * 16)) * L::ASTR + (p % (kKqCS * 16)) * 16) = r.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::DP) reinterpret_cast<uint32_t*>(b + L::D_OFF)[(p / kKqCS) * L::DSTR + p % kKqCS] = r.d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = tid + L::NT * i;
+      if (p < L::SP) {
+        reinterpret_cast<float*>(b + L::SA_OFF)[(p % L::NG) * L::TOKS + p / L::NG] = r.sa[i];
+        reinterpret_cast<int*>(b + L::SM_OFF)[(p % L::NG) * L::TOKS + p / L::NG] = r.sm[i];
+      }
+    }
+  };
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int buf, int c) __attribute__((always_inline)) {
+    const uint8_t* b = lds + buf * L::BYTES;
+    const uint8_t* arow = b + L::A_OFF + (ttile * 16 + j) * L::ASTR + 8 * kg;
+    const uint8_t* wrow = b + (rtile * 16 + j) * L::WSTR;
+    const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + (rtile * 16 + j) * L::DSTR;
+    const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + ttile * 16 + 4 * kg;
+    const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + ttile * 16 + 4 * kg;
+    const int nlive = min(kKqCS, NB - c * kKqCS);  // uniform
+#pragma unroll
+    for (int sbl = 0; sbl < kKqCS; sbl++) {
+      const uint8_t* blk = wrow + sbl * L::UB;
+      const bool live = sbl < nlive;
+#pragma unroll
+      for (int g32 = 0; g32 < 8; g32++) {
+        const int gl = sbl * 8 + g32;  // group within the chunk
+        const long av = *reinterpret_cast<const long*>(arow + sbl * 256 + g32 * 32);
+        const float4 s4 = *reinterpret_cast<const float4*>(sab + gl * L::TOKS);
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        const v4i_t z = {0, 0, 0, 0};
+        if constexpr (KIND == kKindQ4_K) {
+          const int4 m4 = *reinterpret_cast<const int4*>(smb + gl * L::TOKS);
+          const int mv[4] = {m4.x, m4.y, m4.z, m4.w};
+          const long raw = *reinterpret_cast<const long*>(blk + 16 + (g32 >> 1) * 32 + 8 * kg);
+          const long nib = (g32 & 1) ? ((raw >> 4) & 0x0F0F0F0F0F0F0F0FL) : (raw & 0x0F0F0F0F0F0F0F0FL);
+          const v4i_t cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, nib, z, 0, 0, 0);
+          const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
+          const float d = f16_to_f32(static_cast<uint16_t>(dd & 0xffffu));
+          const float dmin = f16_to_f32(static_cast<uint16_t>(dd >> 16));
+          int sc, mn;
+          Fmt<kKindQ4_K>::scale_min(g32, blk + 4, sc, mn);
+          const float dsc = d * static_cast<float>(sc), dmn = dmin * static_cast<float>(mn);
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const float t = acc[v] + sv[v] * (dsc * static_cast<float>(cc[v]) - dmn * static_cast<float>(mv[v]));
+            acc[v] = live ? t : acc[v];
+          }
+        } else {
+          const int half = g32 >> 2, g = g32 & 3;
+          const long ql = *reinterpret_cast<const long*>(blk + half * 64 + (g & 1) * 32 + 8 * kg);
+          const long qh = *reinterpret_cast<const long*>(blk + 128 + half * 32 + 8 * kg);
+          const long nib = g < 2 ? (ql & 0x0F0F0F0F0F0F0F0FL) : ((ql >> 4) & 0x0F0F0F0F0F0F0F0FL);
+          const long q6 = nib | (((qh >> (2 * g)) & 0x0303030303030303L) << 4);  // 0..63 per byte
+          // q - 32 per byte: add 0x80, subtract 0x20 (no borrow leaves a byte), flip the top bit
+          const long qs = ((q6 | static_cast<long>(0x8080808080808080ULL)) - 0x2020202020202020L) ^
+                          static_cast<long>(0x8080808080808080ULL);
+          const v4i_t c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kg < 2 ? av : 0L, qs, z, 0, 0, 0);
+          const v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kg < 2 ? 0L : av, qs, z, 0, 0, 0);
+          const float d = f16_operand(static_cast<uint16_t>(drow[sbl]));
+          const int8_t* scp = reinterpret_cast<const int8_t*>(blk + 192 + half * 8 + g * 2);
+          const float sc0 = static_cast<float>(scp[0]), sc1 = static_cast<float>(scp[1]);
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const float ds = d * sv[v];
+            float t = acc[v] + ds * sc0 * static_cast<float>(c0[v]);
+            t = t + ds * sc1 * static_cast<float>(c1[v]);
+            acc[v] = live ? t : acc[v];
+          }
+        }
+        if (g32 % 4 == 3) asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]) : "memory");
+      }
+    }
+  };
+
+  KqRegs<KIND, RW, TT> r0 = load(0), r1;
+  store(r0, 0);
+  if (n_chunks > 1) r0 = load(1);
+  if (n_chunks > 2) r1 = load(2);
+  __syncthreads();
+  for (int c = 0; c < n_chunks; c += 2) {
+    compute(0, c);
+    if (c + 1 < n_chunks) store(r0, 1);
+    if (c + 3 < n_chunks) r0 = load(c + 3);
+    __syncthreads();
+    if (c + 1 >= n_chunks) break;
+    compute(1, c + 1);
+    if (c + 2 < n_chunks) store(r1, 0);
+    if (c + 4 < n_chunks) r1 = load(c + 4);
+    __syncthreads();
+  }
+  const int n_row = row0 + rtile * 16 + j;
+  if (n_row < R) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int t = 16 * ttile + 4 * kg + v;
+      if (t < n_tok) store_out(o, t, n_row, acc[v]);
+    }
+  }
+}
+
+template <int KIND, int RW, int TT>
+int launch_kq_t(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok, const GemvOut& o,
+                hipStream_t s) {
+  using L = KqLayout<KIND, RW, TT>;
+  static const bool attr_ok = [] {
+    return L::BYTES * 2 <= 65536 ||
+           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kq_kernel<KIND, RW, TT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+  }();
+  PRANA_CHECK(attr_ok, "gemm_kq: LDS size not granted");
+  hipLaunchKernelGGL((gemm_kq_kernel<KIND, RW, TT>),
+                     dim3((m.rows + L::ROWS - 1) / L::ROWS, (n_tok + L::TOKS - 1) / L::TOKS), dim3(L::NT),
+                     L::BYTES * 2, s, m, q, sa, sums, (int)n_tok, o);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// Batches of any size: grid (row tiles, groups of 64 tokens).
+template <int KIND>
+int launch_gemm_kq(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                   const GemvOut& o, hipStream_t s) {
+  PRANA_CHECK(m.cols % 256 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30) && n_tok <= (1u << 24),
+              "gemm_kq: shape out of range");
+  const bool two = (m.rows + 31) / 32 * ((n_tok + 63) / 64) >= 256;  // 32-row tiles still fill the GPU
+  if (two) return launch_kq_t<KIND, 2, 4>(m, q, sa, sums, n_tok, o, s);
+  return launch_kq_t<KIND, 1, 4>(m, q, sa, sums, n_tok, o, s);
+}
+
 template <int KIND>
 int launch_q(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok, const GemvOut& o,
              hipStream_t s) {
@@ -1266,8 +1506,8 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
     case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
     case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
     case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ4_K: return launch_q<kKindQ4_K>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ6_K: return launch_q<kKindQ6_K>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ4_K: return launch_gemm_kq<kKindQ4_K>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ6_K: return launch_gemm_kq<kKindQ6_K>(m, q, sa, sums, n_tok, o, s);
   }
   return fail(kErrUnsupported, "gemv: unknown matrix kind");
 }

@@ -145,6 +145,23 @@ def test_c2_qwen2_05b_short_decode_token_identical():
     assert same_bits(gc.forward(int(prompt[8]), 8), oc.forward(int(prompt[8]), 8))
 
 
+def test_kquant_prefill_and_verify_batches_bitexact():
+    # Q4_K / Q6_K weights (every width a multiple of 256) with prompt and
+    # verify batches of more than 16 tokens: the K-quant matrix-core kernel
+    cfg = M.config(512, 1536, 2, 8, 2, 1000, 128, head_dim=64, rope_theta=1e6, norm_eps=1e-6, rope_neox=1)
+    t = M.synth_tensors(cfg, M.types_c2, 5, biases=True)
+    assert {t[k][0] for k in t if k.endswith("ffn_down.weight")} == {P.Q6_K}
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(128), o.cache(128)
+    prompt = np.random.default_rng(5).integers(0, cfg["vocab_size"], 70).astype(np.uint32)
+    gc.prefill(prompt[:40])
+    oc.prefill(prompt[:40])
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(gc.read(layer, 1, 40), oc.read(layer, 1, 40))
+    batch = [int(x) for x in prompt[40:70]]
+    assert same_bits(gc.forward_batch(batch, 40), oc.forward_batch(batch, 40))
+
+
 # ------------------------------------------------------------------ config 4: 7B shape, Q4_0
 @pytest.fixture(scope="module")
 def c4():
