@@ -636,6 +636,176 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
   }
 }
 
+// ---------------------------------------------------------------- wide path
+// Verify batches (two or more query rows) over cache windows below
+// kSplitMinRows with 64/128-wide heads: one 1024-lane workgroup per (query
+// row, head) does the whole head. Scores: one lane per cache row (a second
+// row past 1024), into LDS at exact::run_pad positions; softmax with the
+// exact sum over that LDS row; P·V like the split path's PV launch (fold
+// waves for the head's dims, the other waves form the products of the next
+// chunk from the LDS probabilities and V). A single decode row stays on the
+// one-launch kernel: with one workgroup per head the row-per-lane K gathers
+// of 32 workgroups are slower than its 128 (23.0 against 18.7 us at 512
+// rows), while 8 verify rows gain (24.4 against 31.8 us).
+constexpr int kWideNT = 1024;
+constexpr int kWideMax = kSplitMinRows - 1;  // rows a wide workgroup takes at most
+constexpr size_t kWideMinRows = 256;          // shorter windows stay on the one-launch kernel
+
+template <int HD>
+struct WideCfg {
+  static constexpr int F = HD / 64;                 // fold waves
+  static constexpr int CH = HD == 128 ? 64 : 128;   // rows per PV chunk
+  static constexpr int PL = kWideNT - 64 * F;       // producer lanes
+  static constexpr int TASKS = CH / 4 * (HD / 2);   // (row quad, dim pair) per chunk
+  static constexpr int PER = (TASKS + PL - 1) / PL;
+  static constexpr int SC = exact::run_pad(kWideMax - 1) + 1;  // probability words
+};
+
+template <int HD>
+__global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restrict__ q,
+                                                            const uint16_t* __restrict__ k,
+                                                            const uint16_t* __restrict__ v, int pos0, int n_heads,
+                                                            int group, float* __restrict__ out,
+                                                            int8_t* __restrict__ qd, float* __restrict__ qsa,
+                                                            int* __restrict__ qsum) {
+  using C = WideCfg<HD>;
+  __shared__ __align__(16) float s_q[HD];
+  __shared__ float s_red[kWideNT / 64];
+  __shared__ __align__(16) float s_p[C::SC];
+  __shared__ __align__(16) float s_prod[2][C::CH * HD];
+  const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+  const int n = pos0 + i + 1;  // <= kWideMax rows
+  const int kvh = h / group;
+  const int kv_stride = (n_heads / group) * HD;
+  for (int d = tid; d < HD; d += kWideNT) s_q[d] = q[((size_t)i * n_heads + h) * HD + d];
+  __syncthreads();
+  // ---- scores (attention.rs:165-185): (fold_d q[d]*k_t[d] from -0.0) * (1/sqrt(hd))
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  const uint16_t* kb = k + (size_t)kvh * HD;
+  const int t1 = tid, t2 = tid + kWideNT;
+  float mx = -INFINITY;
+  if (t1 < n) {
+    const float s1 = row_dot<HD, true>(s_q, kb + (size_t)t1 * kv_stride, HD) * scale;
+    s_p[exact::run_pad(t1)] = s1;
+    mx = s1;
+  }
+  if (t2 < n) {
+    const float s2 = row_dot<HD, true>(s_q, kb + (size_t)t2 * kv_stride, HD) * scale;
+    s_p[exact::run_pad(t2)] = s2;
+    mx = fmaxf(mx, s2);
+  }
+  mx = wave_max_f32(mx);
+  if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kWideNT / 64; w++) mx = fmaxf(mx, s_red[w]);
+  float e1 = 0.0f, e2 = 0.0f;
+  if (t1 < n) s_p[exact::run_pad(t1)] = e1 = dev_expf(s_p[exact::run_pad(t1)] - mx);
+  if (t2 < n) s_p[exact::run_pad(t2)] = e2 = dev_expf(s_p[exact::run_pad(t2)] - mx);
+  __syncthreads();
+  // softmax sum in the reference's left-to-right order (norms.rs:53)
+  const float sum = exact::block_seq_sum_short<kWideNT>([](int t) { return s_p[exact::run_pad(t)]; }, n);
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  if (t1 < n) s_p[exact::run_pad(t1)] = e1 * inv;
+  if (t2 < n) s_p[exact::run_pad(t2)] = e2 * inv;
+  __syncthreads();
+
+  // ---- P·V: fold lanes (waves 0..F-1) own the head's dims; the others form
+  // the products of the next chunk as [row/4][dim][row%4]. Rows past n are
+  // zero products, which leave the fold (started from +0.0) unchanged.
+  const bool folder = tid < 64 * C::F;
+  const int pl = tid - 64 * C::F;
+  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(v + (size_t)kvh * HD);
+  const int kv_words = kv_stride / 2;
+  const int n_chunks = (n + C::CH - 1) / C::CH;
+  uint32_t vr[C::PER][4];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int kk = 0; kk < C::PER; kk++) {
+      const int task = min(pl + C::PL * kk, C::TASKS - 1);
+      const int dp = task % (HD / 2), rq = task / (HD / 2);
+      const int t = c * C::CH + 4 * rq;
+#pragma unroll
+      for (int r = 0; r < 4; r++) vr[kk][r] = v32[(size_t)min(t + r, n - 1) * kv_words + dp];
+    }
+  };
+  auto produce = [&](int c, float* buf) {
+#pragma unroll
+    for (int kk = 0; kk < C::PER; kk++) {
+      const int task = pl + C::PL * kk;
+      if (task >= C::TASKS) break;
+      const int dp = task % (HD / 2), rq = task / (HD / 2);
+      const int t = c * C::CH + 4 * rq;
+      float a[4], b[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const bool live = t + r < n;
+        const float p = s_p[exact::run_pad(min(t + r, n - 1))];
+        a[r] = live ? p * f16_operand(static_cast<uint16_t>(vr[kk][r] & 0xffffu)) : 0.0f;
+        b[r] = live ? p * f16_operand(static_cast<uint16_t>(vr[kk][r] >> 16)) : 0.0f;
+      }
+      float4* dst = reinterpret_cast<float4*>(buf) + rq * HD + 2 * dp;
+      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+      dst[1] = make_float4(b[0], b[1], b[2], b[3]);
+    }
+  };
+  float acc = 0.0f;
+  if (!folder) {
+    fetch(0);
+    produce(0, s_prod[0]);
+    if (n_chunks > 1) fetch(1);
+  }
+  __syncthreads();
+  for (int c = 0; c < n_chunks; c++) {
+    if (folder) {
+      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid;
+#pragma unroll
+      for (int g = 0; g < C::CH / 32; g++) {
+        float4 x[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) x[jj] = src[(g * 8 + jj) * HD];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+          acc += x[jj].x;
+          acc += x[jj].y;
+          acc += x[jj].z;
+          acc += x[jj].w;
+        }
+      }
+    } else if (c + 1 < n_chunks) {
+      produce(c + 1, s_prod[(c + 1) & 1]);
+      if (c + 2 < n_chunks) fetch(c + 2);
+    }
+    __syncthreads();
+  }
+  if (folder) {
+    const size_t gi = ((size_t)i * n_heads + h) * HD + tid;
+    out[gi] = acc;
+    if (qd) {
+      float qscale;
+      int qs;
+      const int qi = quantize_lane(acc, &qscale, &qs);
+      qd[gi] = static_cast<int8_t>(qi);
+      if ((gi & 31) == 0) {
+        qsa[gi >> 5] = qscale;
+        qsum[gi >> 5] = qs;
+      }
+    }
+  }
+}
+
+template <int HD>
+int launch_wide(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, size_t n_q, size_t n_heads,
+                size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, hipStream_t s) {
+  const bool fuse_q = aq && aq->q;  // whole heads are whole 32-blocks
+  if (quantized) *quantized = fuse_q;
+  hipLaunchKernelGGL(attn_wide_kernel<HD>, dim3(n_heads, n_q), dim3(kWideNT), 0, s, q, k, v, (int)pos0,
+                     (int)n_heads, (int)(n_heads / n_kv_heads), out, fuse_q ? aq->q : nullptr,
+                     fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 // grid: (n_heads*dsplit, n_q). Query row i sits at position p0 + i.
 // mode: 0 scalar rows; -1 vector V chunks with a runtime head width;
 // 48/64/128 vector K and V loads with that compiled head width.
@@ -739,6 +909,13 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
   const size_t elem = F16 ? 2 : 4;
   const bool aligned = reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                        (hd * elem) % 16 == 0;
+  if (F16 && aligned && !pos_dev && n_q >= 2 && pos0 + n_q >= kWideMinRows && pos0 + n_q <= (size_t)kWideMax &&
+      (hd == 64 || hd == 128)) {
+    const uint16_t* kc = static_cast<const uint16_t*>(k);
+    const uint16_t* vc = static_cast<const uint16_t*>(v);
+    return hd == 64 ? launch_wide<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s)
+                    : launch_wide<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s);
+  }
   if (F16 && aligned && !pos_dev && scratch && pos0 + n_q >= kSplitMinRows && (hd == 64 || hd == 128)) {
     const uint16_t* kc = static_cast<const uint16_t*>(k);
     const uint16_t* vc = static_cast<const uint16_t*>(v);

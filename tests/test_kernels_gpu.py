@@ -326,11 +326,14 @@ def _cache(n, nkv, hd, seed):
 
 
 # Windows of 2048+ rows with 64/128-wide heads take the three-launch split
-# path (scores, softmax, PV); the rest the one-launch kernel.
+# path (scores, softmax, PV); the rest the one-launch kernel (verify batches
+# of 256..2047 rows: the wide kernel, see test_attention_verify).
 @pytest.mark.parametrize("nh,nkv,hd,pos", [(6, 6, 48, 0), (6, 6, 48, 255), (14, 2, 64, 700), (32, 8, 128, 1030),
                                             (32, 8, 128, 5000), (4, 2, 80, 300), (4, 4, 36, 130), (2, 1, 256, 64),
                                             (32, 8, 128, 2046), (32, 8, 128, 2047), (14, 2, 64, 2600),
-                                            (8, 8, 64, 2048), (32, 8, 128, 16500), (4, 2, 80, 4500)])
+                                            (8, 8, 64, 2048), (32, 8, 128, 16500), (4, 2, 80, 4500),
+                                            (32, 8, 128, 254), (32, 8, 128, 255), (8, 8, 64, 1023),
+                                            (8, 8, 64, 1024), (32, 8, 128, 2045)])
 def test_attention_decode(nh, nkv, hd, pos):
     kc, vc = _cache(pos + 1, nkv, hd, pos)
     q = rng(pos + 3).standard_normal(nh * hd).astype(np.float32)
@@ -379,7 +382,8 @@ def test_attention_decode_special_values(pos):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,seq", [(32, 8, 128, 512, 9), (32, 8, 128, 3000, 8), (32, 8, 128, 2040, 9),
-                                                 (14, 2, 64, 2046, 3)])
+                                                 (14, 2, 64, 2046, 3), (32, 8, 128, 2040, 7), (32, 8, 128, 250, 9),
+                                                 (14, 2, 64, 700, 5)])
 def test_attention_verify(nh, nkv, hd, pos0, seq):
     kc, vc = _cache(pos0 + seq, nkv, hd, 4)
     q = rng(5).standard_normal(seq * nh * hd).astype(np.float32)
