@@ -806,6 +806,171 @@ int launch_wide(const float* q, const uint16_t* k, const uint16_t* v, size_t pos
   return kOk;
 }
 
+// ---------------------------------------------------------------- prefill blocks
+// Prefill attention over the f32 K/V of the window (attention.rs:236-284)
+// with one 256-lane workgroup per (head, block of kPbQ consecutive query
+// rows): each K row a lane fetches serves the block's kPbQ score chains (side
+// by side), and each V element a lane fetches serves kPbQ*hd/256 P·V chains.
+// Row qq of the block attends keys 0..i0+qq; its softmax sum is the exact
+// left-to-right fold, one row after another.
+constexpr int kPbQ = 8;
+constexpr int kPbNT = 256;
+constexpr int kPbMax = 2048;  // window rows a block workgroup takes
+constexpr int kPbW = exact::run_pad(kPbMax - 1) + 1;
+
+template <int HD>
+__global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restrict__ q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, int seq, int n_heads,
+                                                          int group, float* __restrict__ out,
+                                                          int8_t* __restrict__ qd, float* __restrict__ qsa,
+                                                          int* __restrict__ qsum) {
+  static_assert(HD % 4 == 0 && (kPbQ * HD) % kPbNT == 0, "whole chains per lane");
+  constexpr int QPL = kPbQ * HD / kPbNT;  // P·V chains per lane
+  constexpr int QSTEP = kPbNT / HD;       // query rows between a lane's chains
+  __shared__ __align__(16) float s_q[kPbQ][HD];
+  __shared__ __align__(16) float s_sc[kPbQ][kPbW];
+  __shared__ float s_red[kPbQ][kPbNT / 64];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int i0 = blockIdx.y * kPbQ;
+  const int nk = min(i0 + kPbQ, seq);  // keys any row of the block attends
+  const int kvh = h / group;
+  const int kv_dim = (n_heads / group) * HD;
+  for (int e = tid; e < kPbQ * HD; e += kPbNT) {
+    const int qq = e / HD, d = e % HD;
+    s_q[qq][d] = i0 + qq < seq ? q[((size_t)(i0 + qq) * n_heads + h) * HD + d] : 0.0f;
+  }
+  __syncthreads();
+  // ---- scores: (fold_d q[d]*k_t[d] from -0.0) * (1/sqrt(hd)), lane per key row
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+  float mxl[kPbQ];
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) mxl[qq] = -INFINITY;
+  for (int t = tid; t < nk; t += kPbNT) {
+    const float4* kp = reinterpret_cast<const float4*>(k + (size_t)t * kv_dim + (size_t)kvh * HD);
+    float dot[kPbQ];
+#pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) dot[qq] = -0.0f;
+#pragma unroll 4
+    for (int c = 0; c < HD / 4; c++) {
+      const float4 kv = kp[c];
+#pragma unroll
+      for (int qq = 0; qq < kPbQ; qq++) {
+        const float4 qv = reinterpret_cast<const float4*>(s_q[qq])[c];
+        dot[qq] += qv.x * kv.x;
+        dot[qq] += qv.y * kv.y;
+        dot[qq] += qv.z * kv.z;
+        dot[qq] += qv.w * kv.w;
+      }
+    }
+#pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) {
+      if (t <= i0 + qq) {  // causal: row i0+qq attends keys 0..i0+qq
+        const float sv = dot[qq] * scale;
+        s_sc[qq][exact::run_pad(t)] = sv;
+        mxl[qq] = fmaxf(mxl[qq], sv);
+      }
+    }
+  }
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) {
+    const float m = wave_max_f32(mxl[qq]);
+    if ((tid & 63) == 0) s_red[qq][tid >> 6] = m;
+  }
+  __syncthreads();
+  float mx[kPbQ];
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) {
+    mx[qq] = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kPbNT / 64; w++) mx[qq] = fmaxf(mx[qq], s_red[qq][w]);
+  }
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) {
+    const int n = i0 + qq + 1;
+    if (i0 + qq < seq)
+      for (int t = tid; t < n; t += kPbNT) s_sc[qq][exact::run_pad(t)] = dev_expf(s_sc[qq][exact::run_pad(t)] - mx[qq]);
+  }
+  __syncthreads();
+  // softmax sums in the reference's left-to-right order (norms.rs:53), one row at a time
+  float inv[kPbQ];
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) {
+    inv[qq] = 0.0f;
+    if (i0 + qq < seq) {  // uniform
+      const float sum =
+          exact::block_seq_sum_short<kPbNT>([qq](int t) { return s_sc[qq][exact::run_pad(t)]; }, i0 + qq + 1);
+      inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) {
+    const int n = i0 + qq + 1;
+    if (i0 + qq < seq)
+      for (int t = tid; t < n; t += kPbNT) s_sc[qq][exact::run_pad(t)] = s_sc[qq][exact::run_pad(t)] * inv[qq];
+  }
+  __syncthreads();
+  // ---- P·V: lane (d, qg) folds rows qg, qg+QSTEP, ... of dim d over t from +0.0
+  const int d = tid % HD, qg = tid / HD;
+  const float* vcol = v + (size_t)kvh * HD + d;
+  float acc[QPL];
+#pragma unroll
+  for (int c = 0; c < QPL; c++) acc[c] = 0.0f;
+  int t = 0;
+  for (; t + 4 <= nk; t += 4) {
+    float vt[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) vt[u] = vcol[(size_t)(t + u) * kv_dim];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+      for (int c = 0; c < QPL; c++) {
+        const int qq = qg + c * QSTEP;
+        const float nv = acc[c] + s_sc[qq][exact::run_pad(t + u)] * vt[u];
+        acc[c] = t + u <= i0 + qq ? nv : acc[c];
+      }
+  }
+  for (; t < nk; t++) {
+    const float vt = vcol[(size_t)t * kv_dim];
+#pragma unroll
+    for (int c = 0; c < QPL; c++) {
+      const int qq = qg + c * QSTEP;
+      const float nv = acc[c] + s_sc[qq][exact::run_pad(t)] * vt;
+      acc[c] = t <= i0 + qq ? nv : acc[c];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < QPL; c++) {
+    const int qq = qg + c * QSTEP, i = i0 + qq;
+    const bool live = i < seq;
+    const size_t gi = ((size_t)min(i, seq - 1) * n_heads + h) * HD + d;
+    if (live) out[gi] = acc[c];
+    if (qd) {  // 32-lane groups share qq (HD is a multiple of 32 here)
+      float qscale;
+      int qs;
+      const int qi = quantize_lane(live ? acc[c] : 0.0f, &qscale, &qs);
+      if (live) {
+        qd[gi] = static_cast<int8_t>(qi);
+        if ((gi & 31) == 0) {
+          qsa[gi >> 5] = qscale;
+          qsum[gi >> 5] = qs;
+        }
+      }
+    }
+  }
+}
+
+template <int HD>
+int launch_prefill_blk(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
+                       size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, hipStream_t s) {
+  const bool fuse_q = aq && aq->q;
+  if (quantized) *quantized = fuse_q;
+  hipLaunchKernelGGL(attn_prefill_blk<HD>, dim3(n_heads, (seq + kPbQ - 1) / kPbQ), dim3(kPbNT), 0, s, q, k, v,
+                     (int)seq, (int)n_heads, (int)(n_heads / n_kv_heads), out, fuse_q ? aq->q : nullptr,
+                     fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 // grid: (n_heads*dsplit, n_q). Query row i sits at position p0 + i.
 // mode: 0 scalar rows; -1 vector V chunks with a runtime head width;
 // 48/64/128 vector K and V loads with that compiled head width.
@@ -983,6 +1148,11 @@ int launch_attention_prefill(const float* q, const float* k, const float* v, siz
   if (seq == 0) return kOk;
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "attention: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
+  const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0;
+  if (aligned && seq <= (size_t)kPbMax && seq >= 2 * kPbQ && (hd == 64 || hd == 128)) {
+    return hd == 64 ? launch_prefill_blk<64>(q, k, v, seq, n_heads, n_kv_heads, out, aq, quantized, s)
+                    : launch_prefill_blk<128>(q, k, v, seq, n_heads, n_kv_heads, out, aq, quantized, s);
+  }
   return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, aq, quantized, s);
 }
 

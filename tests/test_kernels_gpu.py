@@ -391,8 +391,11 @@ def test_attention_verify(nh, nkv, hd, pos0, seq):
                      O.attention_verify(q, kc, vc, pos0, seq, nh, nkv, hd))
 
 
+# 64/128-wide heads over windows of 16..2048 rows: the block kernel (8 query
+# rows per workgroup); the rest the one-launch kernel
 @pytest.mark.parametrize("seq,nh,nkv,hd", [(1, 2, 2, 16), (37, 14, 2, 64), (64, 6, 6, 48), (300, 4, 2, 128),
-                                            (4200, 2, 1, 16), (50, 3, 3, 20)])
+                                            (4200, 2, 1, 16), (50, 3, 3, 20), (17, 4, 2, 64), (16, 2, 2, 128),
+                                            (511, 32, 8, 128), (2048, 14, 2, 64), (2049, 2, 1, 64)])
 def test_attention_prefill(seq, nh, nkv, hd):
     r = rng(seq)
     q = r.standard_normal(seq * nh * hd).astype(np.float32)
