@@ -891,17 +891,25 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
       for (int t = tid; t < n; t += kPbNT) s_sc[qq][exact::run_pad(t)] = dev_expf(s_sc[qq][exact::run_pad(t)] - mx[qq]);
   }
   __syncthreads();
-  // softmax sums in the reference's left-to-right order (norms.rs:53), one row at a time
-  float inv[kPbQ];
+  // softmax sums in the reference's left-to-right order (norms.rs:53): each
+  // wave folds one row at a time, the waves' rows at once
+  __shared__ float s_inv[kPbQ];
+  static_assert(kPbQ % (kPbNT / 64) == 0, "whole rounds of rows");
 #pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) {
-    inv[qq] = 0.0f;
-    if (i0 + qq < seq) {  // uniform
+  for (int r = 0; r < kPbQ / (kPbNT / 64); r++) {
+    const int qq = r * (kPbNT / 64) + (tid >> 6);
+    if (i0 + qq < seq) {  // wave-uniform; the group barriers are the wave's own
       const float sum =
-          exact::block_seq_sum_short<kPbNT>([qq](int t) { return s_sc[qq][exact::run_pad(t)]; }, i0 + qq + 1);
-      inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
+          exact::group_seq_sum_short<64, kPbNT / 64>([qq](int t) { return s_sc[qq][exact::run_pad(t)]; }, i0 + qq + 1);
+      if ((tid & 63) == 0) s_inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    } else if ((tid & 63) == 0) {
+      s_inv[qq] = 0.0f;
     }
   }
+  __syncthreads();
+  float inv[kPbQ];
+#pragma unroll
+  for (int qq = 0; qq < kPbQ; qq++) inv[qq] = s_inv[qq];
 #pragma unroll
   for (int qq = 0; qq < kPbQ; qq++) {
     const int n = i0 + qq + 1;
@@ -915,19 +923,27 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
   float acc[QPL];
 #pragma unroll
   for (int c = 0; c < QPL; c++) acc[c] = 0.0f;
+  // rows 0..i0 are attended by every query row of the block: no causal test
+  // there, so the probability and V reads of a batch issue together; only
+  // the last kPbQ - 1 keys need the per-row select
   int t = 0;
-  for (; t + 4 <= nk; t += 4) {
-    float vt[4];
+  for (; t + 8 <= i0 + 1; t += 8) {
+    float vt[8], pt[8][QPL];
 #pragma unroll
-    for (int u = 0; u < 4; u++) vt[u] = vcol[(size_t)(t + u) * kv_dim];
+    for (int u = 0; u < 8; u++) vt[u] = vcol[(size_t)(t + u) * kv_dim];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < 8; u++)
 #pragma unroll
-      for (int c = 0; c < QPL; c++) {
-        const int qq = qg + c * QSTEP;
-        const float nv = acc[c] + s_sc[qq][exact::run_pad(t + u)] * vt[u];
-        acc[c] = t + u <= i0 + qq ? nv : acc[c];
-      }
+      for (int c = 0; c < QPL; c++) pt[u][c] = s_sc[qg + c * QSTEP][exact::run_pad(t + u)];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+#pragma unroll
+      for (int c = 0; c < QPL; c++) acc[c] = acc[c] + pt[u][c] * vt[u];
+  }
+  for (; t <= i0; t++) {
+    const float vt = vcol[(size_t)t * kv_dim];
+#pragma unroll
+    for (int c = 0; c < QPL; c++) acc[c] = acc[c] + s_sc[qg + c * QSTEP][exact::run_pad(t)] * vt;
   }
   for (; t < nk; t++) {
     const float vt = vcol[(size_t)t * kv_dim];

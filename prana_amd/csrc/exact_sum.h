@@ -340,6 +340,28 @@ __device__ __forceinline__ void seg_push(SegAcc& acc, bool cross, Pair pr) {
   acc.c += cross ? 1 : 0;
 }
 
+// Barrier and OR-vote of a lane group (see group_seq_sum_pred): the
+// workgroup for NG == 1, else the calling wave.
+template <int NG>
+__device__ __forceinline__ void group_sync() {
+  if constexpr (NG == 1) {
+    __syncthreads();
+  } else {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+template <int NG>
+__device__ __forceinline__ bool group_or(bool p) {
+  if constexpr (NG == 1) {
+    return __syncthreads_or(p) != 0;
+  } else {
+    group_sync<NG>();
+    return __builtin_amdgcn_ballot_w64(p) != 0;
+  }
+}
+
 // The fold of term(0..n) with n > kPredHead and n - kPredHead <= NT *
 // kPredMaxPerLane, terms >= 0; term(i) must return the same value in every
 // lane and every call (an LDS or global read, or a pure function of one).
@@ -347,19 +369,36 @@ __device__ __forceinline__ void seg_push(SegAcc& acc, bool cross, Pair pr) {
 // them out so that runs of C consecutive positions in different lanes fall
 // in different banks. Returns the value in every lane and *ok; *ok is false
 // (value meaningless) when a term is not finite or the prediction failed.
-// Must be called by all NT lanes; contains five barriers.
-template <int NT, class Term>
-__device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
+// Must be called by all NT lanes; contains five group barriers.
+// NG lane groups of NT lanes each evaluate their own sum at once (group g is
+// lanes [g*NT, g*NT + NT) of the workgroup, with its own LDS records): NG ==
+// 1 is the whole workgroup; NG > 1 needs NT == 64, one sum per wave, and
+// then the barriers are wave-level (a wave's LDS accesses complete in issue
+// order, so compiler fences suffice).
+template <int NT, int NG, class Term>
+__device__ inline float group_seq_sum_pred(Term a, int n, bool* ok) {
+  static_assert(NG == 1 || NT == 64, "groups are the workgroup or single waves");
   constexpr int W = NT / 64;
   static_assert(kPredMaxCross < 64, "the walk keeps one segment per lane of wave 0");
-  __shared__ float s_fw[W];
-  __shared__ int s_epl[W], s_sw[3 * W];
-  __shared__ int s_tot[2 * (kPredMaxCross + 1)];
-  __shared__ float s_ct[kPredMaxCross + 1];
-  __shared__ int s_ce[kPredMaxCross + 1];
-  __shared__ float s_head, s_res;
-  __shared__ int s_ok;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float s_fw_[NG][W];
+  __shared__ int s_epl_[NG][W], s_sw_[NG][3 * W];
+  __shared__ int s_tot_[NG][2 * (kPredMaxCross + 1)];
+  __shared__ float s_ct_[NG][kPredMaxCross + 1];
+  __shared__ int s_ce_[NG][kPredMaxCross + 1];
+  __shared__ float s_head_[NG], s_res_[NG];
+  __shared__ int s_ok_[NG];
+  const int g = NG > 1 ? static_cast<int>(threadIdx.x) / NT : 0;
+  float* s_fw = s_fw_[g];
+  int* s_epl = s_epl_[g];
+  int* s_sw = s_sw_[g];
+  int* s_tot = s_tot_[g];
+  float* s_ct = s_ct_[g];
+  int* s_ce = s_ce_[g];
+  float& s_head = s_head_[g];
+  float& s_res = s_res_[g];
+  int& s_ok = s_ok_[g];
+  const int tid = NG > 1 ? static_cast<int>(threadIdx.x) % NT : static_cast<int>(threadIdx.x);
+  const int lane = tid & 63, wave = tid >> 6;
   const int C = (n - kPredHead + NT - 1) / NT;
   const int i0 = kPredHead + tid * C;
   const int nv = max(0, min(C, n - i0));
@@ -384,7 +423,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   });
   const float inc = scan_add_f32(ls);
   if (lane == 63) s_fw[wave] = inc;
-  if (__syncthreads_or(bad)) {
+  if (group_or<NG>(bad)) {
     *ok = false;
     return 0.0f;
   }
@@ -481,7 +520,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
   }
   int prev_last = wave_shr1(ep_last);
   if (lane == 63) s_epl[wave] = ep_last;
-  __syncthreads();
+  group_sync<NG>();
   if (lane == 0) prev_last = wave > 0 ? s_epl[wave - 1] : binade_code(sH, R);
   int next_first = __shfl_down(ep_first, 1, 64);
   const bool cross0 = seg_break(ep_first, prev_last);
@@ -495,9 +534,10 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
     s_sw[3 * wave + 2] = incs.c;
   }
   // the first lane of each wave needs the next wave's first binade
-  __shared__ int s_epf[W];
+  __shared__ int s_epf_[NG][W];
+  int* s_epf = s_epf_[g];
   if (lane == 0) s_epf[wave] = ep_first;
-  __syncthreads();
+  group_sync<NG>();
   if (lane == 63) next_first = wave + 1 < W ? s_epf[wave + 1] : 0;
   SegAcc run{Pair{0, 0}, 0}, all;
   {
@@ -565,7 +605,7 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
       s_tot[2 * fin.c + 1] = fin.p.o;
     }
   }
-  __syncthreads();
+  group_sync<NG>();
   // the walk: wave 0 holds segment j in lane j and carries the exact value
   // from segment to segment
   if (wave == 0) {
@@ -595,11 +635,16 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
       s_ok = good;
     }
   }
-  __syncthreads();
+  group_sync<NG>();
   *ok = s_ok != 0;
   return s_res;
 }
 
+
+template <int NT, class Term>
+__device__ __forceinline__ float block_seq_sum_pred(Term a, int n, bool* ok) {
+  return group_seq_sum_pred<NT, 1>(a, n, ok);
+}
 
 // The sequential fold of a[0..n), a[i] >= 0, evaluated by an NT-lane
 // workgroup (blockDim.x == NT); every lane returns the same value. Must be
@@ -613,23 +658,30 @@ __device__ inline float block_seq_sum_pred(Term a, int n, bool* ok) {
 // owns the contiguous run [t*C, t*C + C), C = ceil(n/NT)) and streaming
 // longer sums from `a`; non-finite terms again run on one lane.
 // The same fold for sums of at most kPredHead + NT * kPredMaxPerLane terms
-// given by a term function (see block_seq_sum_pred): the predicted-binade scan
-// with a one-lane fallback.
-template <int NT, class Term>
-__device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
-  __shared__ float s_short;
+// given by a term function (see group_seq_sum_pred): the predicted-binade
+// scan with a one-lane fallback, evaluated by NG lane groups at once, each
+// with its own term function and n (uniform within the group); every lane of
+// a group gets its group's sum.
+template <int NT, int NG, class Term>
+__device__ __forceinline__ float group_seq_sum_short(Term term, int n) {
+  __shared__ float s_short[NG];
+  const int g = NG > 1 ? static_cast<int>(threadIdx.x) / NT : 0;
   if (n > kPredHead) {
     bool ok;
-    const float v = block_seq_sum_pred<NT>(term, n, &ok);
+    const float v = group_seq_sum_pred<NT, NG>(term, n, &ok);
     if (ok) return v;
   }
-  if (threadIdx.x == 0) {
+  if (threadIdx.x % NT == 0) {
     float s = -0.0f;
     for (int i = 0; i < n; i++) s += term(i);
-    s_short = s;
+    s_short[g] = s;
   }
-  __syncthreads();
-  return s_short;
+  group_sync<NG>();
+  return s_short[g];
+}
+template <int NT, class Term>
+__device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
+  return group_seq_sum_short<NT, 1>(term, n);
 }
 
 template <int NT, bool PADDED, int CMAX = 16>
