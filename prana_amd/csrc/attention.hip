@@ -362,13 +362,14 @@ __host__ __device__ constexpr size_t split_stride(size_t ctx_cap) {
 template <int HD>
 __global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ k, int pos0,
-                                                                int n_heads, int group, int n_kv,
-                                                                float* __restrict__ sc, int sc_stride) {
+                                                                const int* __restrict__ pos_dev, int n_heads,
+                                                                int group, int n_kv, float* __restrict__ sc,
+                                                                int sc_stride) {
   __shared__ __align__(16) float s_q[4 * HD];
   const int nhb = (group + 3) / 4;
   const int hb = blockIdx.y % nhb, ik = blockIdx.y / nhb;
   const int i = ik / n_kv, kvh = ik % n_kv;
-  const int n = pos0 + i + 1;
+  const int n = (pos_dev ? *pos_dev : pos0) + i + 1;
   const int row0 = blockIdx.x * kSplitRows;
   if (row0 >= n) return;  // uniform, before the barrier
   const int h0 = kvh * group + 4 * hb;  // first head of the block
@@ -435,12 +436,12 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __r
 constexpr int kSmPer = 36;
 template <bool IN_LDS>
 __global__ __launch_bounds__(kSmNT) void attn_split_softmax(float* __restrict__ sc, int sc_stride, int pos0,
-                                                            int n_heads) {
+                                                            const int* __restrict__ pos_dev, int n_heads) {
   extern __shared__ float4 smem_e4[];
   float* e = reinterpret_cast<float*>(smem_e4);
   __shared__ float s_red[kSmNT / 64];
   const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
-  const int n = pos0 + i + 1;
+  const int n = (pos_dev ? *pos_dev : pos0) + i + 1;
   float* row = sc + ((size_t)i * n_heads + h) * sc_stride;
   const bool in_regs = n <= kSmNT * kSmPer;
   float vals[kSmPer];
@@ -515,7 +516,8 @@ __global__ __launch_bounds__(kSmNT) void attn_split_softmax(float* __restrict__ 
 // leave the fold (started from +0.0) unchanged.
 template <int HD, int CH>
 __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__ prob, int sc_stride,
-                                                       const uint16_t* __restrict__ v, int pos0, int n_heads,
+                                                       const uint16_t* __restrict__ v, int pos0,
+                                                       const int* __restrict__ pos_dev, int n_heads,
                                                        int group, float* __restrict__ out,
                                                        int8_t* __restrict__ qd, float* __restrict__ qsa,
                                                        int* __restrict__ qsum) {
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
   __shared__ __align__(16) float s_prod[2][CH * 64];
   const int lb = logical_block(n_heads * NS);
   const int h = lb / NS, slice = lb % NS, i = blockIdx.y;
-  const int n = pos0 + i + 1;
+  const int n = (pos_dev ? *pos_dev : pos0) + i + 1;
   const int kvh = h / group;
   const int kv_words = (n_heads / group) * HD / 2;  // a cache row in 32-bit words
   const int tid = threadIdx.x;
@@ -1039,15 +1041,18 @@ size_t max_dyn_lds() {
 }
 
 template <int HD>
-int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, size_t n_q, size_t n_heads,
-                 size_t n_kv_heads, float* out, float* scratch, size_t ctx_cap, const ActQuant* aq, bool* quantized,
-                 hipStream_t s) {
+int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, const int* pos_dev, size_t n_q,
+                 size_t n_heads, size_t n_kv_heads, float* out, float* scratch, size_t ctx_cap, const ActQuant* aq,
+                 bool* quantized, hipStream_t s) {
   const int group = static_cast<int>(n_heads / n_kv_heads);
   const int stride = static_cast<int>(split_stride(ctx_cap));
-  const size_t rows = pos0 + n_q;
+  // a position read from device memory can be anything up to the capacity:
+  // the grid and the staging cover the whole window then (blocks past the
+  // window return at once)
+  const size_t rows = pos_dev ? ctx_cap : pos0 + n_q;
   hipLaunchKernelGGL(attn_split_scores<HD>,
                      dim3((rows + kSplitRows - 1) / kSplitRows, n_q * n_kv_heads * ((group + 3) / 4)),
-                     dim3(kSplitRows), 0, s, q, k, (int)pos0, (int)n_heads, group,
+                     dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_heads, group,
                      (int)n_kv_heads, scratch, stride);
   PRANA_LAUNCH_CHECK();
   // the softmax stages the longest row's exponentials in LDS when they fit
@@ -1061,10 +1066,10 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   }();
   if (lds <= lds_cap)
     hipLaunchKernelGGL(attn_split_softmax<true>, dim3(n_heads, n_q), dim3(kSmNT), lds, s, scratch, stride,
-                       (int)pos0, (int)n_heads);
+                       (int)pos0, pos_dev, (int)n_heads);
   else
     hipLaunchKernelGGL(attn_split_softmax<false>, dim3(n_heads, n_q), dim3(kSmNT), 0, s, scratch, stride,
-                       (int)pos0, (int)n_heads);
+                       (int)pos0, pos_dev, (int)n_heads);
   PRANA_LAUNCH_CHECK();
   const bool fuse_q = aq && aq->q;  // 64-dim slices are whole 32-blocks
   if (quantized) *quantized = fuse_q;
@@ -1075,10 +1080,10 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   int* qsum = fuse_q ? aq->sums : nullptr;
   if (n_heads * (HD / 64) * n_q <= 256)
     hipLaunchKernelGGL((attn_split_pv<HD, 256>), dim3(n_heads * (HD / 64), n_q), dim3(kPvNT), 0, s, scratch, stride,
-                       v, (int)pos0, (int)n_heads, group, out, qd, qsa, qsum);
+                       v, (int)pos0, pos_dev, (int)n_heads, group, out, qd, qsa, qsum);
   else
     hipLaunchKernelGGL((attn_split_pv<HD, 128>), dim3(n_heads * (HD / 64), n_q), dim3(kPvNT), 0, s, scratch, stride,
-                       v, (int)pos0, (int)n_heads, group, out, qd, qsa, qsum);
+                       v, (int)pos0, pos_dev, (int)n_heads, group, out, qd, qsa, qsum);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -1097,13 +1102,14 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
     return hd == 64 ? launch_wide<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s)
                     : launch_wide<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s);
   }
-  if (F16 && aligned && !pos_dev && scratch && pos0 + n_q >= kSplitMinRows && (hd == 64 || hd == 128)) {
+  // with pos_dev, pos0 still picks the path (the kernels read the position)
+  if (F16 && aligned && scratch && pos0 + n_q >= kSplitMinRows && (hd == 64 || hd == 128)) {
     const uint16_t* kc = static_cast<const uint16_t*>(k);
     const uint16_t* vc = static_cast<const uint16_t*>(v);
-    return hd == 64 ? launch_split<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap, aq,
-                                       quantized, s)
-                    : launch_split<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap, aq,
-                                        quantized, s);
+    return hd == 64 ? launch_split<64>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap,
+                                       aq, quantized, s)
+                    : launch_split<128>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap,
+                                        aq, quantized, s);
   }
   int mode = 0;
   if (aligned) {
@@ -1134,6 +1140,8 @@ int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, boo
   while (n_q * n_heads * ds < 128 && ds < 4 && hd % (2 * ds) == 0 && (hd / (2 * ds)) * elem % 16 == 0) ds *= 2;
   return ds;
 }
+
+bool attention_split_window(size_t rows, size_t hd) { return rows >= kSplitMinRows && (hd == 64 || hd == 128); }
 
 size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap, bool cache) {
   // split path (cache windows): scores / probabilities of every (query row, head)

@@ -424,6 +424,24 @@ int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStrea
   return kOk;
 }
 
+// One replayed decode step's bookkeeping: state = {position, step}; the
+// step's argmax (tok) becomes ids[step + 1], then both counters advance.
+__global__ void decode_advance_kernel(int* __restrict__ state, const uint32_t* __restrict__ tok,
+                                      uint32_t* __restrict__ ids) {
+  if (threadIdx.x == 0) {
+    const int step = state[1];
+    ids[step + 1] = tok[0];
+    state[0] += 1;
+    state[1] = step + 1;
+  }
+}
+
+int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStream_t s) {
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, s, state, tok, ids);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 // ---------------------------------------------------------------- embedding
 // Embedding::row (checkpoint.rs:169-174): dense copy, or one row of a packed
 // table dequantized (kquant.rs:39-112; Q8_0 tables are f32 rows q*d as

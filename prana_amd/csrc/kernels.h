@@ -47,6 +47,9 @@ int launch_expf(const float* in, size_t n, float* out, hipStream_t s);
 int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s);
 int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStream_t s);
 int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale, float* out, hipStream_t s);
+// state = {position, step} in device memory: ids[step + 1] = tok[0], then
+// position and step advance by one (the tail of a replayed decode step).
+int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStream_t s);
 
 // ---- gemv.hip
 // Optional dispatch timestamps for the next decode GEMV launch on this
@@ -100,8 +103,9 @@ size_t terms_per_row(const DevMat& m);
 // f16 cache: n_q query rows at positions pos0 + i (pos0 read from pos_dev when
 // non-null). scratch >= attention_scratch_floats(n_q, n_heads, ctx_cap)
 // floats, ctx_cap >= pos0+n_q (0 = exactly pos0+n_q). Windows of at least
-// 2048 rows with 64- or 128-wide heads and a host-side position take the
-// three-launch split path.
+// 2048 rows with 64- or 128-wide heads take the three-launch split path;
+// with pos_dev the host-side pos0 still chooses the path, and the launches
+// cover any device position up to ctx_cap - n_q.
 // Optional quantized copy of an attention output (quantize_acts layout, one
 // row of n_heads*hd per query). The launchers fill it in the same pass when
 // every workgroup's output dims are whole 32-element blocks and report that
@@ -122,6 +126,8 @@ int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* v
 // 4096 positions spill from LDS to it on the one-launch path. Also the dim
 // slices per head a launch uses.
 size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap, bool cache = true);
+// Whether a one-row cache window of `rows` rows takes the split path.
+bool attention_split_window(size_t rows, size_t hd);
 int attention_dim_slices(size_t n_q, size_t n_heads, size_t hd, size_t elem, bool aligned);
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
                              size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s,

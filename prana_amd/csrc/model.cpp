@@ -7,6 +7,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -181,6 +182,7 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
   int rc;
   if (n_tok > ws.cap_tok) {
     size_t n = n_tok;
+    ws.gen++;
     if ((rc = ws.x.alloc(n * c.dim * 4)) || (rc = ws.xb.alloc(n * c.dim * 4)) || (rc = ws.q.alloc(n * q_dim * 4)) ||
         (rc = ws.k.alloc(n * kv_dim * 4)) || (rc = ws.v.alloc(n * kv_dim * 4)) ||
         (rc = ws.attn.alloc(n * q_dim * 4)) || (rc = ws.gate.alloc(n * c.hidden_dim * 4)) ||
@@ -195,7 +197,9 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
   }
   size_t need = (prefill_attn ? attention_scratch_floats(n_tok, c.n_heads, n_tok, false)
                               : attention_scratch_floats(n_tok, c.n_heads, ctx_cap)) * 4;
+  const void* before = ws.scratch.p;
   if ((rc = ws.scratch.ensure(std::max<size_t>(need, 4)))) return rc;
+  if (ws.scratch.p != before) ws.gen++;
   return kOk;
 }
 
@@ -319,16 +323,85 @@ int GemvProfile::collect() {
 // Greedy decode of n_steps tokens over an existing cache: feed `token` at
 // `pos`, take the argmax, feed it at pos+1, ... (the sampled part of the
 // generate loop, infer.rs:729-763, without prompt handling or stop ids).
+void StepGraph::reset() {
+  if (exec) (void)hipGraphExecDestroy(exec);
+  exec = nullptr;
+  cache_buf = ids = nullptr;
+}
+
+static bool decode_graphs_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("PRANA_DECODE_GRAPH");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+int Model::step_graph_ready(Cache& cache, size_t pos, uint32_t* ids, hipStream_t s, hipGraphExec_t* exec) {
+  StepGraph& g = step_graph[attention_split_window(pos + 1, c.head_dim) ? 1 : 0];
+  *exec = nullptr;
+  if (g.exec && g.cache_buf == cache.buf.p && g.cache_len == cache.len && g.ws_gen == ws.gen && g.ids == ids) {
+    *exec = g.exec;
+    return kOk;
+  }
+  g.reset();
+  pos_dev = ws.step_state.as<int>();
+  PRANA_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = forward_dev(cache, nullptr, ws.tokens.as<uint32_t>(), pos, true, s);
+  if (!rc) rc = launch_argmax(ws.logits.as<float>(), 1, c.vocab_size, ws.tokens.as<uint32_t>(), s);
+  if (!rc) rc = launch_decode_advance(ws.step_state.as<int>(), ws.tokens.as<uint32_t>(), ids, s);
+  pos_dev = nullptr;
+  hipGraph_t graph = nullptr;
+  const hipError_t e = hipStreamEndCapture(s, &graph);
+  if (!rc && e == hipSuccess) {
+    const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+      g.exec = nullptr;
+      rc = fail(kErrHip, std::string("decode step graph: ") + hipGetErrorString(ei));
+    }
+  } else if (!rc) {
+    rc = fail(kErrHip, std::string("decode step capture: ") + hipGetErrorString(e));
+  }
+  if (graph) (void)hipGraphDestroy(graph);
+  if (rc) return rc;
+  g.cache_buf = cache.buf.p;
+  g.cache_len = cache.len;
+  g.ws_gen = ws.gen;
+  g.ids = ids;
+  *exec = g.exec;
+  return kOk;
+}
+
 int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out) {
   hipStream_t s = ctx().stream;
   PRANA_CHECK(pos + n_steps <= cache.len, "decode: positions beyond the cache length");
+  PRANA_CHECK(cache.len <= 0x7fffffff, "decode: cache length out of range");
   int rc = ensure_ws(1, cache.len, false);
   if (rc) return rc;
   if ((rc = ws.stream_out.ensure((n_steps + 1) * 4))) return rc;
+  if ((rc = ws.step_state.ensure(8))) return rc;
   uint32_t* ids = ws.stream_out.as<uint32_t>();
   // ids[i] feeds step i; step i's argmax lands in ids[i+1].
   PRANA_HIP(hipMemcpyAsync(ids, &token, 4, hipMemcpyHostToDevice, s));
-  for (size_t i = 0; i < n_steps; i++) {
+  // Steps replay a captured step (the position and the step index live in
+  // device memory), one captured step per run of steps on the same attention
+  // path; while GEMV dispatches are being timed, steps launch kernel by
+  // kernel. Both run the same kernels on the same data.
+  size_t i = 0;
+  if (decode_graphs_enabled() && !gemv_profile().on && n_steps > 0) {
+    const int st[2] = {static_cast<int>(pos), 0};
+    PRANA_HIP(hipMemcpyAsync(ws.step_state.p, st, 8, hipMemcpyHostToDevice, s));
+    PRANA_HIP(hipMemcpyAsync(ws.tokens.p, &token, 4, hipMemcpyHostToDevice, s));
+    auto regime = [&](size_t k) { return attention_split_window(pos + k + 1, c.head_dim); };
+    while (i < n_steps) {
+      size_t j = i;
+      while (j < n_steps && regime(j) == regime(i)) j++;
+      hipGraphExec_t exec;
+      if ((rc = step_graph_ready(cache, pos + i, ids, s, &exec))) return rc;
+      for (; i < j; i++) PRANA_HIP(hipGraphLaunch(exec, s));
+    }
+  }
+  for (; i < n_steps; i++) {
     if ((rc = forward_dev(cache, nullptr, ids + i, pos + i, true, s))) return rc;
     if ((rc = launch_argmax(ws.logits.as<float>(), 1, c.vocab_size, ids + i + 1, s))) return rc;
   }
@@ -368,10 +441,10 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     bool quantized = false;
     if (mode == 0) {
       if ((rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd, tab,
-                               c.rope_neox, kc, vc, nullptr, pos0, s)))
+                               c.rope_neox, kc, vc, pos_dev, pos0, s)))
         return rc;
       if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
-                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s, &aq,
+                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, pos_dev, s, &aq,
                                        &quantized)))
         return rc;
     } else {
@@ -489,8 +562,8 @@ bool is_stop(uint32_t t, const uint32_t* stops, size_t n) {
 }  // namespace
 
 // generate (infer.rs:696-771), greedy. The sampled id goes from the device
-// argmax straight into the next step's embedding input; the host reads it back
-// only to emit it and test the stop set.
+// argmax straight into the next step's embedding input; the host reads the
+// ids back a chunk of steps at a time to emit them and test the stop set.
 int Model::generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
                     uint32_t* out, size_t* n_out, prana_gen_stats* st) {
   PRANA_CHECK(p > 0, "prompt encoded to zero tokens");
@@ -509,8 +582,32 @@ int Model::generate(const uint32_t* prompt, size_t p, size_t steps, const uint32
     token = prompt[p - 1];
   }
   double t1 = now_s();
+  if (start_pos == p - 1) {
+    // The prompt is in the cache: steps at positions p-1 .. max_pos-2 each
+    // produce one token. They run as decode() chunks (one host round trip
+    // per chunk); the chunk is scanned for stop ids, and tokens after a stop
+    // are discarded (greedy steps do not depend on later ones).
+    const size_t total = max_pos - p;
+    constexpr size_t kChunk = 16;
+    size_t pos = start_pos;
+    bool stopped = false;
+    while (generated < total && !stopped) {
+      const size_t n = std::min(kChunk, total - generated);
+      if ((rc = decode(cache, token, pos, n, out + generated))) return rc;
+      size_t keep = n;
+      for (size_t j = 0; j < n; j++)
+        if (is_stop(out[generated + j], stops, n_stops)) {
+          keep = j;
+          stopped = true;
+          break;
+        }
+      token = out[generated + n - 1];
+      generated += keep;
+      pos += n;
+    }
+  }
   bool token_on_device = false;
-  for (size_t pos = start_pos; pos < max_pos; pos++) {
+  for (size_t pos = start_pos; start_pos != p - 1 && pos < max_pos; pos++) {
     bool need = pos + 1 >= p && pos + 1 < max_pos;
     if ((rc = forward_dev(cache, token_on_device ? nullptr : &token, nullptr, pos, need, s))) return rc;
     if (pos + 1 >= max_pos) break;
@@ -570,14 +667,8 @@ int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, si
   bool done = false;
   while (!done && pos + 1 < max_pos) {
     size_t budget = std::min(max_pos - 1 - pos, k);
-    uint32_t d_tok = last;
-    for (size_t j = 0; j < budget; j++) {
-      if ((rc = draft.forward_dev(dc, &d_tok, nullptr, pos + j, true, s))) return rc;
-      if ((rc = launch_argmax(draft.ws.logits.as<float>(), 1, V, draft.ws.argmax.as<uint32_t>(), s))) return rc;
-      PRANA_HIP(hipMemcpyAsync(&d_tok, draft.ws.argmax.p, 4, hipMemcpyDeviceToHost, s));
-      PRANA_HIP(hipStreamSynchronize(s));
-      drafts[j] = d_tok;
-    }
+    // the draft's greedy steps from `last` at pos (one host round trip)
+    if ((rc = draft.decode(dc, last, pos, budget, drafts.data()))) return rc;
     proposed += budget;
     inputs[0] = last;
     for (size_t j = 0; j < budget; j++) inputs[j + 1] = drafts[j];

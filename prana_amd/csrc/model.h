@@ -40,6 +40,21 @@ struct Workspace {
   DevBuf scratch;       // attention scores
   DevBuf tokens, argmax;
   DevBuf stream_out;  // device-side token stream of decode()
+  DevBuf step_state;  // {position, step} of a replayed decode step
+  size_t gen = 0;     // bumped whenever a buffer above moves
+};
+
+// decode()'s captured step: embed, layers, head, argmax and the state
+// advance, replayed once per token (one per attention path: the kernels read
+// the position from device memory, the host position at capture chooses the
+// path). Valid while the buffers it was captured with stay where they are.
+struct StepGraph {
+  hipGraphExec_t exec = nullptr;
+  const void* cache_buf = nullptr;
+  size_t cache_len = 0, ws_gen = 0;
+  const void* ids = nullptr;
+  void reset();
+  ~StepGraph() { reset(); }
 };
 
 // Optional per-launch timing of the model's GEMVs (HIP events on the stream
@@ -78,6 +93,10 @@ struct Model {
   DevBuf rope;                // float2 [seq_len][head_dim/2] (cos, sin)
   bool finalized = false;
   Workspace ws;
+  StepGraph step_graph[2];  // windows below / on the split attention path
+  // While a decode step is captured: the position the step's RoPE and
+  // attention read (device memory) instead of the host-side one.
+  const int* pos_dev = nullptr;
 
   int set_tensor(const std::string& name, int ggml_type, const uint64_t* dims, int n_dims, const void* bytes,
                  size_t nbytes);
@@ -110,6 +129,9 @@ struct Model {
 
   int forward(Cache& cache, uint32_t token, size_t pos, bool need_logits, float* logits_host);
   int decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out);
+  // Capture (or reuse) the replayable decode step for the attention path of
+  // position pos, writing its tokens to ids.
+  int step_graph_ready(Cache& cache, size_t pos, uint32_t* ids, hipStream_t s, hipGraphExec_t* exec);
   int prefill(Cache& cache, const uint32_t* tokens, size_t n);
   int forward_batch(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, float* logits_host);
   int generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,

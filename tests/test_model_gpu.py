@@ -97,6 +97,58 @@ def test_long_window_split_attention_bitexact():
         assert np.array_equal(gc.read(layer, 1, 2054), oc.read(layer, 1, 2054))
 
 
+def oracle_chain(oc, tok, pos, n):
+    """The oracle's greedy stream: feed tok at pos, take the argmax, repeat."""
+    out = []
+    for i in range(n):
+        tok = int(O.argmax(oc.forward(tok, pos + i)))
+        out.append(tok)
+    return out
+
+
+def test_decode_replay_across_split_window_bitexact():
+    # decode() replays one captured step while the window stays below the
+    # split attention path (device-side position), then launches kernel by
+    # kernel: windows 2040..2051 cover both.
+    cfg = M.config(256, 512, 2, 4, 1, 512, 2200, head_dim=64, rope_neox=1)
+    t = M.synth_tensors(cfg, M.types_c0, 8)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(2200), o.cache(2200)
+    prompt = np.random.default_rng(8).integers(0, cfg["vocab_size"], 2040).astype(np.uint32)
+    gc.prefill(prompt[:2039])
+    oc.prefill(prompt[:2039])
+    got = gc.decode(int(prompt[2039]), 2039, 12)
+    assert list(got) == oracle_chain(oc, int(prompt[2039]), 2039, 12)
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, 2051), oc.read(layer, which, 2051)), (layer, which)
+
+
+def test_decode_replay_reuse_and_recapture_bitexact():
+    # Consecutive decode() calls reuse the captured step; a forward_batch in
+    # between grows the workspace, so the next call captures again.
+    cfg = M.config(128, 384, 2, 4, 2, 300, 96)
+    t = M.synth_tensors(cfg, M.types_c0, 9)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(96), o.cache(96)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab_size"], 6).astype(np.uint32)
+    gc.prefill(prompt[:5])
+    oc.prefill(prompt[:5])
+    a = gc.decode(int(prompt[5]), 5, 7)
+    ra = oracle_chain(oc, int(prompt[5]), 5, 7)
+    assert list(a) == ra
+    b = gc.decode(int(a[-1]), 12, 9)
+    rb = oracle_chain(oc, ra[-1], 12, 9)
+    assert list(b) == rb
+    batch = [int(x) for x in prompt[:6]]
+    assert same_bits(gc.forward_batch(batch, 21), oc.forward_batch(batch, 21))
+    c = gc.decode(int(rb[-1]), 27, 10)
+    assert list(c) == oracle_chain(oc, rb[-1], 27, 10)
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, 37), oc.read(layer, which, 37)), (layer, which)
+
+
 # ------------------------------------------------------------------ config 0: 15M shape, Q8_0, 256-step greedy decode
 @pytest.fixture(scope="module")
 def c0():
