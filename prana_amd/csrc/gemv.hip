@@ -664,6 +664,14 @@ TileGeom choose_geom(size_t K, bool act) {
     if ((256 * u) % nb == 0 && 256 * u / nb <= 64) return TileGeom{u, 256 * u / nb, nb, 256};
   }
   if (small_unit) return TileGeom{2, 8, 64, 256};
+  // K-quant rows of up to 64 super-blocks that no whole-row stage divides
+  // (e.g. 19 for 4864-wide rows): one stage padded to the next power of two
+  // (the spare slots clamp their loads and write nothing), so short matrices
+  // still spread over many workgroups; at most 64 rows per tile keeps a
+  // folder lane for every (token, row).
+  int sb = 4;
+  while (sb < nb) sb *= 2;
+  if (sb <= 64) return TileGeom{1, 256 / sb, sb, 256};
   return TileGeom{1, 32, 8, 256};
 }
 
