@@ -75,6 +75,15 @@ __device__ __forceinline__ uint16_t f32_to_f16(float x) {
   return nan ? static_cast<uint16_t>(((u >> 16) & 0x8000u) | 0x7e00u) : hw;
 }
 
+// RoPE pair rotation with host-computed (cos, sin) = glibc (cosf, sinf) of
+// (pos as f32) * powf(theta, -(2m)/hd), the exact values the reference
+// computes inline (attention.rs:93-100, 111-119).
+__device__ __forceinline__ void rotate(float& a, float& b, float2 cs) {
+  float x0 = a, x1 = b;
+  a = x0 * cs.x - x1 * cs.y;
+  b = x0 * cs.y + x1 * cs.x;
+}
+
 // ---------------------------------------------------------------- expf
 // The reference reaches expf through Rust's f32::exp -> glibc expf. glibc
 // (2.28+) computes it with the ARM optimized-routines algorithm: a 32-entry

@@ -216,14 +216,7 @@ int launch_add(float* x, const float* y, size_t n, size_t period, hipStream_t s)
 }
 
 // ---------------------------------------------------------------- RoPE
-// Pair rotation with host-computed (cos, sin) = glibc (cosf, sinf) of
-// (pos as f32) * powf(theta, -(2m)/hd) — the exact values the reference
-// computes inline (attention.rs:93-100, 111-119). table: [pos][hd/2] float2.
-__device__ __forceinline__ void rotate(float& a, float& b, float2 cs) {
-  float x0 = a, x1 = b;
-  a = x0 * cs.x - x1 * cs.y;
-  b = x0 * cs.y + x1 * cs.x;
-}
+// Pair rotation: see rotate() in common.h. table: [pos][hd/2] float2.
 
 // x: n_rows rows of row_len floats (row_stride apart); row t is at position
 // pos0 + t. neox: pairs (j, j + hd/2) per head; else adjacent pairs.

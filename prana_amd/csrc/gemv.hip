@@ -420,6 +420,9 @@ struct DecodeJob {
   int8_t* hq;
   float* hsa;
   int* hsum;
+  // one-token Q|K|V (m = q, k, v): rope and the cache rows in the epilogue
+  // when rk.table is set (tiles then hold whole rotation pairs)
+  RopeKv rk;
 };
 
 constexpr int kDecMaxTok = 4;   // tokens per launch (LDS permitting)
@@ -590,7 +593,49 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   }
 
   if (!ACT) {
-    if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
+    if (!job.rk.table) {
+      if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
+      return;
+    }
+    // q/k/v + bias, exchanged through LDS for the rotation pairs (n_tok == 1)
+    __syncthreads();  // every fold read of the term buffers is done
+    float* xv = reinterpret_cast<float*>(sm8);
+    const GemvOut& o = job.o[mi];
+    const size_t r = r0 + fl_lr;
+    float val = 0.0f;
+    if (folder) {
+      val = o.bias ? acc + o.bias[r] : acc;
+      xv[fl_lr] = val;
+    }
+    __syncthreads();
+    if (folder) {
+      const RopeKv& rk = job.rk;
+      const int pos = rk.pos_dev ? *rk.pos_dev : rk.pos;
+      const size_t crow = (size_t)pos * rows_m + r;  // k and v have kv_dim = rows_m rows
+      if (mi == 2) {
+        o.out[r] = val;
+        rk.vc[crow] = f32_to_f16(val);
+      } else {
+        const int half = rk.hd / 2;
+        bool first;
+        int lp, m;
+        if (rk.neox) {  // pairs (j, j + hd/2) of a head; tiles start on head boundaries
+          const int j = fl_lr % rk.hd;
+          first = j < half;
+          lp = first ? fl_lr + half : fl_lr - half;
+          m = first ? j : j - half;
+        } else {  // adjacent pairs; tiles start on even rows
+          first = (fl_lr & 1) == 0;
+          lp = fl_lr ^ 1;
+          m = static_cast<int>((r & ~static_cast<size_t>(1)) % rk.hd) / 2;
+        }
+        float a = first ? val : xv[lp], b = first ? xv[lp] : val;
+        rotate(a, b, rk.table[(size_t)pos * half + m]);
+        const float y = first ? a : b;
+        o.out[r] = y;
+        if (mi == 1) rk.kc[crow] = f32_to_f16(y);
+      }
+    }
     return;
   }
   // act epilogue: gate lanes (row < rt) pair with up lanes (row + rt);
@@ -1439,8 +1484,9 @@ int dispatch_kind(int kind, F&& f) {
 constexpr size_t kDecodeMaxTokens = kGemvDecodeMaxTokens;
 
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
-                      size_t n_tok, hipStream_t s) {
+                      size_t n_tok, hipStream_t s, const RopeKv* rk, bool* fused) {
   PRANA_CHECK(n >= 1 && n <= 3, "gemv_multi: 1..3 matrices");
+  if (fused) *fused = false;
   if (n_tok == 0) return kOk;
   for (int i = 1; i < n; i++)
     PRANA_CHECK(ms[i].kind == ms[0].kind && ms[i].cols == ms[0].cols, "gemv_multi: matrices must share kind and cols");
@@ -1457,6 +1503,22 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
     job.o[i] = os[i];
   }
   job.n_mats = n;
+  if (rk && n == 3 && n_tok == 1 && ms[1].rows == ms[2].rows && rk->hd > 0 && rk->hd % 2 == 0 &&
+      ms[0].rows % rk->hd == 0 && ms[1].rows % rk->hd == 0 && !os[0].residual && !os[1].residual &&
+      !os[2].residual) {
+    // the tile must hold whole rotation pairs: even row counts (adjacent
+    // pairs) or whole heads (NeoX pairs), in a single stage
+    const bool ok = dispatch_kind(ms[0].kind, [&](auto k) {
+      constexpr int KIND = decltype(k)::value;
+      const TileGeom g = choose_geom<KIND>(ms[0].cols, false);
+      const int nb = static_cast<int>(ms[0].cols / RegUnit<KIND>::kElems);
+      return static_cast<int>(g.sb >= nb && (rk->neox ? g.rt % rk->hd == 0 : g.rt % 2 == 0));
+    });
+    if (ok) {
+      job.rk = *rk;
+      if (fused) *fused = true;
+    }
+  }
   return dispatch_kind(ms[0].kind, [&](auto k) { return launch_decode_t<decltype(k)::value>(job, q, sa, sums, n_tok, s); });
 }
 

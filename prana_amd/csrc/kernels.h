@@ -86,8 +86,21 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
                 const GemvOut& o, hipStream_t s);
 // Up to three quantized matrices of one kind sharing the input (fused
 // Q|K|V), one launch.
+// Decode glue a one-token Q|K|V launch (n = 3: q, k, v rows) can fold into
+// its epilogue (infer.rs:169-178): rope q and k at the position, then write k
+// and v as the f16 cache row at that position, exactly as launch_rope_kv. The
+// launcher sets *fused when it did (kinds, widths and the tile layout allow
+// it); otherwise the caller runs launch_rope_kv.
+struct RopeKv {
+  const float2* table;  // [pos][hd/2] (cos, sin)
+  int hd, neox;
+  int pos;              // used when pos_dev is null
+  const int* pos_dev;
+  uint16_t* kc;
+  uint16_t* vc;
+};
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
-                      size_t n_tok, hipStream_t s);
+                      size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr);
 // gate|up in one launch with the activation fused: h = act(gate) * up
 // (norms.rs:27-41, infer.rs:193-199), quantized for the down projection;
 // act 0 = silu, 1 = gelu_tanh. h (f32) is optional.

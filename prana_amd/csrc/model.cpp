@@ -247,7 +247,9 @@ int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipS
   });
 }
 
-int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s) {
+int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s,
+                       const RopeKv* rk, bool* fused) {
+  if (fused) *fused = false;
   int i = 0;
   while (i < n_mats) {
     int j = i + 1;
@@ -262,8 +264,10 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
         d[k - i] = w[k]->d;
         bytes += w[k]->stream_bytes;
       }
+      const bool all3 = i == 0 && j - i == 3;
       int rc = timed(bytes, n, s, [&] {
-        return launch_gemv_multi(d, o + i, j - i, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, s);
+        return launch_gemv_multi(d, o + i, j - i, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, s,
+                                 all3 ? rk : nullptr, all3 ? fused : nullptr);
       });
       if (rc) return rc;
     }
@@ -432,16 +436,18 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
     GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
     GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
+    bool roped = false;  // the decode Q|K|V launch also did RoPE and the cache rows
     {
       const Mat* w[3] = {L.w[kWq].get(), L.w[kWk].get(), L.w[kWv].get()};
       const GemvOut o[3] = {oq, ok, ov};
-      if ((rc = apply_multi(w, o, 3, n, ws.xb.as<float>(), s))) return rc;
+      const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), pos_dev, kc, vc};
+      if ((rc = apply_multi(w, o, 3, n, ws.xb.as<float>(), s, mode == 0 ? &rk : nullptr, &roped))) return rc;
     }
     const ActQuant aq{ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>()};
     bool quantized = false;
     if (mode == 0) {
-      if ((rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd, tab,
-                               c.rope_neox, kc, vc, pos_dev, pos0, s)))
+      if (!roped && (rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd,
+                                         tab, c.rope_neox, kc, vc, pos_dev, pos0, s)))
         return rc;
       if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
                                        ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, pos_dev, s, &aq,

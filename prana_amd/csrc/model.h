@@ -109,7 +109,10 @@ struct Model {
   // hset: read the quantized MLP hidden state (ws.hq) instead of ws.qa.
   int apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipStream_t s, bool hset = false);
   // Several matrices over the same input (Q|K|V); runs of equal kind share a launch.
-  int apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s);
+  // rk: one-token Q|K|V glue (rope, cache rows) the launch may fold in;
+  // *fused tells whether it did.
+  int apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s,
+                  const RopeKv* rk = nullptr, bool* fused = nullptr);
   // gate/up projections with the activation and the down projection's
   // quantization fused when both share a kind; h lands in ws.gate (f32) and
   // ws.hq/hsa/hsum (quantized).

@@ -124,10 +124,14 @@ def test_decode_replay_across_split_window_bitexact():
             assert np.array_equal(gc.read(layer, which, 2051), oc.read(layer, which, 2051)), (layer, which)
 
 
-def test_decode_replay_reuse_and_recapture_bitexact():
+@pytest.mark.parametrize("heads,kv_heads,neox", [(4, 2, 0), (2, 1, 1)])
+def test_decode_replay_reuse_and_recapture_bitexact(heads, kv_heads, neox):
     # Consecutive decode() calls reuse the captured step; a forward_batch in
-    # between grows the workspace, so the next call captures again.
-    cfg = M.config(128, 384, 2, 4, 2, 300, 96)
+    # between grows the workspace, so the next call captures again. The
+    # one-token Q|K|V launch applies RoPE and writes the cache rows itself:
+    # adjacent pairs, and (2 heads of 64, NeoX) pairs half a head apart in
+    # tiles of whole heads.
+    cfg = M.config(128, 384, 2, heads, kv_heads, 300, 96, rope_neox=neox)
     t = M.synth_tensors(cfg, M.types_c0, 9)
     g, o = pair(cfg, t)
     gc, oc = g.cache(96), o.cache(96)
