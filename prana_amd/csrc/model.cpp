@@ -329,7 +329,9 @@ int GemvProfile::collect() {
 // generate loop, infer.rs:729-763, without prompt handling or stop ids).
 void StepGraph::reset() {
   if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
   exec = nullptr;
+  graph = nullptr;
   cache_buf = ids = nullptr;
 }
 
@@ -366,8 +368,11 @@ int Model::step_graph_ready(Cache& cache, size_t pos, uint32_t* ids, hipStream_t
   } else if (!rc) {
     rc = fail(kErrHip, std::string("decode step capture: ") + hipGetErrorString(e));
   }
-  if (graph) (void)hipGraphDestroy(graph);
-  if (rc) return rc;
+  if (rc) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  g.graph = graph;
   g.cache_buf = cache.buf.p;
   g.cache_len = cache.len;
   g.ws_gen = ws.gen;

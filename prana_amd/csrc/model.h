@@ -49,6 +49,7 @@ struct Workspace {
 // the position from device memory, the host position at capture chooses the
 // path). Valid while the buffers it was captured with stay where they are.
 struct StepGraph {
+  hipGraph_t graph = nullptr;  // kept alive as long as its executable form
   hipGraphExec_t exec = nullptr;
   const void* cache_buf = nullptr;
   size_t cache_len = 0, ws_gen = 0;
