@@ -425,7 +425,7 @@ struct DecodeJob {
   RopeKv rk;
 };
 
-constexpr int kDecMaxTok = 4;   // tokens per launch (LDS permitting)
+constexpr int kDecMaxTok = 8;   // tokens per launch (LDS and folder lanes permitting)
 constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: one quantization block
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
@@ -740,8 +740,21 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     total += job.tiles[i];
   }
   const size_t per_tok = astride + term_bytes;
-  size_t group = std::min<size_t>(kDecMaxTok, (64 * 1024) / per_tok);
-  if (ACT) group = std::min<size_t>(group, NT / rows_wg);
+  // verify batches of up to kDecMaxTok tokens stream the weights once; the
+  // activations and term rows of every token sit in LDS, beyond 64 KB when
+  // the device grants it
+  static const size_t lds_cap = [] {
+    int dev = 0, b = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || b <= 65536)
+      return size_t{65536};
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, b) == hipSuccess
+               ? static_cast<size_t>(b)
+               : size_t{65536};
+  }();
+  size_t group = std::min<size_t>(kDecMaxTok, lds_cap / per_tok);
+  group = std::min<size_t>(group, NT / rows_wg);  // one folder lane per (token, row)
   PRANA_CHECK(K <= 16384, "gemv: decode kernel supports cols <= 16384");
   PRANA_CHECK(rows_wg * g.sb == NT * U, "gemv: tile geometry mismatch");
   PRANA_CHECK(group >= 1, "gemv: decode tile exceeds LDS");
