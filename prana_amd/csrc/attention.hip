@@ -638,6 +638,145 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
   }
 }
 
+// grid: (n_heads * HD/64, ceil(n_q / QR)). The verify form of the PV launch:
+// QR query rows of one (head, 64-dim slice) per workgroup share each V chunk;
+// eight producer waves keep the VALU load on each fold wave's SIMD light (a
+// busy neighbour delays the fold's dependent adds).
+// Fold wave q (q < QR) owns dim 64*slice + lane of query row i0 + q; the
+// producer lanes take (row quad, dim pair) tasks, load the four V rows' dim
+// pair once and form the products of all QR query rows (a row's keys past
+// its own window are zero products, which leave its fold from +0.0
+// unchanged). LDS: [2][QR][CH/4][64] float4, dynamic.
+constexpr int kPvrQR = 2;      // query rows per workgroup
+constexpr int kPvrCH = 128;    // cache rows per chunk
+constexpr int kPvrProd = 512;  // producer lanes: light VALU load beside each fold wave
+template <int HD>
+__global__ __launch_bounds__(64 * kPvrQR + kPvrProd) void attn_split_pv_rows(
+    const float* __restrict__ prob, int sc_stride, const uint16_t* __restrict__ v, int pos0,
+    const int* __restrict__ pos_dev, int n_q, int n_heads, int group, float* __restrict__ out,
+    int8_t* __restrict__ qd, float* __restrict__ qsa, int* __restrict__ qsum) {
+  constexpr int QR = kPvrQR, CH = kPvrCH;
+  constexpr int NS = HD / 64;
+  constexpr int kTasks = CH / 4 * 32;
+  constexpr int kPer = kTasks / kPvrProd;
+  constexpr int kQuadStep = kPvrProd / 32;
+  static_assert(kTasks % kPvrProd == 0, "whole tasks per producer lane");
+  static_assert(kSplitRows % CH == 0, "probability reads of the last chunk stay inside the scratch row");
+  extern __shared__ float4 pvr_smem[];
+  float* s_prod = reinterpret_cast<float*>(pvr_smem);
+  const int lb = logical_block(n_heads * NS);
+  const int h = lb / NS, slice = lb % NS;
+  const int i0 = blockIdx.y * QR;
+  const int nr = min(QR, n_q - i0);  // live query rows of this block
+  const int p0 = pos_dev ? *pos_dev : pos0;
+  const int n_max = p0 + i0 + nr;  // keys of the block's last live row
+  const int kvh = h / group;
+  const int kv_words = (n_heads / group) * HD / 2;
+  const int tid = threadIdx.x;
+  const int n_chunks = (n_max + CH - 1) / CH;
+  const bool folder = tid < 64 * QR;
+  const int pl = tid - 64 * QR;
+  const int dp = pl & 31, rq0 = pl >> 5;
+  const uint32_t* vlane = reinterpret_cast<const uint32_t*>(v + (size_t)kvh * HD + slice * 64) + dp;
+  const float* plane[QR];
+#pragma unroll
+  for (int q = 0; q < QR; q++)  // dead rows read the last live row's (valid) scratch
+    plane[q] = prob + ((size_t)(i0 + min(q, nr - 1)) * n_heads + h) * sc_stride + 4 * rq0;
+
+  uint32_t vr[kPer][4];
+  float4 pr[kPer][QR];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int t = c * CH + 4 * rq0 + 4 * kQuadStep * k;
+#pragma unroll
+      for (int q = 0; q < QR; q++)
+        pr[k][q] = *reinterpret_cast<const float4*>(plane[q] + c * CH + 4 * kQuadStep * k);  // t + 3 < sc_stride
+#pragma unroll
+      for (int r = 0; r < 4; r++) vr[k][r] = vlane[(size_t)min(t + r, n_max - 1) * kv_words];  // past n_max: unused
+    }
+  };
+  auto produce = [&](int c, float* buf) {
+#pragma unroll
+    for (int k = 0; k < kPer; k++) {
+      const int t = c * CH + 4 * rq0 + 4 * kQuadStep * k;
+      float va[4], vb[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        va[r] = f16_operand(static_cast<uint16_t>(vr[k][r] & 0xffffu));
+        vb[r] = f16_operand(static_cast<uint16_t>(vr[k][r] >> 16));
+      }
+#pragma unroll
+      for (int q = 0; q < QR; q++) {
+        const int n = p0 + i0 + q + 1;  // keys of query row i0 + q
+        const float pv[4] = {pr[k][q].x, pr[k][q].y, pr[k][q].z, pr[k][q].w};
+        float a[4], b[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const bool live = t + r < n;
+          a[r] = live ? pv[r] * va[r] : 0.0f;
+          b[r] = live ? pv[r] * vb[r] : 0.0f;
+        }
+        float4* dst = reinterpret_cast<float4*>(buf + q * CH * 64) + (rq0 + kQuadStep * k) * 64 + 2 * dp;
+        dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+        dst[1] = make_float4(b[0], b[1], b[2], b[3]);
+      }
+    }
+  };
+
+  float acc = 0.0f;
+  if (!folder) {
+    fetch(0);
+    produce(0, s_prod);
+    if (n_chunks > 1) fetch(1);
+  }
+  __syncthreads();
+  const int fq = tid >> 6, lane = tid & 63;
+  for (int c = 0; c < n_chunks; c++) {
+    if (folder) {
+      const float4* src = reinterpret_cast<const float4*>(s_prod + ((c & 1) * QR + fq) * CH * 64) + lane;
+      float4 x[8], y[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) x[j] = src[j * 64];
+#pragma unroll
+      for (int g = 0; g < CH / 32; g++) {
+        if (g + 1 < CH / 32) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) y[j] = src[((g + 1) * 8 + j) * 64];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          acc += x[j].x;
+          acc += x[j].y;
+          acc += x[j].z;
+          acc += x[j].w;
+        }
+        asm volatile("" ::"v"(acc) : "memory");
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = y[j];
+      }
+    } else if (c + 1 < n_chunks) {
+      produce(c + 1, s_prod + ((c + 1) & 1) * QR * CH * 64);
+      if (c + 2 < n_chunks) fetch(c + 2);
+    }
+    __syncthreads();
+  }
+  if (folder && fq < nr) {
+    const size_t gi = (size_t)(i0 + fq) * n_heads * HD + (size_t)h * HD + slice * 64 + lane;
+    out[gi] = acc;
+    if (qd) {  // one wave: two whole 32-blocks
+      float scale;
+      int sum;
+      const int qi = quantize_lane(acc, &scale, &sum);
+      qd[gi] = static_cast<int8_t>(qi);
+      if ((gi & 31) == 0) {
+        qsa[gi >> 5] = scale;
+        qsum[gi >> 5] = sum;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- wide path
 // Verify batches (two or more query rows) over cache windows below
 // kSplitMinRows with 64/128-wide heads: one 1024-lane workgroup per (query
@@ -1078,7 +1217,18 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   int8_t* qd = fuse_q ? aq->q : nullptr;
   float* qsa = fuse_q ? aq->sa : nullptr;
   int* qsum = fuse_q ? aq->sums : nullptr;
-  if (n_heads * (HD / 64) * n_q <= 256)
+  // several query rows (verify): rows of one head slice share each V chunk,
+  // one 128 KB workgroup per CU, when the device grants that much LDS
+  constexpr size_t kPvrLds = 2 * kPvrQR * kPvrCH * 64 * sizeof(float);
+  static const bool pvr_ok = max_dyn_lds() >= kPvrLds &&
+                             hipFuncSetAttribute(reinterpret_cast<const void*>(attn_split_pv_rows<HD>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(kPvrLds)) == hipSuccess;
+  if (n_q >= 2 && pvr_ok)
+    hipLaunchKernelGGL(attn_split_pv_rows<HD>, dim3(n_heads * (HD / 64), (n_q + kPvrQR - 1) / kPvrQR),
+                       dim3(64 * kPvrQR + kPvrProd), kPvrLds, s, scratch, stride, v, (int)pos0, pos_dev, (int)n_q,
+                       (int)n_heads, group, out, qd, qsa, qsum);
+  else if (n_heads * (HD / 64) * n_q <= 256)
     hipLaunchKernelGGL((attn_split_pv<HD, 256>), dim3(n_heads * (HD / 64), n_q), dim3(kPvNT), 0, s, scratch, stride,
                        v, (int)pos0, pos_dev, (int)n_heads, group, out, qd, qsa, qsum);
   else
