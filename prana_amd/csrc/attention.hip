@@ -254,6 +254,13 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
   if (SC_LDS)  // zero fill for the single-lane fold
     for (int t = n + tid; t < exact::lane_pad(n); t += kNT) sc[t] = 0.0f;
   __syncthreads();
+  // the first V chunk does not depend on the probabilities: its loads are
+  // issued here and land during the sum
+  constexpr int EPV = 16 / sizeof(T);
+  const int ppr = J.vec ? J.dw / EPV : 1;  // pieces per row (vector rows are whole pieces)
+  const int ch = (kPieces / ppr) / 4 * 4;  // rows per chunk, a multiple of 4
+  VPieces v{};
+  if (J.vec) v = fetch_v<F16>(J, 0, min(ch, n), ppr);
   // softmax sum in the reference's left-to-right order (norms.rs:53)
   const float sum = exact::block_seq_sum_nonneg<kNT, SC_LDS>(sc, n);
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
@@ -265,12 +272,8 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
   const bool folder = d < J.dw;
   float acc = 0.0f;
   if (J.vec) {
-    constexpr int EPV = 16 / sizeof(T);
-    const int ppr = J.dw / EPV;                 // pieces per row
-    const int ch = (kPieces / ppr) / 4 * 4;     // rows per chunk, a multiple of 4
     const int stride = ch + 4;
     const int n_chunks = (n + ch - 1) / ch;
-    VPieces v = fetch_v<F16>(J, 0, min(ch, n), ppr);
     make_products<F16>(v, sc, 0, min(ch, n), ppr, ch, L.prod);
     if (n_chunks > 1) v = fetch_v<F16>(J, ch, min(ch, n - ch), ppr);
     __syncthreads();
