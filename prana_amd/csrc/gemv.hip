@@ -898,72 +898,186 @@ typedef int v16i_t __attribute__((ext_vector_type(16)));
 constexpr int kMmaRows = 128;  // weight rows per workgroup (32 per wave)
 constexpr int kMmaToks = 32;   // tokens per workgroup
 
+// Operands stream through LDS in chunks of kMmaCB blocks: every lane loads
+// its share of chunk c+3 (16-byte pieces) into registers while chunk c is
+// multiplied, so two chunks of loads are in flight behind the one in use.
+// LDS rows are padded by 8 bytes (8-byte accesses of neighbouring rows fall
+// in different banks).
+constexpr int kMmaCB = 8;  // blocks per staged chunk
+typedef int sk_i4 __attribute__((ext_vector_type(4)));  // plain vector: stays in registers
+
+template <int KIND>
+struct MmaLayout {
+  static constexpr int QB = KIND == kKindQ4_0 ? 16 : 32;  // quant bytes per block
+  static constexpr int WSTR = kMmaCB * QB + 8;             // bytes per staged weight row
+  static constexpr int ASTR = kMmaCB * 32 + 8;             // bytes per staged activation row
+  static constexpr int DSTR = kMmaCB + 1;                  // words per staged weight-scale row
+  // one buffer: W [kMmaRows][WSTR] | A [kMmaToks][ASTR] | D [kMmaRows][DSTR] | SA, SM [kMmaCB][kMmaToks]
+  static constexpr int A_OFF = kMmaRows * WSTR;
+  static constexpr int D_OFF = A_OFF + kMmaToks * ASTR;
+  static constexpr int SA_OFF = D_OFF + kMmaRows * DSTR * 4;
+  static constexpr int SM_OFF = SA_OFF + kMmaCB * kMmaToks * 4;
+  static constexpr int BYTES = SM_OFF + kMmaCB * kMmaToks * 4;
+  // 16-byte pieces per chunk and per lane (256 lanes)
+  static constexpr int WPR = kMmaCB * QB / 16;  // pieces per weight row
+  static constexpr int WP = kMmaRows * WPR, AP = kMmaToks * kMmaCB * 2;
+  static constexpr int WPL = WP / 256, APL = AP / 256;
+  static constexpr int DPL = kMmaRows * kMmaCB / 256, SPL = kMmaToks * kMmaCB / 256;
+  static_assert(WP % 256 == 0 && AP % 256 == 0 && DPL * 256 == kMmaRows * kMmaCB &&
+                    SPL * 256 == kMmaToks * kMmaCB,
+                "whole pieces per lane");
+};
+
+template <int KIND>
+struct MmaRegs {
+  using L = MmaLayout<KIND>;
+  sk_i4 w[L::WPL], a[L::APL];
+  uint32_t d[L::DPL];
+  float sa[L::SPL];
+  int sm[L::SPL];
+};
+
 template <int KIND>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* __restrict__ q,
                                                         const float* __restrict__ sa, const int* __restrict__ sums,
                                                         int n_tok, GemvOut o) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
-  constexpr int kChunk = 32;  // blocks whose activation scales / sums are staged at a time
-  __shared__ __align__(16) float s_sa[kChunk][kMmaToks];
-  __shared__ __align__(16) int s_sm[kChunk][kMmaToks];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
+  using L = MmaLayout<KIND>;
+  extern __shared__ int4 mma_smem[];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(mma_smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
   const int K = static_cast<int>(m.cols), G = K / 32;
   const int R = static_cast<int>(m.rows);
-  const int n_row = blockIdx.x * kMmaRows + wave * 32 + (lane & 31);  // this lane's weight row (B column)
-  const int row = min(n_row, R - 1);
+  const int row0 = blockIdx.x * kMmaRows;
   const int m0 = blockIdx.y * kMmaToks;
-  const int tok_a = min(m0 + (lane & 31), n_tok - 1);  // this lane's A row
-  const int8_t* qa = q + (size_t)tok_a * K + 8 * h;
+  const int n_chunks = (G + kMmaCB - 1) / kMmaCB;
+
+  auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
+    MmaRegs<KIND> r;
+    const int cb0 = c * kMmaCB;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = tid + 256 * i;
+      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int blk = min(cb0 + pr / (L::QB / 16), G - 1);
+      r.w[i] = *reinterpret_cast<const sk_i4*>(m.qs + (size_t)rr * G * L::QB + (size_t)blk * L::QB +
+                                               (pr % (L::QB / 16)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = tid + 256 * i;
+      const int t = min(m0 + p / (2 * kMmaCB), n_tok - 1), pr = p % (2 * kMmaCB);
+      const int blk = min(cb0 + pr / 2, G - 1);
+      r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = tid + 256 * i;
+      const size_t gi = (size_t)min(row0 + p / kMmaCB, R - 1) * G + min(cb0 + p % kMmaCB, G - 1);
+      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
+                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = tid + 256 * i;  // consecutive lanes: consecutive blocks of one token
+      const size_t gi = (size_t)min(m0 + p / kMmaCB, n_tok - 1) * G + min(cb0 + p % kMmaCB, G - 1);
+      r.sa[i] = sa[gi];
+      r.sm[i] = sums[gi];
+    }
+    return r;
+  };
+  auto store = [&](const MmaRegs<KIND>& r, int buf) __attribute__((always_inline)) {
+    uint8_t* b = lds + buf * L::BYTES;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {  // two 8-byte halves (padded rows are 8-byte aligned)
+      const int p = tid + 256 * i;
+      long* dst = reinterpret_cast<long*>(b + (p / L::WPR) * L::WSTR + (p % L::WPR) * 16);
+      dst[0] = static_cast<long>(static_cast<uint32_t>(r.w[i].x)) | (static_cast<long>(r.w[i].y) << 32);
+      dst[1] = static_cast<long>(static_cast<uint32_t>(r.w[i].z)) | (static_cast<long>(r.w[i].w) << 32);
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = tid + 256 * i;
+      long* dst = reinterpret_cast<long*>(b + L::A_OFF + (p / (2 * kMmaCB)) * L::ASTR + (p % (2 * kMmaCB)) * 16);
+      dst[0] = static_cast<long>(static_cast<uint32_t>(r.a[i].x)) | (static_cast<long>(r.a[i].y) << 32);
+      dst[1] = static_cast<long>(static_cast<uint32_t>(r.a[i].z)) | (static_cast<long>(r.a[i].w) << 32);
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = tid + 256 * i;
+      reinterpret_cast<uint32_t*>(b + L::D_OFF)[(p / kMmaCB) * L::DSTR + p % kMmaCB] = r.d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = tid + 256 * i;
+      reinterpret_cast<float*>(b + L::SA_OFF)[(p % kMmaCB) * kMmaToks + p / kMmaCB] = r.sa[i];
+      reinterpret_cast<int*>(b + L::SM_OFF)[(p % kMmaCB) * kMmaToks + p / kMmaCB] = r.sm[i];
+    }
+  };
   float acc[16];
 #pragma unroll
   for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-  for (int b0 = 0; b0 < G; b0 += kChunk) {
-    // stage the tile's per-block activation scales and sums, [block][token]
-    __syncthreads();  // the previous chunk has been read
-    for (int e = threadIdx.x; e < kChunk * kMmaToks; e += 256) {
-      const int tt = e / kChunk, bb = e % kChunk;  // consecutive lanes: consecutive blocks of one token
-      const size_t gi = (size_t)min(m0 + tt, n_tok - 1) * G + min(b0 + bb, G - 1);
-      s_sa[bb][tt] = sa[gi];
-      s_sm[bb][tt] = sums[gi];
-    }
-    __syncthreads();
-    const int cb = min(kChunk, G - b0);
-    for (int bb = 0; bb < cb; bb++) {
-      const int b = b0 + bb;
-      const long a1 = *reinterpret_cast<const long*>(qa + 32 * b);
-      const long a2 = *reinterpret_cast<const long*>(qa + 32 * b + 16);
+  const int wr_row = wave * 32 + (lane & 31);  // this lane's weight row in the tile (B column)
+  auto compute = [&](int buf, int c) __attribute__((always_inline)) {
+    const uint8_t* b = lds + buf * L::BYTES;
+    const uint8_t* arow = b + L::A_OFF + (lane & 31) * L::ASTR + 8 * h;  // this lane's A row (token)
+    const uint8_t* wrow = b + wr_row * L::WSTR + 8 * h;
+    const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + wr_row * L::DSTR;
+    const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + 4 * h;
+    const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + 4 * h;
+    const int nlive = min(kMmaCB, G - c * kMmaCB);  // uniform
+#pragma unroll
+    for (int bb = 0; bb < kMmaCB; bb++) {
+      if (bb >= nlive) break;  // uniform
+      const long a1 = *reinterpret_cast<const long*>(arow + bb * 32);
+      const long a2 = *reinterpret_cast<const long*>(arow + bb * 32 + 16);
       long b1, b2;
-      float d;
       if constexpr (KIND == kKindQ4_0) {
-        const long w = *reinterpret_cast<const long*>(m.qs + ((size_t)row * G + b) * 16 + 8 * h);
+        const long w = *reinterpret_cast<const long*>(wrow + bb * 16);
         b1 = w & 0x0F0F0F0F0F0F0F0FL;
         b2 = (w >> 4) & 0x0F0F0F0F0F0F0F0FL;
-        d = ld_f16(m.sc, (size_t)row * G + b);
       } else {
-        const int8_t* wr = reinterpret_cast<const int8_t*>(m.qs) + (size_t)row * K + 32 * b + 8 * h;
-        b1 = *reinterpret_cast<const long*>(wr);
-        b2 = *reinterpret_cast<const long*>(wr + 16);
-        d = KIND == kKindQ8F ? reinterpret_cast<const float*>(m.sc)[(size_t)row * G + b]
-                             : ld_f16(m.sc, (size_t)row * G + b);
+        b1 = *reinterpret_cast<const long*>(wrow + bb * 32);
+        b2 = *reinterpret_cast<const long*>(wrow + bb * 32 + 16);
       }
-      v16i_t c = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-      c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a2, b2, c, 0, 0, 0);
+      const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
+      v16i_t cc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      cc = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, cc, 0, 0, 0);
+      cc = __builtin_amdgcn_mfma_i32_32x32x16_i8(a2, b2, cc, 0, 0, 0);
 #pragma unroll
       for (int g = 0; g < 4; g++) {  // tokens 8g + 4h + e of the tile hold values v = 4g + e
-        const float4 s4 = *reinterpret_cast<const float4*>(&s_sa[bb][8 * g + 4 * h]);
-        const int4 m4 = *reinterpret_cast<const int4*>(&s_sm[bb][8 * g + 4 * h]);
+        const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * kMmaToks + 8 * g);
+        const int4 m4 = *reinterpret_cast<const int4*>(smb + bb * kMmaToks + 8 * g);
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
         const int mv[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          int isum = c[4 * g + e];
+          int isum = cc[4 * g + e];
           if constexpr (KIND == kKindQ4_0) isum -= 8 * mv[e];
           acc[4 * g + e] += d * sv[e] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
         }
       }
     }
+  };
+
+  MmaRegs<KIND> r0 = load(0), r1;
+  store(r0, 0);
+  if (n_chunks > 1) r0 = load(1);
+  if (n_chunks > 2) r1 = load(2);
+  __syncthreads();
+  // chunk c+1 sits in r0 when c is even, in r1 when c is odd
+  for (int c = 0; c < n_chunks; c += 2) {
+    compute(0, c);
+    if (c + 1 < n_chunks) store(r0, 1);
+    if (c + 3 < n_chunks) r0 = load(c + 3);
+    __syncthreads();
+    if (c + 1 >= n_chunks) break;
+    compute(1, c + 1);
+    if (c + 2 < n_chunks) store(r1, 0);
+    if (c + 4 < n_chunks) r1 = load(c + 4);
+    __syncthreads();
   }
+  const int n_row = row0 + wr_row;
   if (n_row < R) {
 #pragma unroll
     for (int v = 0; v < 16; v++) {
@@ -977,8 +1091,15 @@ template <int KIND>
 int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                      const GemvOut& o, hipStream_t s) {
   PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30), "gemm: shape out of range");
+  using L = MmaLayout<KIND>;
+  static const bool attr_ok = [] {
+    return L::BYTES * 2 <= 65536 ||
+           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_mfma_kernel<KIND>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+  }();
+  PRANA_CHECK(attr_ok, "gemm: LDS size not granted");
   dim3 grid((m.rows + kMmaRows - 1) / kMmaRows, (n_tok + kMmaToks - 1) / kMmaToks);
-  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), 0, s, m, q, sa, sums, (int)n_tok, o);
+  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, m, q, sa, sums, (int)n_tok, o);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -1018,8 +1139,6 @@ struct SkLayout {
   static constexpr int WPL = (WP + NT - 1) / NT, APL = (AP + NT - 1) / NT;
   static constexpr int DPL = (DP + NT - 1) / NT, SPL = (SP + NT - 1) / NT;
 };
-
-typedef int sk_i4 __attribute__((ext_vector_type(4)));  // plain vector: stays in registers
 
 template <int KIND, int RW, int TT>
 struct SkRegs {
