@@ -898,34 +898,34 @@ typedef int v16i_t __attribute__((ext_vector_type(16)));
 constexpr int kMmaRows = 128;  // weight rows per workgroup (32 per wave)
 constexpr int kMmaToks = 32;   // tokens per workgroup
 
-// Operands stream through LDS in chunks of kMmaCB blocks: every lane loads
+// Operands stream through LDS in chunks of L::CB blocks: every lane loads
 // its share of chunk c+3 (16-byte pieces) into registers while chunk c is
 // multiplied, so two chunks of loads are in flight behind the one in use.
 // LDS rows are padded by 8 bytes (8-byte accesses of neighbouring rows fall
 // in different banks).
-constexpr int kMmaCB = 8;  // blocks per staged chunk
+constexpr int kMmaCB = 4;  // blocks per staged chunk (small chunks: several workgroups per CU)
 typedef int sk_i4 __attribute__((ext_vector_type(4)));  // plain vector: stays in registers
 
 template <int KIND>
 struct MmaLayout {
   static constexpr int QB = KIND == kKindQ4_0 ? 16 : 32;  // quant bytes per block
-  static constexpr int WSTR = kMmaCB * QB + 8;             // bytes per staged weight row
-  static constexpr int ASTR = kMmaCB * 32 + 8;             // bytes per staged activation row
-  static constexpr int DSTR = kMmaCB + 1;                  // words per staged weight-scale row
-  // one buffer: W [kMmaRows][WSTR] | A [kMmaToks][ASTR] | D [kMmaRows][DSTR] | SA, SM [kMmaCB][kMmaToks]
+  static constexpr int CB = kMmaCB;  // blocks per chunk
+  static constexpr int WSTR = CB * QB + 8;             // bytes per staged weight row
+  static constexpr int ASTR = CB * 32 + 8;             // bytes per staged activation row
+  static constexpr int DSTR = CB + 1;                  // words per staged weight-scale row
+  // one buffer: W [kMmaRows][WSTR] | A [kMmaToks][ASTR] | D [kMmaRows][DSTR] | SA, SM [CB][kMmaToks]
   static constexpr int A_OFF = kMmaRows * WSTR;
   static constexpr int D_OFF = A_OFF + kMmaToks * ASTR;
   static constexpr int SA_OFF = D_OFF + kMmaRows * DSTR * 4;
-  static constexpr int SM_OFF = SA_OFF + kMmaCB * kMmaToks * 4;
-  static constexpr int BYTES = SM_OFF + kMmaCB * kMmaToks * 4;
+  static constexpr int SM_OFF = SA_OFF + CB * kMmaToks * 4;
+  static constexpr int BYTES = SM_OFF + CB * kMmaToks * 4;
   // 16-byte pieces per chunk and per lane (256 lanes)
-  static constexpr int WPR = kMmaCB * QB / 16;  // pieces per weight row
-  static constexpr int WP = kMmaRows * WPR, AP = kMmaToks * kMmaCB * 2;
+  static constexpr int WPR = CB * QB / 16;  // pieces per weight row
+  static constexpr int WP = kMmaRows * WPR, AP = kMmaToks * CB * 2;
   static constexpr int WPL = WP / 256, APL = AP / 256;
-  static constexpr int DPL = kMmaRows * kMmaCB / 256, SPL = kMmaToks * kMmaCB / 256;
-  static_assert(WP % 256 == 0 && AP % 256 == 0 && DPL * 256 == kMmaRows * kMmaCB &&
-                    SPL * 256 == kMmaToks * kMmaCB,
-                "whole pieces per lane");
+  static constexpr int SP = kMmaToks * CB;  // activation scales (and sums) per chunk
+  static constexpr int DPL = kMmaRows * CB / 256, SPL = (SP + 255) / 256;
+  static_assert(WP % 256 == 0 && AP % 256 == 0 && DPL * 256 == kMmaRows * CB, "whole pieces per lane");
 };
 
 template <int KIND>
@@ -950,11 +950,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
   const int R = static_cast<int>(m.rows);
   const int row0 = blockIdx.x * kMmaRows;
   const int m0 = blockIdx.y * kMmaToks;
-  const int n_chunks = (G + kMmaCB - 1) / kMmaCB;
+  const int n_chunks = (G + L::CB - 1) / L::CB;
 
   auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
     MmaRegs<KIND> r;
-    const int cb0 = c * kMmaCB;
+    const int cb0 = c * L::CB;
 #pragma unroll
     for (int i = 0; i < L::WPL; i++) {
       const int p = tid + 256 * i;
@@ -966,21 +966,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
 #pragma unroll
     for (int i = 0; i < L::APL; i++) {
       const int p = tid + 256 * i;
-      const int t = min(m0 + p / (2 * kMmaCB), n_tok - 1), pr = p % (2 * kMmaCB);
+      const int t = min(m0 + p / (2 * L::CB), n_tok - 1), pr = p % (2 * L::CB);
       const int blk = min(cb0 + pr / 2, G - 1);
       r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
     }
 #pragma unroll
     for (int i = 0; i < L::DPL; i++) {
       const int p = tid + 256 * i;
-      const size_t gi = (size_t)min(row0 + p / kMmaCB, R - 1) * G + min(cb0 + p % kMmaCB, G - 1);
+      const size_t gi = (size_t)min(row0 + p / L::CB, R - 1) * G + min(cb0 + p % L::CB, G - 1);
       r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
                                 : reinterpret_cast<const uint16_t*>(m.sc)[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
-      const int p = tid + 256 * i;  // consecutive lanes: consecutive blocks of one token
-      const size_t gi = (size_t)min(m0 + p / kMmaCB, n_tok - 1) * G + min(cb0 + p % kMmaCB, G - 1);
+      const int p = min(tid + 256 * i, L::SP - 1);  // consecutive lanes: consecutive blocks of one token
+      const size_t gi = (size_t)min(m0 + p / L::CB, n_tok - 1) * G + min(cb0 + p % L::CB, G - 1);
       r.sa[i] = sa[gi];
       r.sm[i] = sums[gi];
     }
@@ -998,20 +998,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
 #pragma unroll
     for (int i = 0; i < L::APL; i++) {
       const int p = tid + 256 * i;
-      long* dst = reinterpret_cast<long*>(b + L::A_OFF + (p / (2 * kMmaCB)) * L::ASTR + (p % (2 * kMmaCB)) * 16);
+      long* dst = reinterpret_cast<long*>(b + L::A_OFF + (p / (2 * L::CB)) * L::ASTR + (p % (2 * L::CB)) * 16);
       dst[0] = static_cast<long>(static_cast<uint32_t>(r.a[i].x)) | (static_cast<long>(r.a[i].y) << 32);
       dst[1] = static_cast<long>(static_cast<uint32_t>(r.a[i].z)) | (static_cast<long>(r.a[i].w) << 32);
     }
 #pragma unroll
     for (int i = 0; i < L::DPL; i++) {
       const int p = tid + 256 * i;
-      reinterpret_cast<uint32_t*>(b + L::D_OFF)[(p / kMmaCB) * L::DSTR + p % kMmaCB] = r.d[i];
+      reinterpret_cast<uint32_t*>(b + L::D_OFF)[(p / L::CB) * L::DSTR + p % L::CB] = r.d[i];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
       const int p = tid + 256 * i;
-      reinterpret_cast<float*>(b + L::SA_OFF)[(p % kMmaCB) * kMmaToks + p / kMmaCB] = r.sa[i];
-      reinterpret_cast<int*>(b + L::SM_OFF)[(p % kMmaCB) * kMmaToks + p / kMmaCB] = r.sm[i];
+      if (p < L::SP) {
+        reinterpret_cast<float*>(b + L::SA_OFF)[(p % L::CB) * kMmaToks + p / L::CB] = r.sa[i];
+        reinterpret_cast<int*>(b + L::SM_OFF)[(p % L::CB) * kMmaToks + p / L::CB] = r.sm[i];
+      }
     }
   };
   float acc[16];
@@ -1025,9 +1027,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
     const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + wr_row * L::DSTR;
     const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + 4 * h;
     const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + 4 * h;
-    const int nlive = min(kMmaCB, G - c * kMmaCB);  // uniform
+    const int nlive = min(L::CB, G - c * L::CB);  // uniform
 #pragma unroll
-    for (int bb = 0; bb < kMmaCB; bb++) {
+    for (int bb = 0; bb < L::CB; bb++) {
       if (bb >= nlive) break;  // uniform
       const long a1 = *reinterpret_cast<const long*>(arow + bb * 32);
       const long a2 = *reinterpret_cast<const long*>(arow + bb * 32 + 16);
