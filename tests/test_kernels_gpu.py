@@ -94,12 +94,24 @@ def test_matmul_prefill_rows_equal_decode():
                                              (300, 1024, 9), (129, 768, 16), (1000, 512, 48), (64, 1280, 64),
                                              (70, 256, 31)])
 def test_matmul_batched(ty, rows, cols, n_tok):
-    # Batches of 5..64 tokens: the skinny int8 matrix-core kernel for
-    # block-32 kinds (ragged row and token tiles, block counts that are not
-    # whole fetch groups); more than 64: the tiled matrix-core kernel; K-quants
-    # the row-outer kernel
+    # Batches of up to 8 tokens: the decode kernel (one launch); 9..64 tokens:
+    # the skinny int8 matrix-core kernel for block-32 kinds (ragged row and
+    # token tiles, block counts that are not whole fetch groups); more than 64:
+    # the LDS-staged 32x32 matrix-core kernel; K-quants above 16 tokens: the
+    # K-quant matrix-core kernel
     raw, g, o = _mat_pair(ty, rows, cols, 41 + n_tok, real=True)
     a = rng(n_tok).standard_normal((n_tok, cols)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
+@pytest.mark.parametrize("rows,cols,n_tok", [(150, 288, 100), (33, 1312, 97), (129, 96, 65)])
+def test_matmul_prefill_partial_chunks(ty, rows, cols, n_tok):
+    # The staged prefill kernel takes blocks in chunks of four: 9, 41 and 3
+    # blocks per row leave a partial last chunk; rows and tokens are ragged
+    # against its 128-row x 32-token tiles.
+    raw, g, o = _mat_pair(ty, rows, cols, 77 + n_tok, real=True)
+    a = rng(n_tok + 1).standard_normal((n_tok, cols)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
 
 
