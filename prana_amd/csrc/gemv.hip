@@ -1,5 +1,7 @@
-// Packed-weight matrix x quantized-activation products (decode GEMV and the
-// row-outer batched form).
+// Packed-weight matrix x quantized-activation products: the decode GEMV (up
+// to 8 tokens per launch), the row-outer fallback, and the int8 matrix-core
+// batched forms (skinny 16x16 tiles, LDS-staged 32x32 prefill tiles, K-quant
+// super-block tiles).
 //
 // Exactness contract (the scalar tier, matmul.rs:395-406, kquant.rs:240-318):
 // every output is a fold `acc = 0; for each term in element order: acc += term`

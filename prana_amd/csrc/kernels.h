@@ -69,7 +69,8 @@ struct GemvOut {
   int residual;
 };
 // Token counts up to this use the weight-streaming decode kernel (and
-// launch_gemv_act); larger batches use the tiled kernel.
+// launch_gemv_act; up to 8 tokens per launch); larger batches use the
+// matrix-core kernels.
 constexpr size_t kGemvDecodeMaxTokens = 16;
 // launch_gemv over block-32 kinds (Q8F, Q8_0, Q4_0) takes batches of
 // kGemvSkinnyMinTokens..kGemvSkinnyMaxTokens tokens to the skinny
