@@ -1343,7 +1343,7 @@ int launch_gemm_skinny(const DevMat& m, const int8_t* q, const float* sa, const 
 //         two MFMAs whose activation operands zero the other half, then
 //         term = ((d*sa)*float(sc))*float(isum16), sub-block 0 first   (kquant.rs:287-318)
 // Every output folds its terms in element order.
-constexpr int kKqCS = 2;  // super-blocks per staged chunk
+constexpr int kKqCS = 1;  // super-blocks per staged chunk
 
 template <int KIND, int RW, int TT>
 struct KqLayout {
