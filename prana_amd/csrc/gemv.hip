@@ -1120,7 +1120,7 @@ int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const in
 // the one being used. Every output folds its block terms (d*sa)*float(isum)
 // in block order, as the decode kernels do.
 typedef int v4i_t __attribute__((ext_vector_type(4)));
-constexpr int kSkCB = 16;  // blocks per staged chunk
+constexpr int kSkCB = 8;  // blocks per staged chunk
 
 template <int KIND, int RW, int TT>
 struct SkLayout {
