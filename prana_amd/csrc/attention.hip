@@ -962,17 +962,26 @@ constexpr int kPbNT = 256;
 constexpr int kPbMax = 2048;  // window rows a block workgroup takes
 constexpr int kPbW = exact::run_pad(kPbMax - 1) + 1;
 
-template <int HD>
+// DYN: the probability rows are dynamic LDS of scw words each (windows up to
+// kPbDynMax: several workgroups per CU); otherwise a static array sized for
+// kPbMax positions (the compiler then keeps more of the score loop in
+// registers, which long windows need more than occupancy).
+constexpr size_t kPbDynMax = 1024;
+template <int HD, bool DYN>
 __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restrict__ q, const float* __restrict__ k,
                                                           const float* __restrict__ v, int seq, int n_heads,
                                                           int group, float* __restrict__ out,
                                                           int8_t* __restrict__ qd, float* __restrict__ qsa,
-                                                          int* __restrict__ qsum) {
+                                                          int* __restrict__ qsum, int scw_arg) {
   static_assert(HD % 4 == 0 && (kPbQ * HD) % kPbNT == 0, "whole chains per lane");
   constexpr int QPL = kPbQ * HD / kPbNT;  // P·V chains per lane
   constexpr int QSTEP = kPbNT / HD;       // query rows between a lane's chains
   __shared__ __align__(16) float s_q[kPbQ][HD];
-  __shared__ __align__(16) float s_sc[kPbQ][kPbW];
+  // the block's probability rows, scw words each (run_pad layout)
+  __shared__ __align__(16) float s_sc_st[DYN ? 4 : kPbQ * kPbW];
+  extern __shared__ float4 pb_smem[];
+  float* s_scd = DYN ? reinterpret_cast<float*>(pb_smem) : s_sc_st;
+  const int scw = DYN ? scw_arg : kPbW;
   __shared__ float s_red[kPbQ][kPbNT / 64];
   const int h = blockIdx.x, tid = threadIdx.x;
   const int i0 = blockIdx.y * kPbQ;
@@ -1010,7 +1019,7 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
     for (int qq = 0; qq < kPbQ; qq++) {
       if (t <= i0 + qq) {  // causal: row i0+qq attends keys 0..i0+qq
         const float sv = dot[qq] * scale;
-        s_sc[qq][exact::run_pad(t)] = sv;
+        s_scd[(qq) * scw + exact::run_pad(t)] = sv;
         mxl[qq] = fmaxf(mxl[qq], sv);
       }
     }
@@ -1032,7 +1041,7 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
   for (int qq = 0; qq < kPbQ; qq++) {
     const int n = i0 + qq + 1;
     if (i0 + qq < seq)
-      for (int t = tid; t < n; t += kPbNT) s_sc[qq][exact::run_pad(t)] = dev_expf(s_sc[qq][exact::run_pad(t)] - mx[qq]);
+      for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = dev_expf(s_scd[(qq) * scw + exact::run_pad(t)] - mx[qq]);
   }
   __syncthreads();
   // softmax sums in the reference's left-to-right order (norms.rs:53): each
@@ -1044,7 +1053,7 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
     const int qq = r * (kPbNT / 64) + (tid >> 6);
     if (i0 + qq < seq) {  // wave-uniform; the group barriers are the wave's own
       const float sum =
-          exact::group_seq_sum_short<64, kPbNT / 64>([qq](int t) { return s_sc[qq][exact::run_pad(t)]; }, i0 + qq + 1);
+          exact::group_seq_sum_short<64, kPbNT / 64>([s_scd, scw, qq](int t) { return s_scd[(qq) * scw + exact::run_pad(t)]; }, i0 + qq + 1);
       if ((tid & 63) == 0) s_inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
     } else if ((tid & 63) == 0) {
       s_inv[qq] = 0.0f;
@@ -1058,7 +1067,7 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
   for (int qq = 0; qq < kPbQ; qq++) {
     const int n = i0 + qq + 1;
     if (i0 + qq < seq)
-      for (int t = tid; t < n; t += kPbNT) s_sc[qq][exact::run_pad(t)] = s_sc[qq][exact::run_pad(t)] * inv[qq];
+      for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = s_scd[(qq) * scw + exact::run_pad(t)] * inv[qq];
   }
   __syncthreads();
   // ---- P·V: lane (d, qg) folds rows qg, qg+QSTEP, ... of dim d over t from +0.0
@@ -1078,7 +1087,7 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
 #pragma unroll
     for (int u = 0; u < 8; u++)
 #pragma unroll
-      for (int c = 0; c < QPL; c++) pt[u][c] = s_sc[qg + c * QSTEP][exact::run_pad(t + u)];
+      for (int c = 0; c < QPL; c++) pt[u][c] = s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t + u)];
 #pragma unroll
     for (int u = 0; u < 8; u++)
 #pragma unroll
@@ -1087,14 +1096,14 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
   for (; t <= i0; t++) {
     const float vt = vcol[(size_t)t * kv_dim];
 #pragma unroll
-    for (int c = 0; c < QPL; c++) acc[c] = acc[c] + s_sc[qg + c * QSTEP][exact::run_pad(t)] * vt;
+    for (int c = 0; c < QPL; c++) acc[c] = acc[c] + s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t)] * vt;
   }
   for (; t < nk; t++) {
     const float vt = vcol[(size_t)t * kv_dim];
 #pragma unroll
     for (int c = 0; c < QPL; c++) {
       const int qq = qg + c * QSTEP;
-      const float nv = acc[c] + s_sc[qq][exact::run_pad(t)] * vt;
+      const float nv = acc[c] + s_scd[(qq) * scw + exact::run_pad(t)] * vt;
       acc[c] = t <= i0 + qq ? nv : acc[c];
     }
   }
@@ -1124,9 +1133,19 @@ int launch_prefill_blk(const float* q, const float* k, const float* v, size_t se
                        size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, hipStream_t s) {
   const bool fuse_q = aq && aq->q;
   if (quantized) *quantized = fuse_q;
-  hipLaunchKernelGGL(attn_prefill_blk<HD>, dim3(n_heads, (seq + kPbQ - 1) / kPbQ), dim3(kPbNT), 0, s, q, k, v,
-                     (int)seq, (int)n_heads, (int)(n_heads / n_kv_heads), out, fuse_q ? aq->q : nullptr,
-                     fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
+  const dim3 grid(n_heads, (seq + kPbQ - 1) / kPbQ);
+  int8_t* qd = fuse_q ? aq->q : nullptr;
+  float* qsa = fuse_q ? aq->sa : nullptr;
+  int* qsum = fuse_q ? aq->sums : nullptr;
+  const int group = static_cast<int>(n_heads / n_kv_heads);
+  if (seq <= kPbDynMax) {
+    const int scw = (exact::run_pad(static_cast<int>(seq) - 1) + 1 + 3) & ~3;  // 16-byte aligned rows
+    hipLaunchKernelGGL((attn_prefill_blk<HD, true>), grid, dim3(kPbNT), (size_t)kPbQ * scw * sizeof(float), s, q, k,
+                       v, (int)seq, (int)n_heads, group, out, qd, qsa, qsum, scw);
+  } else {
+    hipLaunchKernelGGL((attn_prefill_blk<HD, false>), grid, dim3(kPbNT), 0, s, q, k, v, (int)seq, (int)n_heads,
+                       group, out, qd, qsa, qsum, 0);
+  }
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
