@@ -431,6 +431,86 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __r
     if (hh < nh) dst[(size_t)hh * sc_stride] = dot[hh] * scale;
 }
 
+// grid: (ceil(rows / kSplitRows), ceil(n_q / 2) * n_kv * ceil(group / 4)).
+// The verify form of the scores launch: two query rows per workgroup share
+// each K row's load (eight side-by-side chains: four heads x two rows, each
+// folded over d in order as above); a row's keys past its own position are
+// not stored, and a dead second row repeats the first (computed, not stored).
+template <int HD>
+__global__ __launch_bounds__(kSplitRows) void attn_split_scores_rows(const float* __restrict__ q,
+                                                                     const uint16_t* __restrict__ k, int pos0,
+                                                                     const int* __restrict__ pos_dev, int n_q,
+                                                                     int n_heads, int group, int n_kv,
+                                                                     float* __restrict__ sc, int sc_stride) {
+  constexpr int QR = 2;
+  __shared__ __align__(16) float s_q[QR][4 * HD];
+  const int nhb = (group + 3) / 4;
+  const int hb = blockIdx.y % nhb, ik = blockIdx.y / nhb;
+  const int ig = ik / n_kv, kvh = ik % n_kv;
+  const int i0 = ig * QR, nr = min(QR, n_q - i0);
+  const int p0 = pos_dev ? *pos_dev : pos0;
+  const int n_max = p0 + i0 + nr;  // keys of the block's last live row
+  const int row0 = blockIdx.x * kSplitRows;
+  if (row0 >= n_max) return;  // uniform, before the barrier
+  const int h0 = kvh * group + 4 * hb;
+  const int nh = min(4, group - 4 * hb);
+  for (int e = threadIdx.x; e < QR * 4 * HD; e += kSplitRows) {
+    const int r = e / (4 * HD), ee = e % (4 * HD);
+    const float* qh = q + (size_t)(i0 + min(r, nr - 1)) * n_heads * HD + (size_t)h0 * HD;
+    s_q[r][ee] = qh[ee / HD < nh ? ee : ee % HD];
+  }
+  __syncthreads();
+  const int t = row0 + threadIdx.x;
+  if (t >= n_max) return;
+  const int kv_stride = n_kv * HD;
+  const uint4* kp = reinterpret_cast<const uint4*>(k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  uint4 raw[HD / 8];
+#pragma unroll
+  for (int e = 0; e < HD / 8; e++) raw[e] = kp[e];
+  float dot[QR][4];
+#pragma unroll
+  for (int r = 0; r < QR; r++)
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) dot[r][hh] = -0.0f;
+#pragma unroll
+  for (int e = 0; e < HD / 8; e++) {
+    const uint32_t w[4] = {raw[e].x, raw[e].y, raw[e].z, raw[e].w};
+    float kf[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      kf[j] = f16_operand(static_cast<uint16_t>(j & 1 ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu));
+#pragma unroll
+    for (int r = 0; r < QR; r++)
+#pragma unroll
+      for (int hh = 0; hh < 4; hh++) {
+        const float4 a = reinterpret_cast<const float4*>(s_q[r])[hh * (HD / 4) + 2 * e];
+        const float4 b = reinterpret_cast<const float4*>(s_q[r])[hh * (HD / 4) + 2 * e + 1];
+        dot[r][hh] += a.x * kf[0];
+        dot[r][hh] += a.y * kf[1];
+        dot[r][hh] += a.z * kf[2];
+        dot[r][hh] += a.w * kf[3];
+        dot[r][hh] += b.x * kf[4];
+        dot[r][hh] += b.y * kf[5];
+        dot[r][hh] += b.z * kf[6];
+        dot[r][hh] += b.w * kf[7];
+      }
+    // keep later steps' q reads from being hoisted above this one (registers)
+    asm volatile("" ::"v"(dot[0][0]), "v"(dot[0][1]), "v"(dot[0][2]), "v"(dot[0][3]), "v"(dot[1][0]),
+                 "v"(dot[1][1]), "v"(dot[1][2]), "v"(dot[1][3])
+                 : "memory");
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+#pragma unroll
+  for (int r = 0; r < QR; r++) {
+    if (r < nr && t < p0 + i0 + r + 1) {
+      float* dst = sc + ((size_t)(i0 + r) * n_heads + h0) * sc_stride + t;
+#pragma unroll
+      for (int hh = 0; hh < 4; hh++)
+        if (hh < nh) dst[(size_t)hh * sc_stride] = dot[r][hh] * scale;
+    }
+  }
+}
+
 // grid: (n_heads, n_q). Softmax of the row's scores in place. Rows of up to
 // kSmNT*kSmPer scores are held in registers (every load in flight at once);
 // longer rows stream. IN_LDS: the exponentials are staged in LDS
@@ -1211,10 +1291,16 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   // the grid and the staging cover the whole window then (blocks past the
   // window return at once)
   const size_t rows = pos_dev ? ctx_cap : pos0 + n_q;
-  hipLaunchKernelGGL(attn_split_scores<HD>,
-                     dim3((rows + kSplitRows - 1) / kSplitRows, n_q * n_kv_heads * ((group + 3) / 4)),
-                     dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_heads, group,
-                     (int)n_kv_heads, scratch, stride);
+  if (n_q >= 2)  // verify: two query rows per workgroup share each K row
+    hipLaunchKernelGGL(attn_split_scores_rows<HD>,
+                       dim3((rows + kSplitRows - 1) / kSplitRows, (n_q + 1) / 2 * n_kv_heads * ((group + 3) / 4)),
+                       dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_q, (int)n_heads, group,
+                       (int)n_kv_heads, scratch, stride);
+  else
+    hipLaunchKernelGGL(attn_split_scores<HD>,
+                       dim3((rows + kSplitRows - 1) / kSplitRows, n_q * n_kv_heads * ((group + 3) / 4)),
+                       dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_heads, group,
+                       (int)n_kv_heads, scratch, stride);
   PRANA_LAUNCH_CHECK();
   // the softmax stages the longest row's exponentials in LDS when they fit
   const size_t lds = (exact::run_pad(static_cast<int>(rows) - 1) + 1) * sizeof(float);
