@@ -653,7 +653,8 @@ __device__ __forceinline__ float block_seq_sum_pred(Term a, int n, bool* ok) {
 // kPredMaxPerLane terms use the predicted-binade scan, falling back to one
 // lane's chain for non-finite terms, very short sums and failed predictions
 // (PADDED: a is an LDS buffer, 16-byte aligned and zero-filled up to
-// lane_pad(n) terms, so the chain runs on 16-byte loads). Longer sums use the
+// lane_pad(n) terms, so the chain runs on 16-byte loads; such rows of up to
+// kPadSerialMax terms take that chain directly). Longer sums use the
 // adaptive binade scan, holding up to NT*CMAX terms in registers (thread t
 // owns the contiguous run [t*C, t*C + C), C = ceil(n/NT)) and streaming
 // longer sums from `a`; non-finite terms again run on one lane.
@@ -684,6 +685,7 @@ __device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
   return group_seq_sum_short<NT, 1>(term, n);
 }
 
+constexpr int kPadSerialMax = 512;
 template <int NT, bool PADDED, int CMAX = 16>
 __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
   static_assert(NT % 64 == 0 && NT <= 1024, "whole waves");
@@ -693,7 +695,10 @@ __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
   const int tid = threadIdx.x;
   if (n <= 0) return -0.0f;
   if (n <= kPredHead + NT * kPredMaxPerLane) {
-    if (n > kPredHead) {
+    // a padded LDS row folds on one lane at the add latency (~4 ns a term, its
+    // 16-byte loads a batch ahead), which beats the scan's fixed cost (five
+    // barriers, ~3.5 us) for rows of up to kPadSerialMax terms
+    if (n > (PADDED ? kPadSerialMax : kPredHead)) {
       bool ok;
       const float v = block_seq_sum_pred<NT>([a](int i) { return a[i]; }, n, &ok);
       if (ok) return v;
