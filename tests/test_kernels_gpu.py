@@ -270,7 +270,7 @@ def test_gelu_tanh_tolerance():
     assert np.all(np.abs(g - o) <= 1e-6 * np.abs(o) + 1e-7)
 
 
-@pytest.mark.parametrize("n", [1, 2, 7, 256, 2049])
+@pytest.mark.parametrize("n", [1, 2, 7, 256, 512, 513, 2049])
 def test_softmax(n):
     x = rng(n).standard_normal((3, n)).astype(np.float32) * 5
     got = P.softmax(x)
@@ -278,7 +278,7 @@ def test_softmax(n):
         assert same_bits(got[r], O.softmax(x[r]))
 
 
-@pytest.mark.parametrize("n", [1, 33, 4096, 4097, 20000])
+@pytest.mark.parametrize("n", [1, 33, 512, 513, 4096, 4097, 20000])
 def test_softmax_adversarial(n):
     r = rng(n + 7)
     rows = [
@@ -345,7 +345,9 @@ def _cache(n, nkv, hd, seed):
                                             (32, 8, 128, 2046), (32, 8, 128, 2047), (14, 2, 64, 2600),
                                             (8, 8, 64, 2048), (32, 8, 128, 16500), (4, 2, 80, 4500),
                                             (32, 8, 128, 254), (32, 8, 128, 255), (8, 8, 64, 1023),
-                                            (8, 8, 64, 1024), (32, 8, 128, 2045)])
+                                            (8, 8, 64, 1024), (32, 8, 128, 2045),
+                                            # the softmax sum folds on one lane up to 512 rows, by scan beyond
+                                            (32, 8, 128, 511), (32, 8, 128, 512), (14, 2, 64, 512)])
 def test_attention_decode(nh, nkv, hd, pos):
     kc, vc = _cache(pos + 1, nkv, hd, pos)
     q = rng(pos + 3).standard_normal(nh * hd).astype(np.float32)
