@@ -223,17 +223,6 @@ int prana_generate_speculative(prana_model_t target, prana_model_t draft, const 
                                size_t steps, size_t k, const uint32_t *stops, size_t n_stops, uint32_t *out,
                                size_t *n_out, prana_gen_stats *stats);
 
-/* ---------------------------------------------------------------- synthetic weights */
-/* Block encoders for synthetic models (the reference has no Q8_0/Q4_0 encoder;
- * Q4_K/Q6_K follow scripts/convert-to-gguf.py:29-89). src is rows x cols f32;
- * out receives ggml bytes. */
-int prana_quantize_tensor(int ggml_type, const float *src, size_t rows, size_t cols, void *out, size_t nbytes);
-/* Seeded N(0, sigma) values (xorshift64* streams + Box-Muller), n floats. */
-int prana_synth_normal(uint64_t seed, float sigma, float *out, size_t n);
-/* prana_synth_normal values for a rows x cols tensor, encoded straight into
- * ggml bytes (no f32 copy of the whole tensor is materialised). */
-int prana_synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, void *out,
-                       size_t nbytes);
 /* Bytes of a ggml tensor of the given type and element count. */
 size_t prana_ggml_nbytes(int ggml_type, size_t n_elems);
 

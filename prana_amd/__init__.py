@@ -13,7 +13,7 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import GenStats, PranaConfig, PranaError, check, load
+from ._lib import GenStats, PranaConfig, PranaError, check, check_synth, load, load_synth
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 GGML_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
@@ -69,24 +69,26 @@ def ggml_nbytes(ggml_type, n_elems):
     return int(load().prana_ggml_nbytes(ggml_type, n_elems))
 
 
+# Fixture encoders (libprana_synth.so, host code): synthetic weights for the
+# tests and the benchmark. The product library only uploads tensor bytes.
 def quantize_tensor(ggml_type, x):
     """Encode an f32 [rows, cols] array into ggml block bytes."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     rows, cols = x.shape
     out = np.zeros(ggml_nbytes(ggml_type, rows * cols), np.uint8)
-    check(load().prana_quantize_tensor(ggml_type, _ptr(x), rows, cols, _ptr(out), out.nbytes))
+    check_synth(load_synth().prana_quantize_tensor(ggml_type, _ptr(x), rows, cols, _ptr(out), out.nbytes))
     return out
 
 
 def synth_normal(seed, sigma, n):
     out = np.empty(n, np.float32)
-    check(load().prana_synth_normal(seed, sigma, _ptr(out), n))
+    check_synth(load_synth().prana_synth_normal(seed, sigma, _ptr(out), n))
     return out
 
 
 def synth_tensor(ggml_type, rows, cols, seed, sigma):
     out = np.empty(ggml_nbytes(ggml_type, rows * cols), np.uint8)
-    check(load().prana_synth_tensor(ggml_type, rows, cols, seed, sigma, _ptr(out), out.nbytes))
+    check_synth(load_synth().prana_synth_tensor(ggml_type, rows, cols, seed, sigma, _ptr(out), out.nbytes))
     return out
 
 

@@ -98,11 +98,19 @@ _SIGS = {
                                C.POINTER(GenStats)]),
     "prana_generate_speculative": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_void_p, c_size,
                                            c_void_p, C.POINTER(c_size), C.POINTER(GenStats)]),
+    "prana_ggml_nbytes": (c_size, [c_int, c_size]),
+}
+
+# libprana_synth.so (prana_amd/synth/prana_synth.h): fixture encoders of the
+# tests and the benchmark, host code only, kept out of the product library.
+SYNTH_PATH = os.path.join(_HERE, "_build", "libprana_synth.so")
+_SYNTH_SIGS = {
+    "prana_synth_last_error": (C.c_char_p, []),
     "prana_quantize_tensor": (c_int, [c_int, c_void_p, c_size, c_size, c_void_p, c_size]),
     "prana_synth_normal": (c_int, [c_u64, c_float, c_void_p, c_size]),
     "prana_synth_tensor": (c_int, [c_int, c_size, c_size, c_u64, c_float, c_void_p, c_size]),
-    "prana_ggml_nbytes": (c_size, [c_int, c_size]),
 }
+_synth = None
 
 _lib = None
 
@@ -126,6 +134,29 @@ def load():
 
 def exported_symbols():
     return list(_SIGS)
+
+
+def load_synth():
+    """Load the fixture-encoder library once and bind its symbols."""
+    global _synth
+    if _synth is not None:
+        return _synth
+    if not os.path.exists(SYNTH_PATH):
+        raise PranaError(f"{SYNTH_PATH} is missing: build it with `python prana_amd/build.py`")
+    lib = C.CDLL(SYNTH_PATH)
+    for name, (res, args) in _SYNTH_SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _synth = lib
+    return lib
+
+
+def check_synth(rc):
+    if rc != 0:
+        msg = load_synth().prana_synth_last_error().decode(errors="replace")
+        raise PranaError(f"prana_synth error {rc}: {msg}")
+    return rc
 
 
 def check(rc):

@@ -1,4 +1,5 @@
-"""Build libprana_hip.so (gfx950) in-tree: prana_amd/_build/libprana_hip.so.
+"""Build libprana_hip.so (gfx950) in-tree: prana_amd/_build/libprana_hip.so,
+plus the host-only fixture-encoder library libprana_synth.so.
 
 Every HIP/C++ source under prana_amd/csrc is compiled with hipcc for gfx950
 only, without FMA contraction (the kernels reproduce the reference's f32
@@ -52,9 +53,26 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_synth()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {SYNTH_LIB}")
     return LIB
+
+
+SYNTH_SRC = os.path.join(HERE, "synth", "synth.cpp")
+SYNTH_LIB = os.path.join(OUT, "libprana_synth.so")
+
+
+def build_synth():
+    """libprana_synth.so: the fixture encoders (host C++ only, no GPU code)."""
+    os.makedirs(OUT, exist_ok=True)
+    tmp = SYNTH_LIB + ".tmp"
+    cmd = ["g++", "-O2", "-fPIC", "-std=c++17", "-shared", "-Wall", "-o", tmp, SYNTH_SRC, "-lpthread"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, SYNTH_LIB)
+    return SYNTH_LIB
 
 
 if __name__ == "__main__":

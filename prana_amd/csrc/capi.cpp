@@ -584,30 +584,6 @@ int prana_generate_speculative(prana_model_t target, prana_model_t draft, const 
   });
 }
 
-// ------------------------------------------------------------------ synthetic weights
-int prana_quantize_tensor(int ggml_type, const float* src, size_t rows, size_t cols, void* out, size_t nbytes) {
-  return guard([&] {
-    PRANA_CHECK(src && out, "null argument");
-    return quantize_tensor(ggml_type, src, rows, cols, static_cast<uint8_t*>(out), nbytes);
-  });
-}
-
-int prana_synth_normal(uint64_t seed, float sigma, float* out, size_t n) {
-  return guard([&] {
-    PRANA_CHECK(out || n == 0, "null argument");
-    synth_normal(seed, sigma, out, n);
-    return static_cast<int>(kOk);
-  });
-}
-
-int prana_synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, void* out,
-                       size_t nbytes) {
-  return guard([&] {
-    PRANA_CHECK(out, "null argument");
-    return synth_tensor(ggml_type, rows, cols, seed, sigma, static_cast<uint8_t*>(out), nbytes);
-  });
-}
-
 size_t prana_ggml_nbytes(int ggml_type, size_t n_elems) { return ggml_nbytes(ggml_type, n_elems); }
 
 }  // extern "C"

@@ -91,8 +91,14 @@ __device__ __forceinline__ void rotate(float& a, float& b, float2 cs) {
 // the multiarch build contracts four products into FMAs. This restatement
 // reproduces that evaluation exactly; it equals the host glibc expf on all
 // 2^32 inputs (exhaustive check in the GPU test suite).
-// kExp2Tab[i] = asuint64(double(2^(i/32))) - (i << 47); regenerated and
-// compared by tests/test_device_numerics.py.
+// Upstream: ARM optimized-routines math/expf.c and math/exp2f_data.c (MIT OR
+// Apache-2.0 WITH LLVM-exception), shipped in glibc as
+// sysdeps/ieee754/flt-32/e_expf.c and e_exp2f_data.c (LGPL-2.1+).
+// kExp2Tab[i] = asuint64(double(2^(i/32))) - (i << 47); the CPU test
+// tests/test_device_tables.py regenerates it from that definition. The three
+// polynomial coefficients below are upstream's minimax fit for N = 32 (with
+// the 1/N scalings folded in), kept unchanged because bit-identical results
+// need exactly upstream's constants.
 static __constant__ const uint64_t kExp2Tab[32] = {
     0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,

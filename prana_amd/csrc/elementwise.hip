@@ -435,6 +435,27 @@ int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStr
   return kOk;
 }
 
+// Seeds a decode run: state = {pos, 0}; the first step's token goes to
+// ids[0] and to tok0 (the embedding input of a replayed step). Values are
+// kernel arguments, so no host buffer has to outlive the call.
+__global__ void decode_seed_kernel(int* __restrict__ state, int pos, uint32_t token, uint32_t* __restrict__ ids,
+                                   uint32_t* __restrict__ tok0) {
+  if (threadIdx.x == 0) {
+    if (state) {
+      state[0] = pos;
+      state[1] = 0;
+    }
+    if (ids) ids[0] = token;
+    if (tok0) tok0[0] = token;
+  }
+}
+
+int launch_decode_seed(int* state, int pos, uint32_t token, uint32_t* ids, uint32_t* tok0, hipStream_t s) {
+  hipLaunchKernelGGL(decode_seed_kernel, dim3(1), dim3(64), 0, s, state, pos, token, ids, tok0);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 // ---------------------------------------------------------------- embedding
 // Embedding::row (checkpoint.rs:169-174): dense copy, or one row of a packed
 // table dequantized (kquant.rs:39-112; Q8_0 tables are f32 rows q*d as

@@ -50,6 +50,8 @@ int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale,
 // state = {position, step} in device memory: ids[step + 1] = tok[0], then
 // position and step advance by one (the tail of a replayed decode step).
 int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStream_t s);
+// state = {pos, 0}, ids[0] = token, tok0[0] = token (each pointer optional).
+int launch_decode_seed(int* state, int pos, uint32_t token, uint32_t* ids, uint32_t* tok0, hipStream_t s);
 
 // ---- gemv.hip
 // Optional dispatch timestamps for the next decode GEMV launch on this

@@ -391,16 +391,16 @@ int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint
   if ((rc = ws.step_state.ensure(8))) return rc;
   uint32_t* ids = ws.stream_out.as<uint32_t>();
   // ids[i] feeds step i; step i's argmax lands in ids[i+1].
-  PRANA_HIP(hipMemcpyAsync(ids, &token, 4, hipMemcpyHostToDevice, s));
+  if ((rc = launch_decode_seed(nullptr, 0, token, ids, nullptr, s))) return rc;
   // Steps replay a captured step (the position and the step index live in
   // device memory), one captured step per run of steps on the same attention
   // path; while GEMV dispatches are being timed, steps launch kernel by
   // kernel. Both run the same kernels on the same data.
   size_t i = 0;
   if (decode_graphs_enabled() && !gemv_profile().on && n_steps > 0) {
-    const int st[2] = {static_cast<int>(pos), 0};
-    PRANA_HIP(hipMemcpyAsync(ws.step_state.p, st, 8, hipMemcpyHostToDevice, s));
-    PRANA_HIP(hipMemcpyAsync(ws.tokens.p, &token, 4, hipMemcpyHostToDevice, s));
+    if ((rc = launch_decode_seed(ws.step_state.as<int>(), static_cast<int>(pos), token, nullptr,
+                                 ws.tokens.as<uint32_t>(), s)))
+      return rc;
     auto regime = [&](size_t k) { return attention_split_window(pos + k + 1, c.head_dim); };
     while (i < n_steps) {
       size_t j = i;

@@ -67,9 +67,4 @@ size_t ggml_nbytes(int ggml_type, size_t n_elems);
 // Host f16 conversion, same semantics as the device helpers (lib.rs:57-113).
 float host_f16_to_f32(uint16_t h);
 
-// Block encoders + synthetic values (synth.cpp).
-int quantize_tensor(int ggml_type, const float* src, size_t rows, size_t cols, uint8_t* out, size_t nbytes);
-void synth_normal(uint64_t seed, float sigma, float* out, size_t n);
-int synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, uint8_t* out, size_t nbytes);
-
 }  // namespace prana

@@ -1,4 +1,6 @@
-// Block encoders and seeded synthetic weights for random-init models.
+// Block encoders and seeded synthetic weights for random-init models: the
+// fixture side of the tests and the benchmark, built as its own host-only
+// library (libprana_synth.so) so the product library carries no encoders.
 //
 // The reference ships no Q8_0 / Q4_0 encoder (its quantize_q8 stores f32
 // scales, matmul.rs:61-84, and Q4_0 is decode-only), so Q8_0 / Q4_0 follow the
@@ -6,17 +8,36 @@
 // d = max/-8 with q = min(15, trunc(x/d + 8.5))). Q4_K / Q6_K follow the
 // reference's own converter (scripts/convert-to-gguf.py:29-89), which computes
 // in Python floats (f64) with round-half-even and packs f16 from f64.
+#include "prana_synth.h"
+
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
+#include <string>
 #include <thread>
 #include <vector>
 
-#include "runtime.h"
-
-namespace prana {
+namespace prana_synth {
 
 namespace {
+
+constexpr int kOk = 0, kErrInvalid = -1, kErrUnsupported = -4;
+
+std::string& last_error() {
+  thread_local std::string e;
+  return e;
+}
+
+int fail(int code, const char* msg) {
+  last_error() = msg;
+  return code;
+}
+
+#define SYNTH_CHECK(cond, msg)                 \
+  do {                                         \
+    if (!(cond)) return fail(kErrInvalid, msg); \
+  } while (0)
 
 uint16_t f32_to_f16_host(float x) {  // lib.rs:78-113
   uint32_t bits;
@@ -274,9 +295,9 @@ int quantize_tensor(int t, const float* src, size_t rows, size_t cols, uint8_t* 
   size_t bv, bb;
   int rc = block_shape(t, bv, bb);
   if (rc) return rc;
-  PRANA_CHECK(cols % bv == 0, "quantize_tensor: cols not a multiple of the block width");
+  SYNTH_CHECK(cols % bv == 0, "quantize_tensor: cols not a multiple of the block width");
   size_t n = rows * cols;
-  PRANA_CHECK(nbytes >= n / bv * bb, "quantize_tensor: output buffer too small");
+  SYNTH_CHECK(nbytes >= n / bv * bb, "quantize_tensor: output buffer too small");
   size_t blocks = n / bv;
   size_t per = std::max<size_t>(1, kChunk / bv);
   parallel_chunks((blocks + per - 1) / per, [&](size_t c) {
@@ -297,9 +318,9 @@ int synth_tensor(int t, size_t rows, size_t cols, uint64_t seed, float sigma, ui
   size_t bv, bb;
   int rc = block_shape(t, bv, bb);
   if (rc) return rc;
-  PRANA_CHECK(cols % bv == 0, "synth_tensor: cols not a multiple of the block width");
+  SYNTH_CHECK(cols % bv == 0, "synth_tensor: cols not a multiple of the block width");
   size_t n = rows * cols;
-  PRANA_CHECK(nbytes >= n / bv * bb, "synth_tensor: output buffer too small");
+  SYNTH_CHECK(nbytes >= n / bv * bb, "synth_tensor: output buffer too small");
   parallel_chunks((n + kChunk - 1) / kChunk, [&](size_t c) {
     std::vector<float> buf(kChunk);
     size_t i0 = c * kChunk, m = std::min(kChunk, n - i0);
@@ -309,4 +330,27 @@ int synth_tensor(int t, size_t rows, size_t cols, uint64_t seed, float sigma, ui
   return kOk;
 }
 
-}  // namespace prana
+}  // namespace prana_synth
+
+extern "C" {
+
+const char* prana_synth_last_error(void) { return prana_synth::last_error().c_str(); }
+
+int prana_quantize_tensor(int ggml_type, const float* src, size_t rows, size_t cols, void* out, size_t nbytes) {
+  if (!src || !out) return prana_synth::fail(prana_synth::kErrInvalid, "null argument");
+  return prana_synth::quantize_tensor(ggml_type, src, rows, cols, static_cast<uint8_t*>(out), nbytes);
+}
+
+int prana_synth_normal(uint64_t seed, float sigma, float* out, size_t n) {
+  if (!out && n) return prana_synth::fail(prana_synth::kErrInvalid, "null argument");
+  prana_synth::synth_normal(seed, sigma, out, n);
+  return prana_synth::kOk;
+}
+
+int prana_synth_tensor(int ggml_type, size_t rows, size_t cols, uint64_t seed, float sigma, void* out,
+                       size_t nbytes) {
+  if (!out) return prana_synth::fail(prana_synth::kErrInvalid, "null argument");
+  return prana_synth::synth_tensor(ggml_type, rows, cols, seed, sigma, static_cast<uint8_t*>(out), nbytes);
+}
+
+}  // extern "C"

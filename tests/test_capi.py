@@ -38,9 +38,19 @@ def test_error_reporting_without_gpu_work():
     lib = _lib.load()
     assert isinstance(lib.prana_last_error(), bytes)
     # an invalid encoder call fails with a message and no abort
-    rc = lib.prana_quantize_tensor(P.Q4_K, None, 1, 100, None, 0)
+    syn = _lib.load_synth()
+    rc = syn.prana_quantize_tensor(P.Q4_K, None, 1, 100, None, 0)
     assert rc == -1
-    assert b"null" in lib.prana_last_error()
+    assert b"null" in syn.prana_synth_last_error()
+
+
+def test_product_library_carries_no_fixture_encoders():
+    lib = C.CDLL(_lib.LIB_PATH)
+    for name in ("prana_quantize_tensor", "prana_synth_normal", "prana_synth_tensor"):
+        assert not hasattr(lib, name), name
+    syn = C.CDLL(_lib.SYNTH_PATH)
+    for name in _lib._SYNTH_SIGS:
+        assert hasattr(syn, name), name
 
 
 def test_ggml_nbytes():
