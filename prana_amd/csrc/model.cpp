@@ -4,6 +4,7 @@
 // bit-identical to the CPU path.
 #include "model.h"
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -335,6 +336,8 @@ void StepGraph::reset() {
   cache_buf = ids = nullptr;
 }
 
+constexpr size_t kStreamFloorIds = 4096;
+
 static bool decode_graphs_enabled() {
   static const bool on = [] {
     const char* e = std::getenv("PRANA_DECODE_GRAPH");
@@ -387,7 +390,13 @@ int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint
   PRANA_CHECK(cache.len <= 0x7fffffff, "decode: cache length out of range");
   int rc = ensure_ws(1, cache.len, false);
   if (rc) return rc;
-  if ((rc = ws.stream_out.ensure((n_steps + 1) * 4))) return rc;
+  // The token stream keeps a floor capacity and grows geometrically: its
+  // address is part of the captured step's key, so a reallocation would force
+  // a fresh capture and instantiation of the step for the next decode call.
+  if ((n_steps + 1) * 4 > ws.stream_out.bytes) {
+    const size_t want = std::max<size_t>({(n_steps + 1) * 4, 2 * ws.stream_out.bytes, kStreamFloorIds * 4});
+    if ((rc = ws.stream_out.ensure(want))) return rc;
+  }
   if ((rc = ws.step_state.ensure(8))) return rc;
   uint32_t* ids = ws.stream_out.as<uint32_t>();
   // ids[i] feeds step i; step i's argmax lands in ids[i+1].

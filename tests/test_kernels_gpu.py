@@ -209,6 +209,34 @@ def test_rmsnorm_adversarial(dim):
         assert same_bits(got[i], want[i]), i
 
 
+@pytest.mark.parametrize("dim", [64, 288, 896, 2048, 4096, 5120, 8192])
+def test_rmsnorm_register_runs_many_rows(dim):
+    # The register-run exact sum (dims % 32 == 0 up to 8192): typical rows
+    # (normal, scaled, heavy-tailed, near-constant) and tie-rich rows (small
+    # integers, powers of two) that take its fallback, all bit-exact.
+    r = rng(dim + 7)
+    rows = []
+    for k in range(48):
+        v = r.standard_normal(dim)
+        kind = k % 6
+        if kind == 1:
+            v = v * 1e-3
+        elif kind == 2:
+            v = v * np.exp(2.0 * r.standard_normal(dim))
+        elif kind == 3:
+            v = 1.0 + 1e-3 * v
+        elif kind == 4:
+            v = np.round(v * 8)
+        elif kind == 5:
+            v = np.ldexp(1.0, r.integers(-8, 8, dim))
+        rows.append(v)
+    x = np.stack(rows).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(dim)).astype(np.float32)
+    got, want = P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5)
+    for i in range(x.shape[0]):
+        assert same_bits(got[i], want[i]), i
+
+
 def test_sequential_order_closed_forms_on_device():
     from tests.test_oracle import order_cases, pv_order_case
     x_rms, y0, x_sm, p0 = order_cases()
