@@ -141,6 +141,19 @@ int prana_attention_decode(const float *q, const uint16_t *k_cache, const uint16
 int prana_attention_verify(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, size_t pos0,
                            size_t seq, size_t n_heads, size_t n_kv_heads, size_t head_dim, float *out,
                            prana_stream_t stream);
+/* Split-K flash decoding: attention_decode (attention.rs:129-160) for n_seq
+ * (1..16) independent sequences, each over its own f16 cache, in tiles of
+ * cache rows whose partial softmax states (max, sum, P.V) are merged by a
+ * second launch. Results are within 1e-4 relative of the reference's
+ * sequential order, not bit-identical (the exact path is
+ * prana_attention_decode). q, out: device [n_seq][n_heads*head_dim] f32, RoPE
+ * already applied to q; k_caches / v_caches: host arrays of n_seq device
+ * pointers to [rows][n_kv_heads*head_dim] f16; pos: host array, sequence i
+ * attends to rows 0..=pos[i]. head_dim 64 or 128; n_heads / n_kv_heads 1, 2, 4
+ * or 8. Synchronous; scratch comes from the library. */
+int prana_attention_decode_splitk(const float *q, const uint16_t *const *k_caches, const uint16_t *const *v_caches,
+                                  const size_t *pos, size_t n_seq, size_t n_heads, size_t n_kv_heads,
+                                  size_t head_dim, float *out, prana_stream_t stream);
 /* attention (prefill, attention.rs:236-284): causal over f32 K/V. */
 int prana_attention_prefill(const float *q, const float *k, const float *v, size_t seq, size_t n_heads,
                             size_t n_kv_heads, size_t head_dim, float *out, prana_stream_t stream);

@@ -74,6 +74,8 @@ _SIGS = {
     "prana_attention_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p, c_void_p]),
     "prana_attention_verify": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_size, c_void_p,
                                        c_void_p]),
+    "prana_attention_decode_splitk": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                                              c_size, c_void_p, c_void_p]),
     "prana_attention_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p,
                                         c_void_p]),
     "prana_argmax": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p]),

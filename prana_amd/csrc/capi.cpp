@@ -1,6 +1,7 @@
 // extern "C" entry points of libprana_hip (declared in include/prana_hip.h).
 // Nothing throws across this boundary: every entry point catches and turns
 // failures into status codes with a thread-local message.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -22,7 +23,7 @@ namespace {
 // intermediate buffers (quantized activations, attention scores).
 struct Scratch {
   std::mutex mu;
-  DevBuf qa, sa, sums, att;
+  DevBuf qa, sa, sums, att, flash;
 };
 Scratch& scratch() {
   static Scratch s;
@@ -363,6 +364,28 @@ int prana_attention_verify(const float* q, const uint16_t* k_cache, const uint16
                            prana_stream_t stream) {
   return guard(
       [&] { return attn_entry(q, k_cache, v_cache, pos0, seq, n_heads, n_kv_heads, head_dim, out, stream); });
+}
+
+int prana_attention_decode_splitk(const float* q, const uint16_t* const* k_caches, const uint16_t* const* v_caches,
+                                  const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                  float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(pos && n_seq >= 1 && n_seq <= 16, "attention_decode_splitk: 1..16 sequences");
+    PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "attention_decode_splitk: n_heads must be a multiple of n_kv_heads");
+    Scratch& sc = scratch();
+    std::lock_guard<std::mutex> lk(sc.mu);
+    const FlashPlan plan = flash_decode_plan(pos, n_seq, n_heads, n_kv_heads, head_dim);
+    int rc = sc.flash.ensure(std::max<size_t>(plan.scratch_floats, 1) * 4);
+    if (rc) return rc;
+    hipStream_t s = pick_stream(stream);
+    rc = launch_flash_decode(q, k_caches, v_caches, pos, n_seq, n_heads, n_kv_heads, head_dim, out,
+                             sc.flash.as<float>(), sc.flash.bytes / 4, s);
+    if (rc) return rc;
+    PRANA_HIP(hipStreamSynchronize(s));
+    return static_cast<int>(kOk);
+  });
 }
 
 int prana_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,

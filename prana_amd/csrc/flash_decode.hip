@@ -1,0 +1,310 @@
+// Split-K flash decoding over the f16 KV cache: the attention of
+// attention_decode (attention.rs:129-195) for independent sequences with long
+// windows, evaluated in tiles of cache rows whose partial softmax states are
+// merged afterwards. The f32 result is within 1e-4 relative of the
+// reference's sequential order (it is not bit-identical: the score dots, the
+// softmax sum and the P.V fold are reassociated); the exact one-query kernels
+// in attention.hip remain the path of the model's decode.
+//
+//   split  : one workgroup per (tile of T cache rows, KV head, sequence). A K
+//            or V row of one KV head is read once, coalesced (hd/8 lanes x 16
+//            bytes), and serves the G query heads of its group: every lane
+//            holds 8 dims of q for each of them, the G partial dots of a row
+//            are reduced over its hd/8 lanes with DPP, and the tile's max,
+//            sum of exp(s - max) and P.V accumulators are kept per head.
+//   combine: one workgroup per (query head, sequence), one lane per dim:
+//            M = max m_s, L = sum l_s exp(m_s - M),
+//            out = sum acc_s exp(m_s - M) / L.
+// Every K/V byte is read once, with all of a tile's loads in flight at once,
+// so the split kernel is bound by HBM bandwidth.
+#include <algorithm>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace prana {
+
+namespace {
+
+constexpr int kFdNT = 256;  // lanes per split workgroup (4 waves)
+constexpr int kFdMaxSeq = 16;
+
+struct FlashArgs {
+  const float* q;  // [n_seq][n_heads * hd], RoPE applied
+  const uint16_t* kc[kFdMaxSeq];
+  const uint16_t* vc[kFdMaxSeq];
+  int pos[kFdMaxSeq];  // attends to rows 0..=pos of sequence s
+  int n_heads, n_kv_heads, max_splits, rows_per_split;
+  float scale;  // 1 / sqrt(hd), as attention.rs:172 computes it
+  float* part;  // [n_seq][n_heads][max_splits][hd + 2]: acc[hd], m, l
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of LPR lanes (8 or 16), every lane getting it.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror: the other quad of the 8-lane half
+  if constexpr (LPR == 16) v += dpp_f<0x140>(v);  // row_mirror: the other half of the row
+  return v;
+}
+
+__device__ __forceinline__ void halves8(const uint4& w, float* x) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    x[2 * k] = f16_operand(static_cast<uint16_t>(u[k] & 0xffffu));
+    x[2 * k + 1] = f16_operand(static_cast<uint16_t>(u[k] >> 16));
+  }
+}
+
+// HD: head width (64 or 128); G: query heads per KV head; ITER: rows each
+// lane group takes per tile (T = 4 waves * ITER * 512/HD rows).
+template <int HD, int G, int ITER>
+__global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
+  constexpr int LPR = HD / 8;      // lanes per cache row
+  constexpr int RPI = 64 / LPR;    // rows per wave per iteration
+  constexpr int T = 4 * ITER * RPI;
+  __shared__ float s_p[G][T];
+  __shared__ float s_red[4][G];
+  __shared__ float s_acc[4][G][HD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = lane / LPR, sub = lane % LPR;
+  const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int n = a.pos[seq] + 1;
+  const int r0 = split * T;
+  if (r0 >= n) return;  // uniform: past this sequence's window
+  const int kv_stride = a.n_kv_heads * HD;
+  const uint16_t* kb = a.kc[seq] + (size_t)kvh * HD + sub * 8;
+  const uint16_t* vb = a.vc[seq] + (size_t)kvh * HD + sub * 8;
+  const int wrow0 = r0 + wave * ITER * RPI + rg;  // this lane group's first row
+  // every K and V load of the tile in flight at once (rows past the window
+  // read row n-1 and are masked below)
+  uint4 kr[ITER], vr[ITER];
+#pragma unroll
+  for (int it = 0; it < ITER; it++) {
+    const int row = min(wrow0 + it * RPI, n - 1);
+    kr[it] = *reinterpret_cast<const uint4*>(kb + (size_t)row * kv_stride);
+  }
+#pragma unroll
+  for (int it = 0; it < ITER; it++) {
+    const int row = min(wrow0 + it * RPI, n - 1);
+    vr[it] = *reinterpret_cast<const uint4*>(vb + (size_t)row * kv_stride);
+  }
+  float qv[G][8];
+  const int h0 = kvh * G;
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0 + g) * HD + sub * 8);
+    const float4 x0 = qp[0], x1 = qp[1];
+    qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
+    qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+  }
+  // scores
+  float mx[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) mx[g] = -INFINITY;
+#pragma unroll
+  for (int it = 0; it < ITER; it++) {
+    float k8[8];
+    halves8(kr[it], k8);
+    const int row = wrow0 + it * RPI;
+    const int lr = row - r0;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float d = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) d += qv[g][k] * k8[k];
+      d = group_sum<LPR>(d) * a.scale;
+      const bool valid = row < n;
+      if (sub == 0) s_p[g][lr] = valid ? d : -INFINITY;
+      mx[g] = valid ? fmaxf(mx[g], d) : mx[g];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float m = mx[g];
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) s_red[wave][g] = m;
+  }
+  __syncthreads();
+  float m_g[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) m_g[g] = fmaxf(fmaxf(s_red[0][g], s_red[1][g]), fmaxf(s_red[2][g], s_red[3][g]));
+  // probabilities of the tile (relative to its own max) and their sums
+  float lsum[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float l = 0.0f;
+    for (int r = tid; r < T; r += kFdNT) {
+      const float p = __expf(s_p[g][r] - m_g[g]);  // exp(-inf) = 0 past the window
+      s_p[g][r] = p;
+      l += p;
+    }
+    lsum[g] = l;
+  }
+  __syncthreads();  // s_red is reused below, s_p holds probabilities
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float l = lsum[g];
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) s_red[wave][g] = l;
+  }
+  // P.V over this lane group's rows
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; g++)
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[g][k] = 0.0f;
+#pragma unroll
+  for (int it = 0; it < ITER; it++) {
+    const int row = wrow0 + it * RPI;
+    if (row < n) {
+      float v8[8];
+      halves8(vr[it], v8);
+      const int lr = row - r0;
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const float p = s_p[g][lr];
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc[g][k] += p * v8[k];
+      }
+    }
+  }
+  // sum the wave's lane groups (lanes LPR apart), then the four waves
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int k = 0; k < 8; k++) acc[g][k] += __shfl_xor(acc[g][k], o, 64);
+  if (rg == 0)
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int k = 0; k < 8; k++) s_acc[wave][g][sub * 8 + k] = acc[g][k];
+  __syncthreads();
+  float* base = a.part + (((size_t)seq * a.n_heads + h0) * a.max_splits + split) * (HD + 2);
+  const size_t hstride = (size_t)a.max_splits * (HD + 2);
+  for (int e = tid; e < G * HD; e += kFdNT) {
+    const int g = e / HD, d = e % HD;
+    base[g * hstride + d] = (s_acc[0][g][d] + s_acc[1][g][d]) + (s_acc[2][g][d] + s_acc[3][g][d]);
+  }
+  if (tid < G) {
+    base[tid * hstride + HD] = m_g[tid];
+    base[tid * hstride + HD + 1] = (s_red[0][tid] + s_red[1][tid]) + (s_red[2][tid] + s_red[3][tid]);
+  }
+}
+
+struct CombineArgs {
+  const float* part;
+  int n_splits[kFdMaxSeq];
+  int n_heads, max_splits;
+  float* out;
+};
+
+template <int HD>
+__global__ __launch_bounds__(HD) void flash_combine_kernel(CombineArgs c) {
+  const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+  const float* p = c.part + ((size_t)seq * c.n_heads + h) * c.max_splits * (HD + 2);
+  const int ns = c.n_splits[seq];
+  float M = -INFINITY;
+  for (int s = 0; s < ns; s++) M = fmaxf(M, p[(size_t)s * (HD + 2) + HD]);
+  float L = 0.0f, o = 0.0f;
+  for (int s = 0; s < ns; s++) {
+    const float* ps = p + (size_t)s * (HD + 2);
+    const float w = __expf(ps[HD] - M);
+    L += ps[HD + 1] * w;
+    o += ps[d] * w;
+  }
+  c.out[((size_t)seq * c.n_heads + h) * HD + d] = o / L;
+}
+
+template <int HD, int G, int ITER>
+int launch_flash_t(const FlashArgs& a, const CombineArgs& c, int n_seq, hipStream_t s) {
+  hipLaunchKernelGGL((flash_split_kernel<HD, G, ITER>), dim3(a.max_splits, a.n_kv_heads, n_seq), dim3(kFdNT), 0, s,
+                     a);
+  PRANA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(flash_combine_kernel<HD>, dim3(a.n_heads, n_seq), dim3(HD), 0, s, c);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+template <int HD, int G>
+int launch_flash_g(const FlashArgs& a, const CombineArgs& c, int iter, int n_seq, hipStream_t s) {
+  if (iter == 16) return launch_flash_t<HD, G, (G > 4 ? 8 : 16)>(a, c, n_seq, s);
+  return launch_flash_t<HD, G, 4>(a, c, n_seq, s);
+}
+
+template <int HD>
+int launch_flash_hd(const FlashArgs& a, const CombineArgs& c, int g, int iter, int n_seq, hipStream_t s) {
+  switch (g) {
+    case 1: return launch_flash_g<HD, 1>(a, c, iter, n_seq, s);
+    case 2: return launch_flash_g<HD, 2>(a, c, iter, n_seq, s);
+    case 4: return launch_flash_g<HD, 4>(a, c, iter, n_seq, s);
+    case 8: return launch_flash_g<HD, 8>(a, c, iter, n_seq, s);
+  }
+  return fail(kErrUnsupported, "flash decode: query heads per KV head must be 1, 2, 4 or 8");
+}
+
+}  // namespace
+
+// Tile size: long windows take T = 4 waves * 16 rows per lane group; shorter
+// ones a quarter of that, so the grid still spreads over the CUs.
+FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd) {
+  FlashPlan p{};
+  const int g = static_cast<int>(n_heads / std::max<size_t>(n_kv_heads, 1));
+  const int rpi = static_cast<int>(512 / std::max<size_t>(hd, 1));
+  size_t max_rows = 0;
+  for (size_t i = 0; i < n_seq; i++) max_rows = std::max(max_rows, pos[i] + 1);
+  const int big_iter = g > 4 ? 8 : 16;
+  const size_t t_big = static_cast<size_t>(4 * big_iter * rpi);
+  const size_t wgs_big = (max_rows + t_big - 1) / t_big * n_kv_heads * n_seq;
+  p.iter = wgs_big >= 512 ? 16 : 4;
+  p.rows_per_split = p.iter == 16 ? static_cast<int>(t_big) : 4 * 4 * rpi;
+  p.max_splits = static_cast<int>((max_rows + p.rows_per_split - 1) / p.rows_per_split);
+  p.scratch_floats = n_seq * n_heads * static_cast<size_t>(p.max_splits) * (hd + 2);
+  return p;
+}
+
+int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const uint16_t* const* v_caches,
+                        const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd, float* out,
+                        float* scratch, size_t scratch_floats, hipStream_t s) {
+  PRANA_CHECK(n_seq >= 1 && n_seq <= static_cast<size_t>(kFdMaxSeq), "flash decode: 1..16 sequences per call");
+  PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "flash decode: n_heads must be a multiple of n_kv_heads");
+  PRANA_CHECK(hd == 64 || hd == 128, "flash decode: head_dim must be 64 or 128");
+  PRANA_CHECK(q && out && k_caches && v_caches && pos && scratch, "flash decode: null argument");
+  const FlashPlan plan = flash_decode_plan(pos, n_seq, n_heads, n_kv_heads, hd);
+  PRANA_CHECK(scratch_floats >= plan.scratch_floats, "flash decode: scratch below the plan's size");
+  FlashArgs a{};
+  CombineArgs c{};
+  a.q = q;
+  for (size_t i = 0; i < n_seq; i++) {
+    PRANA_CHECK(k_caches[i] && v_caches[i], "flash decode: null cache pointer");
+    PRANA_CHECK(pos[i] < 0x7fffffffu, "flash decode: position out of range");
+    a.kc[i] = k_caches[i];
+    a.vc[i] = v_caches[i];
+    a.pos[i] = static_cast<int>(pos[i]);
+    c.n_splits[i] = static_cast<int>((pos[i] + plan.rows_per_split) / plan.rows_per_split);
+  }
+  a.n_heads = static_cast<int>(n_heads);
+  a.n_kv_heads = static_cast<int>(n_kv_heads);
+  a.max_splits = plan.max_splits;
+  a.rows_per_split = plan.rows_per_split;
+  a.scale = 1.0f / sqrtf(static_cast<float>(hd));
+  a.part = scratch;
+  c.part = scratch;
+  c.n_heads = a.n_heads;
+  c.max_splits = a.max_splits;
+  c.out = out;
+  const int g = static_cast<int>(n_heads / n_kv_heads);
+  if (hd == 128) return launch_flash_hd<128>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
+  return launch_flash_hd<64>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
+}
+
+}  // namespace prana

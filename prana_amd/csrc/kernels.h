@@ -149,4 +149,20 @@ int launch_attention_prefill(const float* q, const float* k, const float* v, siz
                              size_t n_kv_heads, size_t hd, float* out, float* scratch, hipStream_t s,
                              const ActQuant* aq = nullptr, bool* quantized = nullptr);
 
+// ---- flash_decode.hip
+// Split-K flash decoding (attention_decode, attention.rs:129-195, for up to 16
+// independent sequences; f32 within 1e-4 relative, not bit-exact). The plan
+// fixes the tile size and the partial-state scratch a call needs.
+struct FlashPlan {
+  int iter, rows_per_split, max_splits;
+  size_t scratch_floats;
+};
+FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd);
+// k_caches / v_caches: host arrays of n_seq device pointers ([rows][n_kv_heads*hd]
+// f16 each); pos: host array, sequence i attends to rows 0..=pos[i]; q / out:
+// device [n_seq][n_heads*hd] f32.
+int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const uint16_t* const* v_caches,
+                        const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd, float* out,
+                        float* scratch, size_t scratch_floats, hipStream_t s);
+
 }  // namespace prana
