@@ -12,11 +12,12 @@
 //            holds 8 dims of q for each of them, the G partial dots of a row
 //            are reduced over its hd/8 lanes with DPP, and the tile's max,
 //            sum of exp(s - max) and P.V accumulators are kept per head.
-//   combine: one workgroup per (query head, sequence), one lane per dim:
+//   combine: one workgroup per (query head, sequence):
 //            M = max m_s, L = sum l_s exp(m_s - M),
-//            out = sum acc_s exp(m_s - M) / L.
+//            out = sum acc_s exp(m_s - M) / L, in parallel over splits.
 // Every K/V byte is read once, with all of a tile's loads in flight at once,
-// so the split kernel is bound by HBM bandwidth.
+// so the split kernel is bound by HBM bandwidth. Products are fused
+// (explicit fmaf): this path is not held to the reference's rounding.
 #include <algorithm>
 
 #include "common.h"
@@ -104,7 +105,10 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
     const float4 x0 = qp[0], x1 = qp[1];
     qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
     qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+#pragma unroll
+    for (int k = 0; k < 8; k++) qv[g][k] *= a.scale;  // (q/sqrt(hd)).k
   }
+  const bool full = r0 + T <= n;  // uniform: no row of the tile lies past the window
   // scores
   float mx[G];
 #pragma unroll
@@ -119,9 +123,9 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
     for (int g = 0; g < G; g++) {
       float d = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; k++) d += qv[g][k] * k8[k];
-      d = group_sum<LPR>(d) * a.scale;
-      const bool valid = row < n;
+      for (int k = 0; k < 8; k++) d = fmaf(qv[g][k], k8[k], d);
+      d = group_sum<LPR>(d);
+      const bool valid = full || row < n;
       if (sub == 0) s_p[g][lr] = valid ? d : -INFINITY;
       mx[g] = valid ? fmaxf(mx[g], d) : mx[g];
     }
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     const int row = wrow0 + it * RPI;
-    if (row < n) {
+    if (full || row < n) {
       float v8[8];
       halves8(vr[it], v8);
       const int lr = row - r0;
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
       for (int g = 0; g < G; g++) {
         const float p = s_p[g][lr];
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc[g][k] += p * v8[k];
+        for (int k = 0; k < 8; k++) acc[g][k] = fmaf(p, v8[k], acc[g][k]);
       }
     }
   }
@@ -208,21 +212,62 @@ struct CombineArgs {
   float* out;
 };
 
+constexpr int kFcNT = 256;
+
+// One workgroup per (query head, sequence): the split maxima and weights
+// w_s = exp(m_s - M) in parallel over splits, then every dim's weighted sum
+// with the splits divided over kFcNT / HD lane groups (independent loads).
 template <int HD>
-__global__ __launch_bounds__(HD) void flash_combine_kernel(CombineArgs c) {
-  const int h = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c) {
+  constexpr int PG = kFcNT / HD;  // lane groups per dim
+  extern __shared__ float s_w[];  // max_splits weights
+  __shared__ float s_r[kFcNT / 64];
+  __shared__ float s_o[PG][HD];
+  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* p = c.part + ((size_t)seq * c.n_heads + h) * c.max_splits * (HD + 2);
   const int ns = c.n_splits[seq];
   float M = -INFINITY;
-  for (int s = 0; s < ns; s++) M = fmaxf(M, p[(size_t)s * (HD + 2) + HD]);
-  float L = 0.0f, o = 0.0f;
-  for (int s = 0; s < ns; s++) {
-    const float* ps = p + (size_t)s * (HD + 2);
+  for (int sp = tid; sp < ns; sp += kFcNT) M = fmaxf(M, p[(size_t)sp * (HD + 2) + HD]);
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  if (lane == 0) s_r[wave] = M;
+  __syncthreads();
+  M = s_r[0];
+#pragma unroll
+  for (int w = 1; w < kFcNT / 64; w++) M = fmaxf(M, s_r[w]);
+  __syncthreads();  // s_r is reused for L
+  float L = 0.0f;
+  for (int sp = tid; sp < ns; sp += kFcNT) {
+    const float* ps = p + (size_t)sp * (HD + 2);
     const float w = __expf(ps[HD] - M);
-    L += ps[HD + 1] * w;
-    o += ps[d] * w;
+    s_w[sp] = w;
+    L = fmaf(ps[HD + 1], w, L);
   }
-  c.out[((size_t)seq * c.n_heads + h) * HD + d] = o / L;
+  for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+  if (lane == 0) s_r[wave] = L;
+  __syncthreads();
+  L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kFcNT / 64; w++) L += s_r[w];
+  const int d = tid % HD, pg = tid / HD;
+  float o = 0.0f;
+  int sp = pg;
+  for (; sp + 3 * PG < ns; sp += 4 * PG) {  // four independent loads per step
+    const float a0 = p[(size_t)sp * (HD + 2) + d], a1 = p[(size_t)(sp + PG) * (HD + 2) + d];
+    const float a2 = p[(size_t)(sp + 2 * PG) * (HD + 2) + d], a3 = p[(size_t)(sp + 3 * PG) * (HD + 2) + d];
+    o = fmaf(a0, s_w[sp], o);
+    o = fmaf(a1, s_w[sp + PG], o);
+    o = fmaf(a2, s_w[sp + 2 * PG], o);
+    o = fmaf(a3, s_w[sp + 3 * PG], o);
+  }
+  for (; sp < ns; sp += PG) o = fmaf(p[(size_t)sp * (HD + 2) + d], s_w[sp], o);
+  s_o[pg][d] = o;
+  __syncthreads();
+  if (tid < HD) {
+    float t = 0.0f;
+#pragma unroll
+    for (int g = 0; g < PG; g++) t += s_o[g][tid];
+    c.out[((size_t)seq * c.n_heads + h) * HD + tid] = t / L;
+  }
 }
 
 template <int HD, int G, int ITER>
@@ -230,14 +275,14 @@ int launch_flash_t(const FlashArgs& a, const CombineArgs& c, int n_seq, hipStrea
   hipLaunchKernelGGL((flash_split_kernel<HD, G, ITER>), dim3(a.max_splits, a.n_kv_heads, n_seq), dim3(kFdNT), 0, s,
                      a);
   PRANA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(flash_combine_kernel<HD>, dim3(a.n_heads, n_seq), dim3(HD), 0, s, c);
+  hipLaunchKernelGGL(flash_combine_kernel<HD>, dim3(a.n_heads, n_seq), dim3(kFcNT), (size_t)a.max_splits * 4, s, c);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
 
 template <int HD, int G>
 int launch_flash_g(const FlashArgs& a, const CombineArgs& c, int iter, int n_seq, hipStream_t s) {
-  if (iter == 16) return launch_flash_t<HD, G, (G > 4 ? 8 : 16)>(a, c, n_seq, s);
+  if (iter == 16) return launch_flash_t<HD, G, 8>(a, c, n_seq, s);
   return launch_flash_t<HD, G, 4>(a, c, n_seq, s);
 }
 
@@ -254,15 +299,17 @@ int launch_flash_hd(const FlashArgs& a, const CombineArgs& c, int g, int iter, i
 
 }  // namespace
 
-// Tile size: long windows take T = 4 waves * 16 rows per lane group; shorter
-// ones a quarter of that, so the grid still spreads over the CUs.
+// Tile size: long windows take T = 4 waves * 8 rows per lane group (small
+// enough in registers for several workgroups per CU, whose load and compute
+// phases then overlap); shorter ones half that, so the grid still spreads
+// over the CUs.
 FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd) {
   FlashPlan p{};
   const int g = static_cast<int>(n_heads / std::max<size_t>(n_kv_heads, 1));
   const int rpi = static_cast<int>(512 / std::max<size_t>(hd, 1));
   size_t max_rows = 0;
   for (size_t i = 0; i < n_seq; i++) max_rows = std::max(max_rows, pos[i] + 1);
-  const int big_iter = g > 4 ? 8 : 16;
+  const int big_iter = 8;
   const size_t t_big = static_cast<size_t>(4 * big_iter * rpi);
   const size_t wgs_big = (max_rows + t_big - 1) / t_big * n_kv_heads * n_seq;
   p.iter = wgs_big >= 512 ? 16 : 4;

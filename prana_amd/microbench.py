@@ -5,8 +5,11 @@ C1: the Q8_0 matmul sweep (R x K in {4096x4096, 14336x4096, 4096x14336,
 32000x4096}, N in {1, 4, 16, 64} tokens). Weight copies rotate so that the
 bytes touched per case exceed twice the 256 MB MALL.
 C3: attention over an f16 cache (32 query / 8 KV heads, head_dim 128) at
-contexts 1024, 4096, 16384 and 32768, for one query row (decode) and for
-eight query rows over one cache (the verify form).
+contexts 1024, 4096, 16384 and 32768, q and the new k row under NeoX RoPE at
+position = context: one sequence (decode) on the exact kernels and on split-K
+flash decoding, eight query rows over one cache (the verify form), and batch
+8 as eight independent caches on both paths. Cache copies rotate so that the
+bytes touched per case exceed twice the MALL.
 
 Timing comes from a rocprofv3 kernel trace, so there is no host overhead in
 the figures. Run
@@ -21,6 +24,7 @@ lands in a timed group. The summary sums every non-runtime kernel between
 the second and third marker of a case, activation quantization included.
 """
 import argparse
+import ctypes as C
 import json
 import os
 import sqlite3
@@ -43,7 +47,7 @@ def _marker(P, buf):
     P.check(P.load().prana_memset_d(buf.ptr, 0, 256))
 
 
-def run(manifest_path):
+def run(manifest_path, only=None):
     import prana_amd as P
 
     P.init()
@@ -51,7 +55,7 @@ def run(manifest_path):
     cases = []
     rng = np.random.default_rng(0)
 
-    for rows, cols in C1_SHAPES:
+    for rows, cols in (C1_SHAPES if only in (None, "C1") else []):
         raw = P.synth_tensor(Q8_0, rows, cols, rows * 7 + cols, 0.02)
         copies = max(3, -(-2 * MALL // raw.nbytes))
         mats = [P.Matrix(Q8_0, rows, cols, raw) for _ in range(copies)]
@@ -71,27 +75,71 @@ def run(manifest_path):
 
     nh, nkv, hd = 32, 8, 128
     kv = nkv * hd
-    for ctx in C3_CTX:
+    lib = P.load()
+    for ctx in (C3_CTX if only in (None, "C3") else []):
         print(f"C3 ctx={ctx}", file=sys.stderr, flush=True)
-        for b in (1, 8):
-            rows = ctx + b
-            k = P.DeviceArray.from_host(rng.standard_normal(rows * kv).astype(np.float16).view(np.uint16))
-            v = P.DeviceArray.from_host(rng.standard_normal(rows * kv).astype(np.float16).view(np.uint16))
-            q = P.DeviceArray.from_host(rng.standard_normal(b * nh * hd).astype(np.float32))
-            out = P.DeviceArray((b * nh * hd,), np.float32)
+        rows = ctx + 1
+        per_seq = 2 * rows * kv * 2
+        # q and the new k row get NeoX RoPE (theta 1e4) at position ctx
+        q8 = np.stack([P.rope(r[None, :], ctx, hd, 1e4, True)[0]
+                       for r in rng.standard_normal((8, nh * hd)).astype(np.float32)])
+        knew = np.stack([P.rope(r[None, :], ctx, hd, 1e4, True)[0]
+                         for r in rng.standard_normal((8, kv)).astype(np.float32)])
+        kh = rng.standard_normal((rows, kv)).astype(np.float16).view(np.uint16)
+        vh = rng.standard_normal((rows, kv)).astype(np.float16).view(np.uint16)
+        # cache copies (same values, distinct addresses) rotate past 2 x MALL
+        n_cache = max(8, -(-2 * MALL // per_seq))
+        kcs, vcs = [], []
+        for i in range(n_cache):
+            kh[ctx] = P.f32_to_f16(knew[i % 8])
+            kcs.append(P.DeviceArray.from_host(kh))
+            vcs.append(P.DeviceArray.from_host(vh))
+        q = P.DeviceArray.from_host(q8)
+        out = P.DeviceArray((8, nh * hd), np.float32)
+        pos8 = (C.c_size_t * 8)(*([ctx] * 8))
+
+        def ptrs(lst, i0, n):
+            return (C.c_void_p * n)(*[lst[(i0 + j) % n_cache].ptr.value for j in range(n)])
+
+        def exact_b1(i):
+            P.check(lib.prana_attention_decode(q.ptr, kcs[i % n_cache].ptr, vcs[i % n_cache].ptr, ctx, nh, nkv, hd,
+                                               out.ptr, None))
+
+        def split_b1(i):
+            P.check(lib.prana_attention_decode_splitk(q.ptr, ptrs(kcs, i, 1), ptrs(vcs, i, 1), pos8, 1, nh, nkv,
+                                                      hd, out.ptr, None))
+
+        def exact_b8(i):
+            for j in range(8):
+                c = (8 * i + j) % n_cache
+                P.check(lib.prana_attention_decode(C.c_void_p(q.ptr.value + j * nh * hd * 4), kcs[c].ptr,
+                                                   vcs[c].ptr, ctx, nh, nkv, hd,
+                                                   C.c_void_p(out.ptr.value + j * nh * hd * 4), None))
+
+        def split_b8(i):
+            P.check(lib.prana_attention_decode_splitk(q.ptr, ptrs(kcs, 8 * i, 8), ptrs(vcs, 8 * i, 8), pos8, 8, nh,
+                                                      nkv, hd, out.ptr, None))
+
+        def verify8(i):
+            # eight query rows at ctx-7..ctx over one cache (the verify form)
+            c = i % n_cache
+            P.check(lib.prana_attention_verify(q.ptr, kcs[c].ptr, vcs[c].ptr, ctx - 7, 8, nh, nkv, hd, out.ptr,
+                                               None))
+
+        for tag, fn, b in (("decode, exact", exact_b1, 1), ("decode, split-K", split_b1, 1),
+                           ("8 query rows at ctx-7..ctx over one cache (verify form), exact", verify8, 1),
+                           ("batch 8 (eight independent caches), exact", exact_b8, 8),
+                           ("batch 8 (eight independent caches), split-K", split_b8, 8)):
             for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
                 _marker(P, marker)
-                for _ in range(calls):
-                    if b == 1:
-                        rc = P.load().prana_attention_decode(q.ptr, k.ptr, v.ptr, ctx, nh, nkv, hd, out.ptr, None)
-                    else:
-                        rc = P.load().prana_attention_verify(q.ptr, k.ptr, v.ptr, ctx, b, nh, nkv, hd, out.ptr, None)
-                    P.check(rc)
+                for i in range(calls):
+                    fn(i)
             _marker(P, marker)
-            P.check(P.load().prana_synchronize())
-            form = "decode" if b == 1 else f"{b} query rows at ctx..ctx+{b - 1} (verify form)"
-            cases.append({"config": "C3", "case": f"ctx={ctx} {form}", "calls": TIMED,
-                          "bytes": 2 * rows * kv * 2 + b * nh * hd * 8})
+            P.check(lib.prana_synchronize())
+            cases.append({"config": "C3", "case": f"ctx={ctx} {tag}", "calls": TIMED,
+                          "bytes": b * per_seq + b * nh * hd * 8})
+        for a in kcs + vcs:
+            a.free()
     with open(manifest_path, "w") as f:
         json.dump(cases, f, indent=1)
     print(f"wrote {len(cases)} cases to {manifest_path}", file=sys.stderr)
@@ -187,6 +235,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--summarize", metavar="DB")
     ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
+    ap.add_argument("--only", choices=["C1", "C3"], help="run one configuration's sweep")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
     if args.models:
@@ -194,7 +243,7 @@ def main():
     elif args.summarize:
         summarize(args.summarize, args.manifest)
     else:
-        run(args.manifest)
+        run(args.manifest, args.only)
 
 
 if __name__ == "__main__":
