@@ -154,6 +154,19 @@ int prana_attention_verify(const float *q, const uint16_t *k_cache, const uint16
 int prana_attention_decode_splitk(const float *q, const uint16_t *const *k_caches, const uint16_t *const *v_caches,
                                   const size_t *pos, size_t n_seq, size_t n_heads, size_t n_kv_heads,
                                   size_t head_dim, float *out, prana_stream_t stream);
+/* prana_attention_decode_splitk without any allocation: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops). The partial softmax states go to a
+ * fixed array of the library, 2^23 floats (32 MiB) per GPU, held until the
+ * process ends; a call whose plan needs more (n_seq * n_heads *
+ * ceil(rows/tile) * (head_dim + 2) floats) fails with PRANA_ERR_INVALID.
+ * Asynchronous on `stream` (NULL = the library's); prana_init must have run.
+ * Every call on one GPU shares that GPU's array, so calls that overlap on one
+ * GPU race; the array keeps the last call's contents. */
+int prana_attention_decode_splitk_noalloc(const float *q, const uint16_t *const *k_caches,
+                                          const uint16_t *const *v_caches, const size_t *pos, size_t n_seq,
+                                          size_t n_heads, size_t n_kv_heads, size_t head_dim, float *out,
+                                          prana_stream_t stream);
 /* attention (prefill, attention.rs:236-284): causal over f32 K/V. */
 int prana_attention_prefill(const float *q, const float *k, const float *v, size_t seq, size_t n_heads,
                             size_t n_kv_heads, size_t head_dim, float *out, prana_stream_t stream);

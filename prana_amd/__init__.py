@@ -296,6 +296,23 @@ def attention_decode_splitk(q, kcs, vcs, pos, n_heads, n_kv_heads, head_dim):
     return do.to_host()
 
 
+def attention_decode_splitk_noalloc(q, kcs, vcs, pos, n_heads, n_kv_heads, head_dim):
+    """attention_decode_splitk through the allocation-free entry point (the
+    library's fixed partial-state array); synchronises after the call."""
+    n = len(pos)
+    dq = DeviceArray.from_host(np.asarray(q, np.float32).reshape(n, n_heads * head_dim))
+    dk = [c if isinstance(c, DeviceArray) else DeviceArray.from_host(np.asarray(c, np.uint16)) for c in kcs]
+    dv = [c if isinstance(c, DeviceArray) else DeviceArray.from_host(np.asarray(c, np.uint16)) for c in vcs]
+    kp = (C.c_void_p * n)(*[c.ptr.value for c in dk])
+    vp = (C.c_void_p * n)(*[c.ptr.value for c in dv])
+    ps = (C.c_size_t * n)(*[int(p) for p in pos])
+    do = DeviceArray((n, n_heads * head_dim), np.float32)
+    check(load().prana_attention_decode_splitk_noalloc(dq.ptr, kp, vp, ps, n, n_heads, n_kv_heads, head_dim, do.ptr,
+                                                        None))
+    check(load().prana_synchronize())
+    return do.to_host()
+
+
 def attention_prefill(q, k, v, seq, n_heads, n_kv_heads, head_dim):
     dq, dk, dv = (DeviceArray.from_host(np.asarray(q, np.float32)), DeviceArray.from_host(np.asarray(k, np.float32)),
                   DeviceArray.from_host(np.asarray(v, np.float32)))

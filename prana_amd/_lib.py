@@ -76,6 +76,8 @@ _SIGS = {
                                        c_void_p]),
     "prana_attention_decode_splitk": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
                                               c_size, c_void_p, c_void_p]),
+    "prana_attention_decode_splitk_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
+                                                      c_size, c_size, c_void_p, c_void_p]),
     "prana_attention_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_size, c_void_p,
                                         c_void_p]),
     "prana_argmax": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p]),

@@ -388,6 +388,28 @@ int prana_attention_decode_splitk(const float* q, const uint16_t* const* k_cache
   });
 }
 
+int prana_attention_decode_splitk_noalloc(const float* q, const uint16_t* const* k_caches,
+                                          const uint16_t* const* v_caches, const size_t* pos, size_t n_seq,
+                                          size_t n_heads, size_t n_kv_heads, size_t head_dim, float* out,
+                                          prana_stream_t stream) {
+  return guard([&] {
+    if (int rc = require_init()) return rc;
+    PRANA_CHECK(pos && n_seq >= 1 && n_seq <= 16, "attention_decode_splitk_noalloc: 1..16 sequences");
+    PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "attention_decode_splitk_noalloc: n_heads must be a multiple of n_kv_heads");
+    float* sc = flash_noalloc_scratch(ctx().device);
+    PRANA_CHECK(sc, "attention_decode_splitk_noalloc: scratch array address unknown");
+    const FlashPlan plan = flash_decode_plan(pos, n_seq, n_heads, n_kv_heads, head_dim);
+    if (plan.scratch_floats > kFlashNoAllocFloats)
+      return fail(kErrInvalid, "attention_decode_splitk_noalloc: the call needs " +
+                                   std::to_string(plan.scratch_floats) + " scratch floats, above the fixed " +
+                                   std::to_string(kFlashNoAllocFloats) +
+                                   " (fewer sequences or shorter windows, or prana_attention_decode_splitk)");
+    return launch_flash_decode(q, k_caches, v_caches, pos, n_seq, n_heads, n_kv_heads, head_dim, out, sc,
+                               kFlashNoAllocFloats, pick_stream(stream));
+  });
+}
+
 int prana_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
                             size_t n_kv_heads, size_t head_dim, float* out, prana_stream_t stream) {
   return guard([&] {

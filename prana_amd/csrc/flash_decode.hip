@@ -25,6 +25,34 @@
 
 namespace prana {
 
+// Partial-state scratch of prana_attention_decode_splitk_noalloc: a fixed
+// array in device memory (one copy per GPU, held until the process ends).
+// Host code never uses the array's name as an address: the device address
+// comes from hipGetSymbolAddress, looked up once per device at set-up
+// (flash_noalloc_setup, called by the library's init with the device
+// current) and kept in g_scratch_dev.
+static __device__ __align__(256) float scratch[kFlashNoAllocFloats];
+
+namespace {
+constexpr int kMaxDevices = 16;
+float* g_scratch_dev[kMaxDevices] = {};
+}  // namespace
+
+int flash_noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(kErrUnsupported, "flash scratch: device index out of range");
+  if (g_scratch_dev[device]) return kOk;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  if (!p) return fail(kErrHip, "hipGetSymbolAddress(scratch) returned a null address");
+  g_scratch_dev[device] = static_cast<float*>(p);
+  return kOk;
+}
+
+float* flash_noalloc_scratch(int device) {
+  return device >= 0 && device < kMaxDevices ? g_scratch_dev[device] : nullptr;
+}
+
 namespace {
 
 constexpr int kFdNT = 256;  // lanes per split workgroup (4 waves)
@@ -321,13 +349,13 @@ FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, siz
 
 int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const uint16_t* const* v_caches,
                         const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd, float* out,
-                        float* scratch, size_t scratch_floats, hipStream_t s) {
+                        float* part_buf, size_t part_floats, hipStream_t s) {
   PRANA_CHECK(n_seq >= 1 && n_seq <= static_cast<size_t>(kFdMaxSeq), "flash decode: 1..16 sequences per call");
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "flash decode: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd == 64 || hd == 128, "flash decode: head_dim must be 64 or 128");
-  PRANA_CHECK(q && out && k_caches && v_caches && pos && scratch, "flash decode: null argument");
+  PRANA_CHECK(q && out && k_caches && v_caches && pos && part_buf, "flash decode: null argument");
   const FlashPlan plan = flash_decode_plan(pos, n_seq, n_heads, n_kv_heads, hd);
-  PRANA_CHECK(scratch_floats >= plan.scratch_floats, "flash decode: scratch below the plan's size");
+  PRANA_CHECK(part_floats >= plan.scratch_floats, "flash decode: partial-state buffer below the plan's size");
   FlashArgs a{};
   CombineArgs c{};
   a.q = q;
@@ -344,8 +372,8 @@ int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const u
   a.max_splits = plan.max_splits;
   a.rows_per_split = plan.rows_per_split;
   a.scale = 1.0f / sqrtf(static_cast<float>(hd));
-  a.part = scratch;
-  c.part = scratch;
+  a.part = part_buf;
+  c.part = part_buf;
   c.n_heads = a.n_heads;
   c.max_splits = a.max_splits;
   c.out = out;

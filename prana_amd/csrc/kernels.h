@@ -163,6 +163,12 @@ FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, siz
 // device [n_seq][n_heads*hd] f32.
 int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const uint16_t* const* v_caches,
                         const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd, float* out,
-                        float* scratch, size_t scratch_floats, hipStream_t s);
+                        float* part_buf, size_t part_floats, hipStream_t s);
+// The library's fixed partial-state array for the allocation-free entry point
+// (kFlashNoAllocFloats floats per GPU): setup looks its device address up
+// once per device (that device current); scratch() returns it (null before).
+constexpr size_t kFlashNoAllocFloats = size_t{1} << 23;  // 32 MiB
+int flash_noalloc_setup(int device);
+float* flash_noalloc_scratch(int device);
 
 }  // namespace prana

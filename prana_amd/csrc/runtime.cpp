@@ -42,7 +42,16 @@ int ensure_init() {
   if (e != hipSuccess || n == 0) return fail(kErrHip, "no HIP device visible (libprana_hip needs an MI355X / gfx950 GPU)");
   PRANA_HIP(hipSetDevice(0));
   PRANA_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+  if (int rc = flash_noalloc_setup(0)) return rc;
   c.device = 0;
+  return kOk;
+}
+
+int require_init() {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  const Context& c = ctx();
+  if (c.device < 0) return fail(kErrInvalid, "library not initialised: call prana_init first");
+  PRANA_HIP(hipSetDevice(c.device));
   return kOk;
 }
 

@@ -20,6 +20,9 @@ struct Context {
 };
 Context& ctx();
 int ensure_init();
+// Selects the library's device when prana_init has run; fails (creating
+// nothing) otherwise.
+int require_init();
 hipStream_t pick_stream(void* s);
 
 // RAII device buffer.
