@@ -9,8 +9,10 @@ roofline figure against the 8 TB/s HBM peak. The same number of steps is also
 timed without any events (reported beside). The
 HBM traffic per GEMV launch comes from the committed rocprofv3 counter
 summary (profiles/q4_0_gemv_7b_decode_traffic.json) when present. The
-reference's CPU path (the C restatement of its scalar tier, row-parallel on
-the host cores) is timed on a bounded sample of the same workload.
+reference's CPU path is timed on a bounded sample of the same workload: its
+scalar tier (the parity oracle, whose greedy stream the GPU must reproduce)
+and its timed tier (runtime-selected SIMD dots on its persistent pool, at its
+default min(nproc, 8) threads and at all host cores), both C restatements.
 
 Prints one JSON line. --gpus above 1 is not supported by this build.
 """
@@ -141,24 +143,42 @@ def main():
         os.environ["PRANA_ORACLE_THREADS"] = str(threads)
         t0 = time.time()
         om = O.Model(cfg, tensors)
-        log(f"oracle model built in {time.time() - t0:.1f}s; timing the CPU path on {threads} threads")
-        oc = om.cache(64)
-        tok, cpu_toks, t0 = int(prompt[0]), [], time.perf_counter()
-        while len(cpu_toks) < 2 or (time.perf_counter() - t0) < args.cpu_seconds:
-            tok = int(O.argmax(oc.forward(tok, len(cpu_toks))))
-            cpu_toks.append(tok)
-            if len(cpu_toks) >= 60:
-                break
-        cdt = time.perf_counter() - t0
+        log(f"oracle model built in {time.time() - t0:.1f}s")
+
+        def cpu_decode(n_max, seconds):
+            oc = om.cache(64)
+            tok, toks, t0 = int(prompt[0]), [], time.perf_counter()
+            while len(toks) < n_max and (len(toks) < 2 or time.perf_counter() - t0 < seconds):
+                tok = int(O.argmax(oc.forward(tok, len(toks))))
+                toks.append(tok)
+            return toks, time.perf_counter() - t0
+
+        # 1) the scalar tier (the parity oracle): the reference stream
+        O.set_tier(0)
+        cpu_toks, sdt = cpu_decode(60, args.cpu_seconds)
         n = len(cpu_toks)
-        cpu = {"value": round(n / cdt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{n} greedy decode steps of the same 7B-shape Q4_0 model at positions 0..{n - 1} "
-                         f"from prompt id {int(prompt[0])} (scalar-tier C restatement, rows split over {threads} "
-                         f"threads; {cdt:.1f}s of CPU work)",
+        log(f"scalar tier: {n} steps, {n / sdt:.3f} tok/s on {threads} threads")
+        # 2) the reference's timed tier (runtime-selected SIMD dots on its
+        #    persistent pool) at its default thread count, then at all cores,
+        #    over the same positions
+        t_def = O.set_tier(1, 0)
+        tier_toks, tdt = cpu_decode(n, 1e9)
+        t_all = O.set_tier(1, os.cpu_count() or 1)
+        _, adt = cpu_decode(n, 1e9)
+        simd = O.tier_name()
+        O.set_tier(0)
+        log(f"timed tier [{simd}]: {n / tdt:.3f} tok/s on {t_def} threads, {n / adt:.3f} on {t_all}")
+        cpu = {"value": round(n / tdt, 4), "unit": "tok/s", "cores": t_def, "kind": "port",
+               "sample": f"{n} greedy decode steps of the same 7B-shape Q4_0 model at positions 0..{n - 1} from "
+                         f"prompt id {int(prompt[0])}: the reference's timed tier (SIMD dots: {simd}; persistent "
+                         f"spin-then-park pool of min(nproc, 8) = {t_def} threads), {tdt:.1f}s of CPU work",
+               "all_cores": {"threads": t_all, "value": round(n / adt, 4)},
+               "scalar_tier": {"threads": threads, "value": round(n / sdt, 4),
+                               "note": "the oracle tier (pthreads per call), the parity reference"},
+               "timed_tier_tokens_match_scalar": f"{sum(a == b for a, b in zip(tier_toks, cpu_toks))}/{n}",
                "host": host_info()}
-        log(f"CPU baseline: {cpu['value']} tok/s")
         # The GPU decodes the very same steps (same prompt id, positions
-        # 0..n-1, fresh cache); the streams must be identical.
+        # 0..n-1, fresh cache); its stream must equal the scalar tier's.
         gcache = model.cache(n + 1)
         P.check(P.load().prana_synchronize())
         t0 = time.perf_counter()

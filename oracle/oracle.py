@@ -52,6 +52,8 @@ _SIGS = {
     "po_mat_row_block_isums": (c_size, [c_vp, c_vp, c_vp, c_size, c_vp]),
     "po_mat_row_f32": (None, [c_vp, c_size, c_vp]),
     "po_set_threads": (None, [c_int]),
+    "po_set_tier": (c_int, [c_int, c_int]),
+    "po_tier_name": (C.c_char_p, []),
     "po_rmsnorm": (None, [c_vp, c_vp, c_size, c_size, c_float, c_vp]),
     "po_silu": (None, [c_vp, c_size]),
     "po_gelu_tanh": (None, [c_vp, c_size]),
@@ -387,3 +389,13 @@ class Cache:
             lib().po_cache_free(self.h)
         except Exception:
             pass
+
+
+def set_tier(tier, threads=0):
+    """1: the reference's timed SIMD tier on its persistent pool (bench.py's
+    cpu_baseline); 0: the scalar tier, the parity oracle. Returns the pool size."""
+    return lib().po_set_tier(int(tier), int(threads))
+
+
+def tier_name():
+    return lib().po_tier_name().decode()

@@ -419,10 +419,33 @@ size_t po_mat_rows(const po_mat *m) { return m->rows; }
 size_t po_mat_cols(const po_mat *m) { return m->cols; }
 int po_mat_kind(const po_mat *m) { return m->kind; }
 
+/* The timed tier (cpu_tier.c): 0 = the scalar tier (the oracle), 1 = the
+ * reference's runtime-selected SIMD dots on its persistent pool. */
+static int g_tier = 0;
+float pt_row_dot(int kind, const float *x, const float *w, const int8_t *qa, const float *sa, const int32_t *suma,
+                 const int8_t *qw, const float *sw, const uint8_t *row, const float *ds, size_t k);
+const char *pt_simd_tier(void);
+int pt_pool_start(int threads);
+void pt_pool_run(size_t n_chunks, void (*fn)(void *, size_t), void *ctx);
+int pt_pool_threads(void);
+
+int po_set_tier(int tier, int threads) {
+  g_tier = tier ? 1 : 0;
+  return g_tier ? pt_pool_start(threads) : 0;
+}
+const char *po_tier_name(void) { return g_tier ? pt_simd_tier() : "scalar"; }
+
 /* Linear::row_dot (checkpoint.rs:129-135) -> the scalar dot of the format. */
 float po_mat_row_dot(const po_mat *m, const float *x, const int8_t *q, const float *sa,
                      const int32_t *sums, size_t r) {
   size_t k = m->cols;
+  if (g_tier) {
+    const int kind = m->kind == PO_F32 ? 0 : m->kind == PO_Q8 ? 1 : m->kind == PO_Q4_0 ? 2 : m->kind == PO_Q4_K ? 3 : 4;
+    return pt_row_dot(kind, x, m->w ? m->w + r * k : NULL, q, sa, sums, m->q ? m->q + r * k : NULL,
+                      m->kind == PO_Q8 ? m->scales + r * (k / 32) : NULL,
+                      m->blocks ? m->blocks + r * m->row_bytes : NULL,
+                      m->kind >= PO_Q4_0 ? m->scales + r * m->scales_per_row : NULL, k);
+  }
   switch (m->kind) {
     case PO_F32: return po_dot_f32(x, m->w + r * k, k);
     case PO_Q8: return po_dot_q8_q8(q, sa, m->q + r * k, m->scales + r * (k / 32), k / 32);
@@ -524,7 +547,37 @@ static void *job_run(void *p) {
   return NULL;
 }
 
+/* run_rows / run_rows_multi chunking (matmul.rs:192-232, 318-350) on the
+ * timed tier's pool. */
+typedef struct { job_t base; size_t chunk; } tier_rows;
+static void tier_chunk(void *ctx, size_t c) {
+  tier_rows *t = ctx;
+  job_t j = t->base;
+  j.r0 = c * t->chunk;
+  j.r1 = j.r0 + t->chunk > j.m->rows ? j.m->rows : j.r0 + t->chunk;
+  job_run(&j);
+}
+static void tier_run_rows(job_t base) {
+  const size_t R = base.m->rows, T = (size_t)pt_pool_threads();
+  const size_t macs = R * base.m->cols * base.n;
+  const int multi = base.n > 1;
+  if (macs < (multi ? (1u << 20) : 256u * 1024u) || T <= 1) {
+    base.r0 = 0;
+    base.r1 = R;
+    job_run(&base);
+    return;
+  }
+  size_t chunk = (R + 4 * T - 1) / (4 * T);
+  if (chunk < (multi ? 4u : 16u)) chunk = multi ? 4 : 16;
+  tier_rows t = {base, chunk};
+  pt_pool_run((R + chunk - 1) / chunk, tier_chunk, &t);
+}
+
 static void run_rows(job_t base) {
+  if (g_tier) {
+    tier_run_rows(base);
+    return;
+  }
   size_t R = base.m->rows;
   int nt = g_threads;
   if (nt <= 1 || R * base.m->cols * base.n < (1u << 16)) {

@@ -34,6 +34,13 @@ void po_f32_to_f16_n(const float *x, size_t n, uint16_t *out);
  * f32::exp is glibc expf), threaded; for exhaustive device comparisons. */
 void po_expf_bits(uint32_t base, size_t n, float *out, int threads);
 
+/* ---------------- timed tier (cpu_tier.c; bench.py's cpu_baseline only) ---------------- */
+/* tier 1: the reference's runtime-selected SIMD dots (simd_x86.rs) on its
+ * persistent pool (pool.rs) with threads workers (<= 0: min(nproc, 8));
+ * tier 0: the scalar tier, the parity oracle (default). Returns the pool size. */
+int po_set_tier(int tier, int threads);
+const char *po_tier_name(void);
+
 /* ---------------- activations (matmul.rs:105-127) ---------------- */
 /* a[k] -> q[k] (i8), scales[k/32] (f32), sums[k/32] (i32). k % 32 == 0. */
 void po_quantize_acts(const float *a, size_t k, int8_t *q, float *scales, int32_t *sums);
