@@ -36,6 +36,9 @@ extern "C" {
 #define PRANA_ERR_HIP (-2)
 #define PRANA_ERR_NOMEM (-3)
 #define PRANA_ERR_UNSUPPORTED (-4)
+/* A caller-sized output buffer was too small; the out-length argument holds
+ * the size needed (prana-cactus lib.rs:337-354 grow-and-retry idiom). */
+#define PRANA_ERR_SHORT_BUFFER (-5)
 
 typedef void *prana_stream_t; /* hipStream_t */
 
@@ -177,6 +180,9 @@ int prana_f32_to_f16(const float *in, size_t n, uint16_t *out, prana_stream_t st
 int prana_f16_to_f32(const uint16_t *in, size_t n, float *out, prana_stream_t stream);
 /* The device expf behind silu/softmax (f32::exp, norms.rs:29,49). */
 int prana_expf(const float *in, size_t n, float *out, prana_stream_t stream);
+/* The device tanhf behind gelu_tanh (f32::tanh, norms.rs:35-41): glibc's
+ * fdlibm tanhf / expm1f, bit for bit. */
+int prana_tanhf(const float *in, size_t n, float *out, prana_stream_t stream);
 
 /* ---------------------------------------------------------------- model */
 /* Config (checkpoint.rs:32-56). rope_neox: 0 interleaved / 1 NeoX;
@@ -251,6 +257,74 @@ int prana_generate_speculative(prana_model_t target, prana_model_t draft, const 
 
 /* Bytes of a ggml tensor of the given type and element count. */
 size_t prana_ggml_nbytes(int ggml_type, size_t n_elems);
+
+/* ---------------------------------------------------------------- GGUF
+ * The reference's container reader and model loader (prana-model gguf.rs).
+ * These entry points run on the host and make no device call, except
+ * prana_model_load_gguf, which uploads the model. Strings and arrays come
+ * back through caller-sized buffers: the out-length is always set, and a
+ * buffer that is too small gives PRANA_ERR_SHORT_BUFFER (grow and retry). */
+typedef struct prana_gguf *prana_gguf_t;
+
+/* Gguf::read (gguf.rs:157-160): the file is memory-mapped read-only, not
+ * copied. GGUF v2/v3; bad magic, other versions, truncation and unknown
+ * value types fail with the reference's messages (gguf.rs:97-130,162-172). */
+int prana_gguf_open(const char *path, prana_gguf_t *out);
+/* Gguf::from_bytes (gguf.rs:162-196) over a copy of the caller's bytes. */
+int prana_gguf_open_bytes(const void *data, size_t nbytes, prana_gguf_t *out);
+int prana_gguf_close(prana_gguf_t g);
+/* Header fields: format version, tensor count (distinct names, file order),
+ * metadata entry count. */
+int prana_gguf_counts(prana_gguf_t g, uint32_t *version, size_t *n_tensors, size_t *n_meta);
+/* Name of the index-th tensor of the directory (file order). */
+int prana_gguf_tensor_name(prana_gguf_t g, size_t index, char *buf, size_t cap, size_t *len);
+/* TensorInfo (gguf.rs:133-138): ggml type, dims in ggml order (dims[0] =
+ * contiguous; dims holds up to 8), and the byte size of its data, checked
+ * against the data section (Gguf::raw, gguf.rs:202-205). */
+int prana_gguf_tensor_info(prana_gguf_t g, const char *name, int *ggml_type, uint64_t *dims, int *n_dims,
+                           size_t *nbytes);
+/* The tensor's bytes in place (valid until prana_gguf_close). */
+int prana_gguf_tensor_data(prana_gguf_t g, const char *name, const void **bytes, size_t *nbytes);
+/* Gguf::tensor_f32 (gguf.rs:208-264): F32, F16, Q4_0, Q8_0, Q4_K, Q6_K
+ * decoded to f32 on the host (kquant.rs:39-112 block decoders). cap counts
+ * floats; *n = the tensor's element count. */
+int prana_gguf_tensor_f32(prana_gguf_t g, const char *name, float *out, size_t cap, size_t *n);
+/* Value type (0..12, gguf.rs:102-130) of a metadata entry; elem_type is the
+ * element type of an array (type 9), else -1. */
+int prana_gguf_meta_type(prana_gguf_t g, const char *key, int *type, int *elem_type);
+/* Value::as_usize (gguf.rs:63-75): unsigned, or signed >= 0, integers. */
+int prana_gguf_meta_u64(prana_gguf_t g, const char *key, uint64_t *out);
+/* Value::as_f32 (gguf.rs:77-83): f32, or f64 narrowed. */
+int prana_gguf_meta_f32(prana_gguf_t g, const char *key, float *out);
+/* A string value's bytes, NUL terminated (GGUF strings may hold NULs: use *len). */
+int prana_gguf_meta_str(prana_gguf_t g, const char *key, char *buf, size_t cap, size_t *len);
+int prana_gguf_meta_array_len(prana_gguf_t g, const char *key, size_t *n);
+/* Element index of a string array (tokenizer.ggml.tokens / merges). */
+int prana_gguf_meta_array_str(prana_gguf_t g, const char *key, size_t index, char *buf, size_t cap, size_t *len);
+/* A float array (tokenizer.ggml.scores) as f32; cap counts elements. */
+int prana_gguf_meta_array_f32(prana_gguf_t g, const char *key, float *out, size_t cap, size_t *n);
+/* An integer or bool array (tokenizer.ggml.token_type) as int64. */
+int prana_gguf_meta_array_i64(prana_gguf_t g, const char *key, int64_t *out, size_t cap, size_t *n);
+/* The Config load derives (gguf.rs:340-378,410-425): llama / qwen2 / gemma
+ * keys with the reference's defaults (head_count_kv = head_count, freq_base
+ * 1e4, key_length = dim / heads, rms epsilon 1e-5), vocab = the length of
+ * tokenizer.ggml.tokens, rope_neox for qwen2 and gemma, gemma's gelu_tanh and
+ * sqrt(dim) embedding scale. */
+int prana_gguf_model_config(prana_gguf_t g, prana_config *cfg);
+/* load (gguf.rs:338-437) without the tokenizer: every tensor by name onto a
+ * new finalized device model. precision 0 = Precision::F32, 1 =
+ * Precision::Q8 (checkpoint.rs:85-91). Q8_0 / Q4_0 rows with cols % 32 == 0
+ * and Q4_K / Q6_K rows with cols % 256 == 0 stay packed (gguf.rs:271-305);
+ * other matrices are decoded to f32 and, at Q8 with cols % 32 == 0,
+ * quantized by quantize_q8 (matmul.rs:61-84), else kept dense. The
+ * embedding stays packed for Q4_0 / Q4_K / Q6_K (gguf.rs:309-326). Gemma
+ * norm weights get the +1 fold (gguf.rs:383-396). Without output.weight the
+ * head reads the table; a dense table at Q8 gets a quantized copy
+ * (gguf.rs:426-437). Backend limits: dim and hidden_dim multiples of 32,
+ * head_dim even and <= 256. */
+int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t *out);
+/* The configuration a model was created or loaded with. */
+int prana_model_config(prana_model_t m, prana_config *cfg);
 
 #ifdef __cplusplus
 }

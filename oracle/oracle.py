@@ -34,6 +34,7 @@ _SIGS = {
     "po_f16_to_f32": (c_float, [C.c_uint16]),
     "po_f32_to_f16": (C.c_uint16, [c_float]),
     "po_expf_bits": (None, [C.c_uint32, c_size, c_vp, c_int]),
+    "po_tanhf_bits": (None, [C.c_uint32, c_size, c_vp, c_int]),
     "po_f16_to_f32_n": (None, [c_vp, c_size, c_vp]),
     "po_f32_to_f16_n": (None, [c_vp, c_size, c_vp]),
     "po_quantize_acts": (None, [c_vp, c_size, c_vp, c_vp, c_vp]),
@@ -139,6 +140,12 @@ def f32_to_f16_n(x):
 def expf_bits(base, n, threads=16):
     out = np.empty(n, np.float32)
     lib().po_expf_bits(base, n, P(out), threads)
+    return out
+
+
+def tanhf_bits(base, n, threads=16):
+    out = np.empty(n, np.float32)
+    lib().po_tanhf_bits(base, n, P(out), threads)
     return out
 
 
@@ -302,10 +309,20 @@ class Model:
     """The oracle model, built from the same {name: (ggml_type, dims, bytes)} as the GPU model."""
 
     def __init__(self, config, tensors):
+        """tensors: {name: (ggml_type, dims, bytes)}; a matrix may also be a
+        ready Mat (e.g. Mat.q8_parts of quantize_q8, Precision::Q8)."""
         self.config = config
         self.cfg = PoConfig(**config)
         self.h = lib().po_model_new(C.byref(self.cfg))
-        for name, (ty, dims, raw) in tensors.items():
+        for name, v in tensors.items():
+            if isinstance(v, Mat):
+                if name == "output.weight":
+                    lib().po_model_set_wcls(self.h, v.release())
+                else:
+                    _, li, rest = name.split(".", 2)
+                    lib().po_model_set_linear(self.h, int(li), SLOTS[rest[: -len(".weight")]], v.release())
+                continue
+            ty, dims, raw = v
             raw = np.ascontiguousarray(raw)
             if name == "token_embd.weight":
                 if lib().po_model_set_embedding(self.h, ty, P(raw), raw.nbytes) != 0:

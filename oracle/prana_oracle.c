@@ -71,28 +71,34 @@ void po_f32_to_f16_n(const float *x, size_t n, uint16_t *out) {
   for (size_t i = 0; i < n; i++) out[i] = po_f32_to_f16(x[i]);
 }
 
-typedef struct { uint32_t base; size_t i0, i1; float *out; } expf_job;
-static void *expf_run(void *p) {
-  expf_job *j = p;
-  for (size_t i = j->i0; i < j->i1; i++) j->out[i] = expf(f_bits(j->base + (uint32_t)i));
+/* The platform libm over a contiguous range of f32 bit patterns: the values
+ * Rust's f32::exp / f32::tanh return on the reference's host (glibc). */
+typedef struct { uint32_t base; size_t i0, i1; float *out; float (*fn)(float); } bits_job;
+static void *bits_run(void *p) {
+  bits_job *j = p;
+  for (size_t i = j->i0; i < j->i1; i++) j->out[i] = j->fn(f_bits(j->base + (uint32_t)i));
   return NULL;
 }
-void po_expf_bits(uint32_t base, size_t n, float *out, int threads) {
+static void libm_bits(float (*fn)(float), uint32_t base, size_t n, float *out, int threads) {
   if (threads < 1) threads = 1;
   if (threads > 64) threads = 64;
   pthread_t th[64];
-  expf_job jobs[64];
+  bits_job jobs[64];
   size_t chunk = (n + threads - 1) / threads;
   int k = 0;
   for (int t = 0; t < threads; t++) {
     size_t i0 = t * chunk, i1 = i0 + chunk > n ? n : i0 + chunk;
     if (i0 >= i1) break;
-    jobs[t] = (expf_job){base, i0, i1, out};
-    pthread_create(&th[t], NULL, expf_run, &jobs[t]);
+    jobs[t] = (bits_job){base, i0, i1, out, fn};
+    pthread_create(&th[t], NULL, bits_run, &jobs[t]);
     k++;
   }
   for (int t = 0; t < k; t++) pthread_join(th[t], NULL);
 }
+static float libm_expf(float x) { return expf(x); }
+static float libm_tanhf(float x) { return tanhf(x); }
+void po_expf_bits(uint32_t base, size_t n, float *out, int threads) { libm_bits(libm_expf, base, n, out, threads); }
+void po_tanhf_bits(uint32_t base, size_t n, float *out, int threads) { libm_bits(libm_tanhf, base, n, out, threads); }
 
 /* Rust `v.round().clamp(-127.0, 127.0) as i32` (matmul.rs:123): NaN -> 0. */
 static int32_t round_clamp127(float v) {

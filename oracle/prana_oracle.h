@@ -33,6 +33,8 @@ void po_f32_to_f16_n(const float *x, size_t n, uint16_t *out);
 /* Bulk host-libm expf over [base, base+n) f32 bit patterns (the reference's
  * f32::exp is glibc expf), threaded; for exhaustive device comparisons. */
 void po_expf_bits(uint32_t base, size_t n, float *out, int threads);
+/* tanhf (norms.rs:40, f32::tanh -> glibc) over the same kind of range. */
+void po_tanhf_bits(uint32_t base, size_t n, float *out, int threads);
 
 /* ---------------- timed tier (cpu_tier.c; bench.py's cpu_baseline only) ---------------- */
 /* tier 1: the reference's runtime-selected SIMD dots (simd_x86.rs) on its

@@ -231,6 +231,13 @@ def expf(x):
     return o.to_host()
 
 
+def tanhf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    d, o = DeviceArray.from_host(x), DeviceArray(x.shape, np.float32)
+    check(load().prana_tanhf(d.ptr, x.size, o.ptr, None))
+    return o.to_host()
+
+
 def rope(x, pos0, head_dim, theta, neox):
     """rope_interleaved / rope_neox on each row of x at positions pos0 + i."""
     x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
@@ -377,6 +384,143 @@ class Model:
                 self.h = None
         except Exception:
             pass
+
+
+def _config_dict(cfg):
+    return {name: getattr(cfg, name) for name, _ in PranaConfig._fields_}
+
+
+class Gguf:
+    """A parsed GGUF file (gguf.rs:140-264): metadata and tensor directory,
+    read on the host by the library (the file is memory-mapped, not copied)."""
+
+    def __init__(self, path=None, data=None):
+        h = C.c_void_p()
+        if (path is None) == (data is None):
+            raise ValueError("give exactly one of path= or data=")
+        if path is not None:
+            check(load().prana_gguf_open(str(path).encode(), C.byref(h)))
+        else:
+            buf = np.frombuffer(bytes(data), np.uint8)
+            check(load().prana_gguf_open_bytes(_ptr(buf) if buf.size else None, buf.size, C.byref(h)))
+        self.h = h
+
+    def counts(self):
+        v, nt, nm = C.c_uint32(), C.c_size_t(), C.c_size_t()
+        check(load().prana_gguf_counts(self.h, C.byref(v), C.byref(nt), C.byref(nm)))
+        return v.value, nt.value, nm.value
+
+    @staticmethod
+    def _grow(call):
+        """Caller-sized buffer, grown once to the size the library asks for."""
+        n = C.c_size_t()
+        rc = call(None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        buf = C.create_string_buffer(n.value + 1)
+        check(call(buf, n.value + 1, C.byref(n)))
+        return buf.raw[: n.value]
+
+    def tensor_names(self):
+        _, nt, _ = self.counts()
+        return [self._grow(lambda b, c, n, i=i: load().prana_gguf_tensor_name(self.h, i, b, c, n)).decode()
+                for i in range(nt)]
+
+    def tensor_info(self, name):
+        ty, nd, nb = C.c_int(), C.c_int(), C.c_size_t()
+        dims = (C.c_uint64 * 8)()
+        check(load().prana_gguf_tensor_info(self.h, name.encode(), C.byref(ty), dims, C.byref(nd), C.byref(nb)))
+        return ty.value, [dims[i] for i in range(nd.value)], nb.value
+
+    def tensor_bytes(self, name):
+        p, nb = C.c_void_p(), C.c_size_t()
+        check(load().prana_gguf_tensor_data(self.h, name.encode(), C.byref(p), C.byref(nb)))
+        return C.string_at(p, nb.value) if nb.value else b""
+
+    def tensor_f32(self, name):
+        """Gguf::tensor_f32: any supported type decoded to f32."""
+        n = C.c_size_t()
+        rc = load().prana_gguf_tensor_f32(self.h, name.encode(), None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        out = np.empty(n.value, np.float32)
+        check(load().prana_gguf_tensor_f32(self.h, name.encode(), _ptr(out), out.size, C.byref(n)))
+        return out
+
+    def meta_type(self, key):
+        t, e = C.c_int(), C.c_int()
+        check(load().prana_gguf_meta_type(self.h, key.encode(), C.byref(t), C.byref(e)))
+        return t.value, e.value
+
+    def meta_usize(self, key):
+        v = C.c_uint64()
+        check(load().prana_gguf_meta_u64(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_f32(self, key):
+        v = C.c_float()
+        check(load().prana_gguf_meta_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_str(self, key):
+        return self._grow(lambda b, c, n: load().prana_gguf_meta_str(self.h, key.encode(), b, c, n))
+
+    def meta_array_len(self, key):
+        n = C.c_size_t()
+        check(load().prana_gguf_meta_array_len(self.h, key.encode(), C.byref(n)))
+        return n.value
+
+    def meta_array_str(self, key):
+        return [self._grow(lambda b, c, n, i=i: load().prana_gguf_meta_array_str(self.h, key.encode(), i, b, c, n))
+                for i in range(self.meta_array_len(key))]
+
+    def _array(self, fn, key, dtype):
+        n = C.c_size_t()
+        rc = fn(self.h, key.encode(), None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        out = np.empty(n.value, dtype)
+        check(fn(self.h, key.encode(), _ptr(out), out.size, C.byref(n)))
+        return out
+
+    def meta_array_f32(self, key):
+        return self._array(load().prana_gguf_meta_array_f32, key, np.float32)
+
+    def meta_array_i64(self, key):
+        return self._array(load().prana_gguf_meta_array_i64, key, np.int64)
+
+    def model_config(self):
+        """The Config load (gguf.rs:340-425) would build from this file."""
+        cfg = PranaConfig()
+        check(load().prana_gguf_model_config(self.h, C.byref(cfg)))
+        return _config_dict(cfg)
+
+    def close(self):
+        if getattr(self, "h", None) is not None:
+            load().prana_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_gguf(source, precision="f32"):
+    """gguf::load (gguf.rs:338-437) without the tokenizer: a finalized device
+    Model from a GGUF path, raw bytes or an open Gguf. precision "f32" or "q8"."""
+    prec = {"f32": 0, "q8": 1}[precision]
+    g = source if isinstance(source, Gguf) else (Gguf(data=source) if isinstance(source, (bytes, bytearray))
+                                                  else Gguf(path=source))
+    init()
+    h = C.c_void_p()
+    check(load().prana_model_load_gguf(g.h, prec, C.byref(h)))
+    cfg = PranaConfig()
+    check(load().prana_model_config(h, C.byref(cfg)))
+    m = Model.__new__(Model)
+    m.h, m.cfg, m.config = h, cfg, _config_dict(cfg)
+    return m
 
 
 def gemv_profile(on, period=1):

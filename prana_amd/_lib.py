@@ -38,7 +38,14 @@ class GenStats(C.Structure):
 
 
 class PranaError(RuntimeError):
-    pass
+    """A failed call: .code is the library's status (PRANA_ERR_*)."""
+
+    def __init__(self, msg, code=None):
+        super().__init__(msg)
+        self.code = code
+
+
+ERR_SHORT_BUFFER = -5
 
 
 # name -> (restype, argtypes)
@@ -84,6 +91,7 @@ _SIGS = {
     "prana_f32_to_f16": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
     "prana_f16_to_f32": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
     "prana_expf": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
+    "prana_tanhf": (c_int, [c_void_p, c_size, c_void_p, c_void_p]),
     "prana_model_create": (c_int, [C.POINTER(PranaConfig), C.POINTER(c_void_p)]),
     "prana_model_destroy": (c_int, [c_void_p]),
     "prana_model_set_tensor": (c_int, [c_void_p, C.c_char_p, c_int, c_u64p, c_int, c_void_p, c_size]),
@@ -103,6 +111,27 @@ _SIGS = {
     "prana_generate_speculative": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_void_p, c_size,
                                            c_void_p, C.POINTER(c_size), C.POINTER(GenStats)]),
     "prana_ggml_nbytes": (c_size, [c_int, c_size]),
+    # GGUF (host only, except prana_model_load_gguf)
+    "prana_gguf_open": (c_int, [C.c_char_p, C.POINTER(c_void_p)]),
+    "prana_gguf_open_bytes": (c_int, [c_void_p, c_size, C.POINTER(c_void_p)]),
+    "prana_gguf_close": (c_int, [c_void_p]),
+    "prana_gguf_counts": (c_int, [c_void_p, C.POINTER(C.c_uint32), C.POINTER(c_size), C.POINTER(c_size)]),
+    "prana_gguf_tensor_name": (c_int, [c_void_p, c_size, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_tensor_info": (c_int, [c_void_p, C.c_char_p, C.POINTER(c_int), c_u64p, C.POINTER(c_int),
+                                       C.POINTER(c_size)]),
+    "prana_gguf_tensor_data": (c_int, [c_void_p, C.c_char_p, C.POINTER(c_void_p), C.POINTER(c_size)]),
+    "prana_gguf_tensor_f32": (c_int, [c_void_p, C.c_char_p, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_meta_type": (c_int, [c_void_p, C.c_char_p, C.POINTER(c_int), C.POINTER(c_int)]),
+    "prana_gguf_meta_u64": (c_int, [c_void_p, C.c_char_p, c_u64p]),
+    "prana_gguf_meta_f32": (c_int, [c_void_p, C.c_char_p, C.POINTER(c_float)]),
+    "prana_gguf_meta_str": (c_int, [c_void_p, C.c_char_p, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_meta_array_len": (c_int, [c_void_p, C.c_char_p, C.POINTER(c_size)]),
+    "prana_gguf_meta_array_str": (c_int, [c_void_p, C.c_char_p, c_size, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_meta_array_f32": (c_int, [c_void_p, C.c_char_p, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_meta_array_i64": (c_int, [c_void_p, C.c_char_p, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_gguf_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
+    "prana_model_load_gguf": (c_int, [c_void_p, c_int, C.POINTER(c_void_p)]),
+    "prana_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
 }
 
 # libprana_synth.so (prana_amd/synth/prana_synth.h): fixture encoders of the
@@ -166,5 +195,5 @@ def check_synth(rc):
 def check(rc):
     if rc != 0:
         msg = load().prana_last_error().decode(errors="replace")
-        raise PranaError(f"prana error {rc}: {msg}")
+        raise PranaError(f"prana error {rc}: {msg}", rc)
     return rc

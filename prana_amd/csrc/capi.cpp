@@ -9,6 +9,7 @@
 #include <new>
 #include <string>
 
+#include "gguf.h"
 #include "model.h"
 
 namespace prana {
@@ -41,6 +42,19 @@ int guard(F&& f) {
   } catch (...) {
     return fail(kErrInvalid, "internal error");
   }
+}
+
+// Caller-sized string output: *len = bytes needed (no NUL); the copy, NUL
+// terminated, happens when buf holds len + 1 bytes, else PRANA_ERR_SHORT_BUFFER
+// and the caller grows buf and calls again.
+int copy_out(const std::string& s, char* buf, size_t cap, size_t* len) {
+  *len = s.size();
+  if (!buf || cap < s.size() + 1)
+    return fail(kErrShortBuffer, "buffer of " + std::to_string(cap) + " bytes; " + std::to_string(s.size() + 1) +
+                                     " needed");
+  std::memcpy(buf, s.data(), s.size());
+  buf[s.size()] = '\0';
+  return kOk;
 }
 
 #define INIT_OR_RETURN()          \
@@ -456,18 +470,20 @@ int prana_expf(const float* in, size_t n, float* out, prana_stream_t stream) {
   });
 }
 
+int prana_tanhf(const float* in, size_t n, float* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    return launch_tanhf(in, n, out, pick_stream(stream));
+  });
+}
+
 // ------------------------------------------------------------------ model
 int prana_model_create(const prana_config* cfg, prana_model_t* out) {
   return guard([&] {
     INIT_OR_RETURN();
     PRANA_CHECK(cfg && out, "null argument");
     const prana_config& c = *cfg;
-    PRANA_CHECK(c.dim > 0 && c.n_layers > 0 && c.n_heads > 0 && c.vocab_size > 0 && c.seq_len > 0,
-                "config: zero-sized dimension");
-    PRANA_CHECK(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "config: n_heads % n_kv_heads != 0");
-    PRANA_CHECK(c.head_dim % 2 == 0 && c.head_dim <= 256, "config: head_dim must be even and <= 256");
-    PRANA_CHECK(c.dim % 32 == 0 && c.hidden_dim % 32 == 0 && (c.n_heads * c.head_dim) % 32 == 0,
-                "config: dim, hidden_dim and n_heads*head_dim must be multiples of 32");
+    if (int rc = check_config(c)) return rc;
     auto* m = new prana_model();
     m->m.c = c;
     m->m.layers.resize(c.n_layers);
@@ -630,5 +646,217 @@ int prana_generate_speculative(prana_model_t target, prana_model_t draft, const 
 }
 
 size_t prana_ggml_nbytes(int ggml_type, size_t n_elems) { return ggml_nbytes(ggml_type, n_elems); }
+
+// ------------------------------------------------------------------ GGUF (host only; no device work)
+int prana_gguf_open(const char* path, prana_gguf_t* out) {
+  return guard([&] {
+    PRANA_CHECK(path && out, "null argument");
+    *out = nullptr;
+    auto h = std::make_unique<prana_gguf>();
+    if (int rc = gguf_open_file(path, h->g)) return rc;
+    *out = h.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_open_bytes(const void* data, size_t nbytes, prana_gguf_t* out) {
+  return guard([&] {
+    PRANA_CHECK((data || nbytes == 0) && out, "null argument");
+    *out = nullptr;
+    auto h = std::make_unique<prana_gguf>();
+    if (int rc = gguf_open_bytes(data, nbytes, h->g)) return rc;
+    *out = h.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_close(prana_gguf_t g) {
+  return guard([&] {
+    delete g;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_counts(prana_gguf_t g, uint32_t* version, size_t* n_tensors, size_t* n_meta) {
+  return guard([&] {
+    PRANA_CHECK(g, "null handle");
+    if (version) *version = g->g->version;
+    if (n_tensors) *n_tensors = g->g->names.size();
+    if (n_meta) *n_meta = g->g->meta.size();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_tensor_name(prana_gguf_t g, size_t index, char* buf, size_t cap, size_t* len) {
+  return guard([&] {
+    PRANA_CHECK(g && len, "null argument");
+    PRANA_CHECK(index < g->g->names.size(), "tensor index out of range");
+    return copy_out(g->g->names[index], buf, cap, len);
+  });
+}
+
+int prana_gguf_tensor_info(prana_gguf_t g, const char* name, int* ggml_type, uint64_t* dims, int* n_dims,
+                           size_t* nbytes) {
+  return guard([&] {
+    PRANA_CHECK(g && name, "null argument");
+    const GTensor* t;
+    const uint8_t* b;
+    size_t nb;
+    if (int rc = g->g->raw(name, &t, &b, &nb)) return rc;
+    if (ggml_type) *ggml_type = static_cast<int>(t->type);
+    if (n_dims) *n_dims = static_cast<int>(t->dims.size());
+    if (dims)
+      for (size_t i = 0; i < t->dims.size(); i++) dims[i] = t->dims[i];
+    if (nbytes) *nbytes = nb;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_tensor_data(prana_gguf_t g, const char* name, const void** bytes, size_t* nbytes) {
+  return guard([&] {
+    PRANA_CHECK(g && name && bytes && nbytes, "null argument");
+    const GTensor* t;
+    const uint8_t* b;
+    if (int rc = g->g->raw(name, &t, &b, nbytes)) return rc;
+    *bytes = b;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_tensor_f32(prana_gguf_t g, const char* name, float* out, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && name && n, "null argument");
+    std::vector<float> v;
+    if (int rc = g->g->tensor_f32(name, v)) return rc;
+    *n = v.size();
+    if (!out || cap < v.size())
+      return fail(kErrShortBuffer, "buffer holds " + std::to_string(cap) + " values, tensor has " +
+                                       std::to_string(v.size()));
+    if (!v.empty()) std::memcpy(out, v.data(), v.size() * 4);
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_type(prana_gguf_t g, const char* key, int* type, int* elem_type) {
+  return guard([&] {
+    PRANA_CHECK(g && key && type, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v) return fail(kErrInvalid, std::string("missing metadata '") + key + "'");
+    *type = static_cast<int>(v->type);
+    if (elem_type) *elem_type = v->type == 9 ? static_cast<int>(v->elem_type) : -1;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_u64(prana_gguf_t g, const char* key, uint64_t* out) {
+  return guard([&] {
+    PRANA_CHECK(g && key && out, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || !gvalue_as_u64(*v, out)) return fail(kErrInvalid, std::string("missing metadata '") + key + "'");
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_f32(prana_gguf_t g, const char* key, float* out) {
+  return guard([&] {
+    PRANA_CHECK(g && key && out, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || !gvalue_as_f32(*v, out)) return fail(kErrInvalid, std::string("missing metadata '") + key + "'");
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_str(prana_gguf_t g, const char* key, char* buf, size_t cap, size_t* len) {
+  return guard([&] {
+    PRANA_CHECK(g && key && len, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || v->type != 8) return fail(kErrInvalid, std::string("missing metadata '") + key + "'");
+    return copy_out(v->s, buf, cap, len);
+  });
+}
+
+int prana_gguf_meta_array_len(prana_gguf_t g, const char* key, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && key && n, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || v->type != 9) return fail(kErrInvalid, std::string("missing metadata '") + key + "'");
+    *n = v->arr.size();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_array_str(prana_gguf_t g, const char* key, size_t index, char* buf, size_t cap, size_t* len) {
+  return guard([&] {
+    PRANA_CHECK(g && key && len, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || v->type != 9 || v->elem_type != 8)
+      return fail(kErrInvalid, std::string("missing string array '") + key + "'");
+    PRANA_CHECK(index < v->arr.size(), "array index out of range");
+    return copy_out(v->arr[index].s, buf, cap, len);
+  });
+}
+
+int prana_gguf_meta_array_f32(prana_gguf_t g, const char* key, float* out, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && key && n, "null argument");
+    const GValue* v = g->g->find(key);
+    if (!v || v->type != 9 || (v->elem_type != 6 && v->elem_type != 12))
+      return fail(kErrInvalid, std::string("missing float array '") + key + "'");
+    *n = v->arr.size();
+    if (!out || cap < v->arr.size()) return fail(kErrShortBuffer, "buffer shorter than the array");
+    for (size_t i = 0; i < v->arr.size(); i++) gvalue_as_f32(v->arr[i], &out[i]);
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_meta_array_i64(prana_gguf_t g, const char* key, int64_t* out, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && key && n, "null argument");
+    const GValue* v = g->g->find(key);
+    const uint32_t et = v ? v->elem_type : 0;
+    const bool ints = et <= 5 || et == 7 || et == 10 || et == 11;
+    if (!v || v->type != 9 || et == 6 || !ints)
+      return fail(kErrInvalid, std::string("missing integer array '") + key + "'");
+    *n = v->arr.size();
+    if (!out || cap < v->arr.size()) return fail(kErrShortBuffer, "buffer shorter than the array");
+    for (size_t i = 0; i < v->arr.size(); i++) {
+      const GValue& e = v->arr[i];
+      out[i] = (et == 1 || et == 3 || et == 5 || et == 11) ? e.i : static_cast<int64_t>(e.u);
+    }
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gguf_model_config(prana_gguf_t g, prana_config* cfg) {
+  return guard([&] {
+    PRANA_CHECK(g && cfg, "null argument");
+    return gguf_model_config(*g->g, cfg);
+  });
+}
+
+int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && out, "null argument");
+    *out = nullptr;
+    prana_config c{};
+    if (int rc = gguf_model_config(*g->g, &c)) return rc;
+    if (int rc = check_config(c)) return rc;
+    auto m = std::make_unique<prana_model>();
+    m->m.c = c;
+    m->m.layers.resize(c.n_layers);
+    if (int rc = gguf_load_model(*g->g, precision, m->m)) return rc;
+    *out = m.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_model_config(prana_model_t m, prana_config* cfg) {
+  return guard([&] {
+    PRANA_CHECK(m && cfg, "null argument");
+    *cfg = m->m.c;
+    return static_cast<int>(kOk);
+  });
+}
 
 }  // extern "C"

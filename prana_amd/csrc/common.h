@@ -23,6 +23,7 @@ enum Status : int {
   kErrHip = -2,
   kErrNoMem = -3,
   kErrUnsupported = -4,
+  kErrShortBuffer = -5,
 };
 
 void set_error(const std::string& msg);
@@ -137,6 +138,113 @@ __device__ __forceinline__ float dev_expf(float x) {
   y = __fma_rn(z, r2, y);
   y = y * s;
   return static_cast<float>(y);
+}
+
+// ---------------------------------------------------------------- tanhf
+// gelu_tanh (norms.rs:35-41) reaches tanhf through Rust's f32::tanh ->
+// glibc tanhf, which (through glibc 2.40) is the fdlibm single-precision
+// tanhf over fdlibm's expm1f: tanh|x| = 1 - 2/(expm1(2|x|) + 2) for |x| >= 1,
+// -t/(t + 2) with t = expm1(-2|x|) below, x(1 + x) under 2^-55, 1 past 22.
+// expm1f reduces x = k ln2 + r (ln2 split hi/lo, correction c) and evaluates
+// fdlibm's rational form with a degree-5 polynomial R1 in x^2/2. The
+// constants are fdlibm's (Sun Microsystems, freely distributable), needed
+// unchanged for bit-identical results. This restatement equals glibc 2.35's
+// tanhf on all 2^32 inputs (exhaustive check in the GPU test suite).
+// Upstream: fdlibm s_tanh.c / s_expm1.c, float versions in glibc
+// sysdeps/ieee754/flt-32/s_tanhf.c and s_expm1f.c.
+__device__ __forceinline__ float dev_expm1f(float x) {
+  const float kHuge = 1.0e+30f, kTiny = 1.0e-30f;
+  const float kOThreshold = 8.8721679688e+01f, kLn2Hi = 6.9313812256e-01f, kLn2Lo = 9.0580006145e-06f;
+  const float kInvLn2 = 1.4426950216e+00f;
+  const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
+              Q5 = -2.0109921195e-07f;
+  const uint32_t bits = __float_as_uint(x);
+  const bool neg = (bits >> 31) != 0;
+  const uint32_t hx = bits & 0x7fffffffu;
+  if (hx >= 0x4195b844u) {  // |x| >= 27 ln2
+    if (hx >= 0x42b17218u) {
+      if (hx > 0x7f800000u) return x + x;  // NaN
+      if (hx == 0x7f800000u) return neg ? -1.0f : x;
+      if (x > kOThreshold) return kHuge * kHuge;  // overflow
+    }
+    if (neg) return kTiny - 1.0f;  // expm1 -> -1
+  }
+  float hi, lo, c = 0.0f;
+  int k;
+  if (hx > 0x3eb17218u) {    // |x| > ln2 / 2
+    if (hx < 0x3f851592u) {  // and |x| < 1.5 ln2
+      if (!neg) {
+        hi = x - kLn2Hi;
+        lo = kLn2Lo;
+        k = 1;
+      } else {
+        hi = x + kLn2Hi;
+        lo = -kLn2Lo;
+        k = -1;
+      }
+    } else {
+      k = static_cast<int>(kInvLn2 * x + (neg ? -0.5f : 0.5f));
+      const float t = static_cast<float>(k);
+      hi = x - t * kLn2Hi;
+      lo = t * kLn2Lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x33000000u) {  // |x| < 2^-25
+    const float t = kHuge + x;
+    return x - (t - (kHuge + x));
+  } else {
+    k = 0;
+  }
+  const float hfx = 0.5f * x;
+  const float hxs = x * hfx;
+  const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  float t = 3.0f - r1 * hfx;
+  float e = hxs * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  e = (x * (e - c) - c);
+  e -= hxs;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) {
+    if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+    return 1.0f + 2.0f * (x - e);
+  }
+  const uint32_t kexp = static_cast<uint32_t>(k) << 23;  // adds k to the exponent
+  float y;
+  if (k <= -2 || k > 56) {
+    y = 1.0f - (e - x);
+    return __uint_as_float(__float_as_uint(y) + kexp) - 1.0f;
+  }
+  if (k < 23) {
+    t = __uint_as_float(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+    y = t - (e - x);
+  } else {
+    t = __uint_as_float(static_cast<uint32_t>(0x7f - k) << 23);  // 2^-k
+    y = x - (e + t);
+    y += 1.0f;
+  }
+  return __uint_as_float(__float_as_uint(y) + kexp);
+}
+
+__device__ __forceinline__ float dev_tanhf(float x) {
+  const uint32_t jx = __float_as_uint(x), ix = jx & 0x7fffffffu;
+  const bool neg = (jx >> 31) != 0;
+  if (ix >= 0x7f800000u) return neg ? 1.0f / x - 1.0f : 1.0f / x + 1.0f;  // +-inf -> +-1, NaN -> NaN
+  float z;
+  if (ix < 0x41b00000u) {  // |x| < 22
+    if (ix == 0) return x;
+    if (ix < 0x24000000u) return x * (1.0f + x);  // |x| < 2^-55
+    if (ix >= 0x3f800000u) {                      // |x| >= 1
+      const float t = dev_expm1f(2.0f * fabsf(x));
+      z = 1.0f - 2.0f / (t + 2.0f);
+    } else {
+      const float t = dev_expm1f(-2.0f * fabsf(x));
+      z = -t / (t + 2.0f);
+    }
+  } else {
+    z = 1.0f - 1.0e-30f;
+  }
+  return neg ? -z : z;
 }
 
 // ---------------------------------------------------------------- rounding

@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(float* __restrict__ g, co
   if (gelu) {
     const float kS = 0.7978846f;  // norms.rs:36
     float x3 = v * v * v;
-    v = 0.5f * v * (1.0f + tanhf(kS * (v + 0.044715f * x3)));
+    v = 0.5f * v * (1.0f + dev_tanhf(kS * (v + 0.044715f * x3)));
   } else {
     v = v * (1.0f / (1.0f + dev_expf(-v)));
   }
@@ -330,6 +330,10 @@ __global__ void expf_kernel(const float* __restrict__ in, size_t n, float* __res
   size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   if (i < n) out[i] = dev_expf(in[i]);
 }
+__global__ void tanhf_kernel(const float* __restrict__ in, size_t n, float* __restrict__ out) {
+  size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i < n) out[i] = dev_tanhf(in[i]);
+}
 // exp over a contiguous range of f32 bit patterns [base, base + n).
 __global__ void expf_bits_kernel(uint32_t base, uint32_t n, float* __restrict__ out) {
   uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -351,6 +355,12 @@ int launch_f16_to_f32(const uint16_t* in, size_t n, float* out, hipStream_t s) {
 int launch_expf(const float* in, size_t n, float* out, hipStream_t s) {
   if (!n) return kOk;
   hipLaunchKernelGGL(expf_kernel, dim3((n + 255) / 256), dim3(256), 0, s, in, n, out);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+int launch_tanhf(const float* in, size_t n, float* out, hipStream_t s) {
+  if (!n) return kOk;
+  hipLaunchKernelGGL(tanhf_kernel, dim3((n + 255) / 256), dim3(256), 0, s, in, n, out);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }

@@ -659,7 +659,7 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
       if (job.act == 2) {
         const float kS = 0.7978846f;  // norms.rs:36
         float x3 = g * g * g;
-        g = 0.5f * g * (1.0f + tanhf(kS * (g + 0.044715f * x3)));
+        g = 0.5f * g * (1.0f + dev_tanhf(kS * (g + 0.044715f * x3)));
       } else {
         g = g * (1.0f / (1.0f + dev_expf(-g)));
       }

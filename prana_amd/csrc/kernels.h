@@ -44,6 +44,7 @@ int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_d
 int launch_f32_to_f16(const float* in, size_t n, uint16_t* out, hipStream_t s);
 int launch_f16_to_f32(const uint16_t* in, size_t n, float* out, hipStream_t s);
 int launch_expf(const float* in, size_t n, float* out, hipStream_t s);
+int launch_tanhf(const float* in, size_t n, float* out, hipStream_t s);
 int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s);
 int launch_argmax(const float* v, size_t rows, size_t n, uint32_t* out, hipStream_t s);
 int launch_embed(const DevMat& m, const uint32_t* tokens, size_t n, float scale, float* out, hipStream_t s);

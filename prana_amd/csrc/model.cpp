@@ -64,15 +64,6 @@ int Model::set_tensor(const std::string& name, int t, const uint64_t* dims, int 
     flag = true;
     return kOk;
   };
-  auto mat_of = [&](size_t cols, size_t rows, std::unique_ptr<Mat>& dst) -> int {
-    int rc = want2(cols, rows);
-    if (rc) return rc;
-    auto m = std::make_unique<Mat>();
-    rc = mat_from_ggml(t, rows, cols, bytes, nbytes, *m);
-    if (rc) return rc;
-    dst = std::move(m);
-    return kOk;
-  };
 
   if (name == "token_embd.weight") {
     int rc = want2(k.dim, k.vocab_size);
@@ -115,8 +106,16 @@ int Model::set_tensor(const std::string& name, int t, const uint64_t* dims, int 
     emb = std::move(m);
     return kOk;
   }
-  if (name == "output.weight") return mat_of(k.dim, k.vocab_size, wcls);
   if (name == "output_norm.weight") return vec_of(k.dim, rms_final, has_rms_final);
+  size_t cols = 0, rows = 0;
+  if (std::unique_ptr<Mat>* slot = mat_slot(name, &cols, &rows)) {
+    int rc = want2(cols, rows);
+    if (rc) return rc;
+    auto m = std::make_unique<Mat>();
+    if ((rc = mat_from_ggml(t, rows, cols, bytes, nbytes, *m))) return rc;
+    *slot = std::move(m);
+    return kOk;
+  }
 
   size_t l;
   std::string rest;
@@ -127,14 +126,63 @@ int Model::set_tensor(const std::string& name, int t, const uint64_t* dims, int 
   if (rest == "attn_q.bias") return vec_of(q_dim, L.vec[kBq], L.has[kBq]);
   if (rest == "attn_k.bias") return vec_of(kv_dim, L.vec[kBk], L.has[kBk]);
   if (rest == "attn_v.bias") return vec_of(kv_dim, L.vec[kBv], L.has[kBv]);
-  if (rest == "attn_q.weight") return mat_of(k.dim, q_dim, L.w[kWq]);
-  if (rest == "attn_k.weight") return mat_of(k.dim, kv_dim, L.w[kWk]);
-  if (rest == "attn_v.weight") return mat_of(k.dim, kv_dim, L.w[kWv]);
-  if (rest == "attn_output.weight") return mat_of(q_dim, k.dim, L.w[kWo]);
-  if (rest == "ffn_gate.weight") return mat_of(k.dim, k.hidden_dim, L.w[kW1]);
-  if (rest == "ffn_down.weight") return mat_of(k.hidden_dim, k.dim, L.w[kW2]);
-  if (rest == "ffn_up.weight") return mat_of(k.dim, k.hidden_dim, L.w[kW3]);
   return fail(kErrInvalid, "unknown tensor '" + name + "'");
+}
+
+// The projection / classifier slot a GGUF name addresses, with its expected
+// [cols, rows]; null for any other name.
+std::unique_ptr<Mat>* Model::mat_slot(const std::string& name, size_t* cols, size_t* rows) {
+  const size_t q_dim = c.n_heads * c.head_dim, kv_dim = c.n_kv_heads * c.head_dim;
+  if (name == "output.weight") {
+    *cols = c.dim;
+    *rows = c.vocab_size;
+    return &wcls;
+  }
+  size_t l;
+  std::string rest;
+  if (!parse_layer(name, l, rest) || l >= layers.size()) return nullptr;
+  static const struct {
+    const char* name;
+    LayerMat slot;
+  } kMats[] = {{"attn_q.weight", kWq},      {"attn_k.weight", kWk},   {"attn_v.weight", kWv},
+               {"attn_output.weight", kWo}, {"ffn_gate.weight", kW1}, {"ffn_down.weight", kW2},
+               {"ffn_up.weight", kW3}};
+  for (const auto& e : kMats) {
+    if (rest != e.name) continue;
+    const size_t in[7] = {c.dim, c.dim, c.dim, q_dim, c.dim, c.hidden_dim, c.dim};
+    const size_t out[7] = {q_dim, kv_dim, kv_dim, c.dim, c.hidden_dim, c.dim, c.hidden_dim};
+    *cols = in[e.slot];
+    *rows = out[e.slot];
+    return &layers[l].w[e.slot];
+  }
+  return nullptr;
+}
+
+// A QuantMatrix with f32 scales (quantize_q8's output, matmul.rs:61-84) into
+// a projection or classifier slot.
+int Model::set_q8(const std::string& name, size_t rows, size_t cols, const int8_t* q, const float* scales) {
+  size_t want_c = 0, want_r = 0;
+  std::unique_ptr<Mat>* slot = mat_slot(name, &want_c, &want_r);
+  if (!slot) return fail(kErrInvalid, "unknown matrix '" + name + "'");
+  PRANA_CHECK(rows == want_r && cols == want_c, "tensor '" + name + "': shape does not match the config");
+  auto m = std::make_unique<Mat>();
+  if (int rc = mat_from_q8_parts(rows, cols, q, scales, *m)) return rc;
+  *slot = std::move(m);
+  finalized = false;
+  return kOk;
+}
+
+// Config checks shared by prana_model_create and the GGUF loader: what the
+// kernels of this backend need (the activation quantizer and the fused
+// norm/MLP epilogues work in whole 32-blocks of dim and hidden_dim).
+int check_config(const prana_config& c) {
+  PRANA_CHECK(c.dim > 0 && c.n_layers > 0 && c.n_heads > 0 && c.vocab_size > 0 && c.seq_len > 0,
+              "config: zero-sized dimension");
+  PRANA_CHECK(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "config: n_heads % n_kv_heads != 0");
+  PRANA_CHECK(c.head_dim > 0 && c.head_dim % 2 == 0 && c.head_dim <= 256, "config: head_dim must be even and <= 256");
+  PRANA_CHECK(c.dim % 32 == 0 && c.hidden_dim % 32 == 0, "config: dim and hidden_dim must be multiples of 32");
+  PRANA_CHECK(c.act == 0 || c.act == 1, "config: act must be 0 (silu) or 1 (gelu_tanh)");
+  return kOk;
 }
 
 int Model::finalize() {
@@ -482,8 +530,11 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
                                     &quantized);
       if (rc) return rc;
     }
-    if (!quantized && (rc = launch_quantize_acts(ws.attn.as<float>(), n, q_dim, ws.qa.as<int8_t>(),
-                                                 ws.sa.as<float>(), ws.sums.as<int>(), s)))
+    // A q_dim that is not a whole number of 32-blocks only occurs with a dense
+    // f32 wo (quantized formats need cols % 32 == 0), which reads ws.attn.
+    if (!quantized && q_dim % 32 == 0 &&
+        (rc = launch_quantize_acts(ws.attn.as<float>(), n, q_dim, ws.qa.as<int8_t>(), ws.sa.as<float>(),
+                                   ws.sums.as<int>(), s)))
       return rc;
     GemvOut ores{x, c.dim, nullptr, 1};
     if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;

@@ -101,6 +101,8 @@ struct Model {
 
   int set_tensor(const std::string& name, int ggml_type, const uint64_t* dims, int n_dims, const void* bytes,
                  size_t nbytes);
+  int set_q8(const std::string& name, size_t rows, size_t cols, const int8_t* q, const float* scales);
+  std::unique_ptr<Mat>* mat_slot(const std::string& name, size_t* cols, size_t* rows);
   int finalize();
   size_t stream_bytes() const;
   const Mat& head() const;
@@ -141,6 +143,8 @@ struct Model {
   int generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
                uint32_t* out, size_t* n_out, prana_gen_stats* st);
 };
+
+int check_config(const prana_config& c);
 
 int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, size_t p, size_t steps, size_t k,
                          const uint32_t* stops, size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* st);

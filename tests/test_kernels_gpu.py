@@ -1,6 +1,6 @@
 """GPU parity: every kernel entry point of libprana_hip against the CPU oracle
 on the same seeded inputs. Integer and f32 results must be bit-identical
-(compared as raw bits), except gelu_tanh (libm tanhf boundary, 1e-6 rel)."""
+(compared as raw bits)."""
 import numpy as np
 import pytest
 
@@ -279,6 +279,25 @@ def test_expf_exhaustive():
         dx.free()
 
 
+def test_tanhf_exhaustive():
+    # Device tanhf (gelu_tanh's f32::tanh) vs the host glibc tanhf over every
+    # f32 bit pattern (16 chunks).
+    lib = P.load()
+    n = 1 << 28
+    d = P.DeviceArray((n,), np.float32)
+    for c in range(16):
+        base = c * n
+        x = np.arange(base, base + n, dtype=np.uint32).view(np.float32)
+        dx = P.DeviceArray.from_host(x)
+        P.check(lib.prana_tanhf(dx.ptr, n, d.ptr, None))
+        got = d.to_host()
+        want = O.tanhf_bits(base, n, 16)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), c
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), c
+        dx.free()
+
+
 def test_act_mul_and_add_bias():
     # g = silu(g) * u and x += bias: the oracle's silu, then one IEEE f32
     # multiply / add per element (numpy float32 arithmetic rounds the same way)
@@ -290,12 +309,15 @@ def test_act_mul_and_add_bias():
     assert same_bits(P.add_bias(x, b), x + b[None, :])
 
 
-def test_gelu_tanh_tolerance():
-    # gelu_tanh is Gemma-only; device tanhf vs glibc tanhf is the libm
-    # boundary, so this is a tolerance check (1e-6 relative + 1e-7).
-    x = rng(5).standard_normal(50000).astype(np.float32) * 4
-    g, o = P.gelu_tanh(x), O.gelu_tanh(x)
-    assert np.all(np.abs(g - o) <= 1e-6 * np.abs(o) + 1e-7)
+def test_gelu_tanh_bitexact():
+    # gelu_tanh (norms.rs:35-41) over normal draws, the tanh saturation range,
+    # tiny and special values, alone and fused with the up product
+    x = np.concatenate([rng(5).standard_normal(50000).astype(np.float32) * 4,
+                        np.linspace(-30, 30, 4001, dtype=np.float32),
+                        np.float32([0.0, -0.0, 1e-30, -1e-30, 1e-20, np.inf, -np.inf, 9.5, -9.5])])
+    assert same_bits(P.gelu_tanh(x), O.gelu_tanh(x))
+    u = rng(6).standard_normal(x.size).astype(np.float32)
+    assert same_bits(P.act_mul(x, u, gelu=True), O.gelu_tanh(x) * u)
 
 
 @pytest.mark.parametrize("n", [1, 2, 7, 256, 512, 513, 2049])
