@@ -326,6 +326,71 @@ int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t *out);
 /* The configuration a model was created or loaded with. */
 int prana_model_config(prana_model_t m, prana_config *cfg);
 
+/* ---------------------------------------------------------------- graph
+ * prana-graph (prana-graph/src/lib.rs:25-220) over device buffers: a
+ * define-then-run graph whose node values are f32 buffers in device memory
+ * and whose ops are this library's kernels (the same ones the model runs, so
+ * each value equals the reference op's output bit for bit). Node ids are
+ * indices handed out by the builders; every builder checks the ids it is
+ * given. Weights are copied to the device when the node is built. */
+typedef struct prana_graph *prana_graph_t;
+
+/* GraphError (lib.rs:55-63), reported by prana_graph_execute. */
+#define PRANA_GRAPH_UNSET_INPUT 1
+#define PRANA_GRAPH_SHAPE_MISMATCH 2
+#define PRANA_GRAPH_NOT_F32 3
+
+/* Graph::new (lib.rs:66-68). */
+int prana_graph_create(prana_graph_t *out);
+int prana_graph_destroy(prana_graph_t g);
+/* Graph::input (lib.rs:82-87): the graph's row count becomes
+ * max(previous, n_tokens). */
+int prana_graph_input(prana_graph_t g, size_t n_tokens, size_t *id);
+/* Graph::matmul_f32 (lib.rs:89-91): weight host [n_rows][k] f32; the value
+ * is [n_tokens, n_rows] (matmul_f32, matmul.rs:150-157). */
+int prana_graph_matmul_f32(prana_graph_t g, size_t x, const float *weight, size_t k, size_t n_rows, size_t *id);
+/* Graph::matmul_q8 (lib.rs:93-95): a QuantMatrix by its parts, host q
+ * [rows][cols] i8 and scales [rows][cols/32] f32 (cols % 32 == 0); the value
+ * is [n_tokens, rows] (matmul_q8_f32, matmul.rs:162-178). */
+int prana_graph_matmul_q8(prana_graph_t g, size_t x, size_t rows, size_t cols, const int8_t *q, const float *scales,
+                          size_t *id);
+/* Graph::rmsnorm (lib.rs:97-99): weight host [dim]; value [rows, dim]. */
+int prana_graph_rmsnorm(prana_graph_t g, size_t x, const float *weight, size_t dim, float eps, size_t *id);
+/* Graph::add (lib.rs:101-103): elementwise, the shape of a. */
+int prana_graph_add(prana_graph_t g, size_t a, size_t b, size_t *id);
+/* Graph::softmax (lib.rs:105-107): one softmax over all values; value [n]. */
+int prana_graph_softmax(prana_graph_t g, size_t x, size_t *id);
+/* Graph::rope (lib.rs:109-113): NeoX RoPE (attention.rs:59-80) on
+ * [n_tokens, n_heads*head_dim], row p at position p. */
+int prana_graph_rope(prana_graph_t g, size_t x, size_t n_heads, size_t head_dim, float theta_base, size_t *id);
+/* Graph::attention (lib.rs:115-124): causal attention over f32 Q/K/V of the
+ * n_tokens rows (attention.rs:236-284); head_dim <= 256 on this backend. */
+int prana_graph_attention(prana_graph_t g, size_t q, size_t k, size_t v, size_t n_heads, size_t n_kv_heads,
+                          size_t head_dim, size_t *id);
+/* Graph::set_input (lib.rs:126-129) with Tensor::from_f32(shape, values):
+ * host values, or (_device) a device pointer, copied into the graph. Any node
+ * may be given a value; execute then keeps it. */
+int prana_graph_set_input(prana_graph_t g, size_t id, const float *values, const size_t *shape, int n_dims);
+int prana_graph_set_input_device(prana_graph_t g, size_t id, const float *values, const size_t *shape, int n_dims);
+/* Graph::execute (lib.rs:132-141): evaluates every node without a value in
+ * definition order and returns when the device is done. Values are kept, as
+ * in the reference: a later set_input does not recompute nodes already
+ * evaluated (see prana_graph_reset). On a GraphError it returns
+ * PRANA_ERR_INVALID with *error_kind = PRANA_GRAPH_* and *error_node = the
+ * unset input or the mismatching node; both are 0 on success. */
+int prana_graph_execute(prana_graph_t g, int *error_kind, size_t *error_node);
+/* No counterpart in the reference: drops every computed (non-input) value so
+ * the next execute recomputes the graph over new inputs, weights kept. */
+int prana_graph_reset(prana_graph_t g);
+/* Shape of a node's value (up to 8 dims). */
+int prana_graph_shape(prana_graph_t g, size_t id, size_t *shape, int *n_dims);
+/* Graph::output_f32 (lib.rs:216-219): copy to host; cap counts floats,
+ * *n = the value's element count (PRANA_ERR_SHORT_BUFFER when cap < *n). */
+int prana_graph_output_f32(prana_graph_t g, size_t id, float *out, size_t cap, size_t *n);
+/* The value in place: a device pointer valid until the node is recomputed
+ * or the graph destroyed. */
+int prana_graph_output_device(prana_graph_t g, size_t id, const float **ptr, size_t *n);
+
 #ifdef __cplusplus
 }
 #endif

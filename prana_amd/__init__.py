@@ -523,6 +523,116 @@ def load_gguf(source, precision="f32"):
     return m
 
 
+class GraphError(PranaError):
+    """GraphError (prana-graph lib.rs:55-63): kind is "UnsetInput",
+    "ShapeMismatch" or "NotF32"; node is the unset input or the failing node."""
+
+    KINDS = {1: "UnsetInput", 2: "ShapeMismatch", 3: "NotF32"}
+
+    def __init__(self, msg, code, kind, node):
+        super().__init__(msg, code)
+        self.kind, self.node = self.KINDS.get(kind, str(kind)), node
+
+
+class Graph:
+    """prana_graph::Graph (lib.rs:25-220) over device buffers: build nodes,
+    bind inputs, execute, read outputs. Node ids are plain ints."""
+
+    def __init__(self):
+        init()
+        h = C.c_void_p()
+        check(load().prana_graph_create(C.byref(h)))
+        self.h = h
+
+    def _node(self, fn, *args):
+        i = C.c_size_t()
+        check(fn(self.h, *args, C.byref(i)))
+        return i.value
+
+    def input(self, n_tokens):
+        return self._node(load().prana_graph_input, n_tokens)
+
+    def matmul_f32(self, x, weight, k, n_rows):
+        w = np.ascontiguousarray(weight, np.float32).ravel()
+        if w.size != k * n_rows:
+            raise ValueError("weight must hold n_rows * k values")
+        return self._node(load().prana_graph_matmul_f32, x, _ptr(w), k, n_rows)
+
+    def matmul_q8(self, x, q, scales):
+        """A QuantMatrix by its parts (quantize_q8's q [rows, cols], scales [rows, cols/32])."""
+        q = np.ascontiguousarray(q, np.int8)
+        sc = np.ascontiguousarray(scales, np.float32)
+        if sc.shape != (q.shape[0], q.shape[1] // 32):
+            raise ValueError("scales must be [rows, cols/32]")
+        return self._node(load().prana_graph_matmul_q8, x, q.shape[0], q.shape[1], _ptr(q), _ptr(sc))
+
+    def rmsnorm(self, x, weight, dim, eps):
+        w = np.ascontiguousarray(weight, np.float32)
+        if w.size != dim:
+            raise ValueError("weight must hold dim values")
+        return self._node(load().prana_graph_rmsnorm, x, _ptr(w), dim, eps)
+
+    def add(self, a, b):
+        return self._node(load().prana_graph_add, a, b)
+
+    def softmax(self, x):
+        return self._node(load().prana_graph_softmax, x)
+
+    def rope(self, x, n_heads, head_dim, theta_base):
+        return self._node(load().prana_graph_rope, x, n_heads, head_dim, theta_base)
+
+    def attention(self, q, k, v, n_heads, n_kv_heads, head_dim):
+        return self._node(load().prana_graph_attention, q, k, v, n_heads, n_kv_heads, head_dim)
+
+    def set_input(self, node, values, shape=None):
+        """Tensor::from_f32(shape, values); a DeviceArray is copied on the device."""
+        if isinstance(values, DeviceArray):
+            shape = tuple(values.shape) if shape is None else tuple(shape)
+            sh = (C.c_size_t * max(len(shape), 1))(*shape)
+            check(load().prana_graph_set_input_device(self.h, node, values.ptr, sh, len(shape)))
+            return
+        v = np.ascontiguousarray(values, np.float32)
+        shape = v.shape if shape is None else tuple(shape)
+        if int(np.prod(shape)) != v.size:
+            raise ValueError(f"shape {shape} does not match {v.size} values")
+        sh = (C.c_size_t * max(len(shape), 1))(*shape)
+        check(load().prana_graph_set_input(self.h, node, _ptr(v) if v.size else None, sh, len(shape)))
+
+    def execute(self):
+        kind, node = C.c_int(), C.c_size_t()
+        rc = load().prana_graph_execute(self.h, C.byref(kind), C.byref(node))
+        if rc != 0:
+            msg = load().prana_last_error().decode(errors="replace")
+            if kind.value:
+                raise GraphError(msg, rc, kind.value, node.value)
+            check(rc)
+
+    def reset(self):
+        check(load().prana_graph_reset(self.h))
+
+    def shape(self, node):
+        sh, nd = (C.c_size_t * 8)(), C.c_int()
+        check(load().prana_graph_shape(self.h, node, sh, C.byref(nd)))
+        return tuple(sh[i] for i in range(nd.value))
+
+    def output_f32(self, node):
+        n = C.c_size_t()
+        rc = load().prana_graph_output_f32(self.h, node, None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        out = np.empty(n.value, np.float32)
+        check(load().prana_graph_output_f32(self.h, node, _ptr(out), out.size, C.byref(n)))
+        return out
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_graph_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
 def gemv_profile(on, period=1):
     """Time every `period`-th decode-GEMV dispatch while on (dispatch timestamps)."""
     check(load().prana_gemv_profile(max(1, int(period)) if on else 0))

@@ -132,6 +132,24 @@ _SIGS = {
     "prana_gguf_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
     "prana_model_load_gguf": (c_int, [c_void_p, c_int, C.POINTER(c_void_p)]),
     "prana_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
+    # graph
+    "prana_graph_create": (c_int, [C.POINTER(c_void_p)]),
+    "prana_graph_destroy": (c_int, [c_void_p]),
+    "prana_graph_input": (c_int, [c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_graph_matmul_f32": (c_int, [c_void_p, c_size, c_void_p, c_size, c_size, C.POINTER(c_size)]),
+    "prana_graph_matmul_q8": (c_int, [c_void_p, c_size, c_size, c_size, c_void_p, c_void_p, C.POINTER(c_size)]),
+    "prana_graph_rmsnorm": (c_int, [c_void_p, c_size, c_void_p, c_size, c_float, C.POINTER(c_size)]),
+    "prana_graph_add": (c_int, [c_void_p, c_size, c_size, C.POINTER(c_size)]),
+    "prana_graph_softmax": (c_int, [c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_graph_rope": (c_int, [c_void_p, c_size, c_size, c_size, c_float, C.POINTER(c_size)]),
+    "prana_graph_attention": (c_int, [c_void_p, c_size, c_size, c_size, c_size, c_size, c_size, C.POINTER(c_size)]),
+    "prana_graph_set_input": (c_int, [c_void_p, c_size, c_void_p, C.POINTER(c_size), c_int]),
+    "prana_graph_set_input_device": (c_int, [c_void_p, c_size, c_void_p, C.POINTER(c_size), c_int]),
+    "prana_graph_execute": (c_int, [c_void_p, C.POINTER(c_int), C.POINTER(c_size)]),
+    "prana_graph_reset": (c_int, [c_void_p]),
+    "prana_graph_shape": (c_int, [c_void_p, c_size, C.POINTER(c_size), C.POINTER(c_int)]),
+    "prana_graph_output_f32": (c_int, [c_void_p, c_size, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_graph_output_device": (c_int, [c_void_p, c_size, C.POINTER(c_void_p), C.POINTER(c_size)]),
 }
 
 # libprana_synth.so (prana_amd/synth/prana_synth.h): fixture encoders of the

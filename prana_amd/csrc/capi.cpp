@@ -10,6 +10,7 @@
 #include <string>
 
 #include "gguf.h"
+#include "graph.h"
 #include "model.h"
 
 namespace prana {
@@ -847,6 +848,223 @@ int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t* out) {
     m->m.layers.resize(c.n_layers);
     if (int rc = gguf_load_model(*g->g, precision, m->m)) return rc;
     *out = m.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+// ------------------------------------------------------------------ graph (prana-graph over device buffers)
+int prana_graph_create(prana_graph_t* out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(out, "null argument");
+    *out = new prana_graph();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_destroy(prana_graph_t g) {
+  return guard([&] {
+    if (g) (void)hipStreamSynchronize(pick_stream(nullptr));
+    delete g;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_input(prana_graph_t g, size_t n_tokens, size_t* id) {
+  return guard([&] {
+    PRANA_CHECK(g && id, "null argument");
+    g->g.n_tokens = std::max(g->g.n_tokens, n_tokens);
+    *id = g->g.push(GraphNode{});
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_matmul_f32(prana_graph_t g, size_t x, const float* weight, size_t k, size_t n_rows, size_t* id) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && weight && id, "null argument");
+    PRANA_CHECK(k > 0 && n_rows > 0, "graph: matmul_f32 needs k > 0 and n_rows > 0");
+    if (int rc = g->g.check_id(x, "matmul_f32")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kMatmulF32;
+    n.a = x;
+    n.w = std::make_unique<Mat>();
+    if (int rc = mat_from_ggml(0, n_rows, k, weight, n_rows * k * 4, *n.w)) return rc;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_matmul_q8(prana_graph_t g, size_t x, size_t rows, size_t cols, const int8_t* q, const float* scales,
+                          size_t* id) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && q && scales && id, "null argument");
+    PRANA_CHECK(rows > 0 && cols > 0, "graph: matmul_q8 needs a non-empty matrix");
+    if (int rc = g->g.check_id(x, "matmul_q8")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kMatmulQ8;
+    n.a = x;
+    n.w = std::make_unique<Mat>();
+    if (int rc = mat_from_q8_parts(rows, cols, q, scales, *n.w)) return rc;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_rmsnorm(prana_graph_t g, size_t x, const float* weight, size_t dim, float eps, size_t* id) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g && weight && id, "null argument");
+    PRANA_CHECK(dim > 0, "graph: rmsnorm needs dim > 0");
+    if (int rc = g->g.check_id(x, "rmsnorm")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kRmsNorm;
+    n.a = x;
+    n.dim = dim;
+    n.eps = eps;
+    if (int rc = n.vec.alloc(dim * 4)) return rc;
+    PRANA_HIP(hipMemcpy(n.vec.p, weight, dim * 4, hipMemcpyHostToDevice));
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_add(prana_graph_t g, size_t a, size_t b, size_t* id) {
+  return guard([&] {
+    PRANA_CHECK(g && id, "null argument");
+    if (int rc = g->g.check_id(a, "add")) return rc;
+    if (int rc = g->g.check_id(b, "add")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kAdd;
+    n.a = a;
+    n.b = b;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_softmax(prana_graph_t g, size_t x, size_t* id) {
+  return guard([&] {
+    PRANA_CHECK(g && id, "null argument");
+    if (int rc = g->g.check_id(x, "softmax")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kSoftmax;
+    n.a = x;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_rope(prana_graph_t g, size_t x, size_t n_heads, size_t head_dim, float theta_base, size_t* id) {
+  return guard([&] {
+    PRANA_CHECK(g && id, "null argument");
+    PRANA_CHECK(head_dim > 0 && head_dim % 2 == 0, "graph: head_dim must be even for RoPE");
+    PRANA_CHECK(n_heads > 0, "graph: rope needs n_heads > 0");
+    if (int rc = g->g.check_id(x, "rope")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kRope;
+    n.a = x;
+    n.n_heads = n_heads;
+    n.head_dim = head_dim;
+    n.theta = theta_base;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_attention(prana_graph_t g, size_t q, size_t k, size_t v, size_t n_heads, size_t n_kv_heads,
+                          size_t head_dim, size_t* id) {
+  return guard([&] {
+    PRANA_CHECK(g && id, "null argument");
+    PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "graph: n_heads must be a multiple of n_kv_heads");
+    PRANA_CHECK(n_heads > 0 && head_dim > 0 && head_dim <= 256, "graph: attention needs head_dim in 1..=256");
+    for (size_t in : {q, k, v})
+      if (int rc = g->g.check_id(in, "attention")) return rc;
+    GraphNode n;
+    n.op = GraphNode::kAttention;
+    n.a = q;
+    n.b = k;
+    n.c = v;
+    n.n_heads = n_heads;
+    n.n_kv_heads = n_kv_heads;
+    n.head_dim = head_dim;
+    *id = g->g.push(std::move(n));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_set_input(prana_graph_t g, size_t id, const float* values, const size_t* shape, int n_dims) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g, "null graph");
+    return g->g.set_value(id, values, false, shape, n_dims, pick_stream(nullptr));
+  });
+}
+
+int prana_graph_set_input_device(prana_graph_t g, size_t id, const float* values, const size_t* shape, int n_dims) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g, "null graph");
+    return g->g.set_value(id, values, true, shape, n_dims, pick_stream(nullptr));
+  });
+}
+
+int prana_graph_execute(prana_graph_t g, int* error_kind, size_t* error_node) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(g, "null graph");
+    int kind = 0;
+    size_t node = 0;
+    const int rc = g->g.execute(pick_stream(nullptr), &kind, &node);
+    if (error_kind) *error_kind = kind;
+    if (error_node) *error_node = node;
+    return rc;
+  });
+}
+
+int prana_graph_reset(prana_graph_t g) {
+  return guard([&] {
+    PRANA_CHECK(g, "null graph");
+    for (GraphNode& n : g->g.nodes)
+      if (n.op != GraphNode::kInput) n.has_value = false;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_shape(prana_graph_t g, size_t id, size_t* shape, int* n_dims) {
+  return guard([&] {
+    PRANA_CHECK(g && shape && n_dims, "null argument");
+    if (int rc = g->g.check_id(id, "shape")) return rc;
+    const GraphNode& n = g->g.nodes[id];
+    if (!n.has_value) return fail(kErrInvalid, "graph: node " + std::to_string(id) + " has no value");
+    *n_dims = static_cast<int>(n.shape.size());
+    for (size_t i = 0; i < n.shape.size(); i++) shape[i] = n.shape[i];
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_output_f32(prana_graph_t g, size_t id, float* out, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && n, "null argument");
+    if (int rc = g->g.check_id(id, "output_f32")) return rc;
+    const GraphNode& node = g->g.nodes[id];
+    if (!node.has_value) return fail(kErrInvalid, "graph: input node " + std::to_string(id) + " is unset");
+    *n = node.numel();
+    if (!out || cap < *n) return fail(kErrShortBuffer, "graph: output buffer shorter than the node's value");
+    if (*n) PRANA_HIP(hipMemcpy(out, node.value.p, *n * 4, hipMemcpyDeviceToHost));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_graph_output_device(prana_graph_t g, size_t id, const float** ptr, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(g && ptr && n, "null argument");
+    if (int rc = g->g.check_id(id, "output_device")) return rc;
+    const GraphNode& node = g->g.nodes[id];
+    if (!node.has_value) return fail(kErrInvalid, "graph: input node " + std::to_string(id) + " is unset");
+    *ptr = node.value.as<float>();
+    *n = node.numel();
     return static_cast<int>(kOk);
   });
 }
