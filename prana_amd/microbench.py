@@ -4,6 +4,11 @@
 C1: the Q8_0 matmul sweep (R x K in {4096x4096, 14336x4096, 4096x14336,
 32000x4096}, N in {1, 4, 16, 64} tokens). Weight copies rotate so that the
 bytes touched per case exceed twice the 256 MB MALL.
+GEMM: the batched matrix-core GEMMs at the prefill batches of C4 (N = 511:
+Q4_0 Q|K|V, wo, gate, down) and C2 (N = 2047: Q6_K ffn_down, a Q4_K
+4096-column matrix, Q4_0 / Q8_0 896-column matrices), plus C1's Q8_0
+4096x4096 at N = 16 and 64 (the skinny kernel), over pre-quantized
+activations, reported as int8 TOPS against the 5.0 POPS dense peak.
 C3: attention over an f16 cache (32 query / 8 KV heads, head_dim 128) at
 contexts 1024, 4096, 16384 and 32768, q and the new k row under NeoX RoPE at
 position = context: one sequence (decode) on the exact kernels and on split-K
@@ -41,6 +46,14 @@ C1_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]
 C1_TOKENS = [1, 4, 16, 64]
 C3_CTX = [1024, 4096, 16384, 32768]
 WARMUP, TIMED = 3, 20
+Q4_0, Q4_K, Q6_K = 2, 12, 14
+GEMM_CASES = [  # (tag, ggml type, rows, cols, N)
+    ("C4 Q|K|V Q4_0", Q4_0, 6144, 4096, 511), ("C4 wo Q4_0", Q4_0, 4096, 4096, 511),
+    ("C4 ffn_gate Q4_0", Q4_0, 14336, 4096, 511), ("C4 ffn_down Q4_0", Q4_0, 4096, 14336, 511),
+    ("C2 ffn_down Q6_K", Q6_K, 896, 4864, 2047), ("C2-width Q4_K", Q4_K, 512, 4096, 2047),
+    ("C2 ffn_gate Q4_0", Q4_0, 4864, 896, 2047), ("C2 attn_v Q8_0", Q8_0, 128, 896, 2047),
+    ("C1 Q8_0", Q8_0, 4096, 4096, 16), ("C1 Q8_0", Q8_0, 4096, 4096, 64),
+]
 
 
 def _marker(P, buf):
@@ -71,6 +84,24 @@ def run(manifest_path, only=None):
             P.check(P.load().prana_synchronize())
             cases.append({"config": "C1", "case": f"Q8_0 {rows}x{cols} N={n}", "calls": TIMED,
                           "bytes": rows * cols // 32 * 34 + n * cols * 4 + n * rows * 4, "copies": copies})
+        del mats
+
+    for tag, ty, rows, cols, n in (GEMM_CASES if only in (None, "GEMM") else []):
+        raw = P.synth_tensor(ty, rows, cols, rows + cols + n, 0.02)
+        mats = [P.Matrix(ty, rows, cols, raw) for _ in range(2)]
+        print(f"GEMM {tag}", file=sys.stderr, flush=True)
+        x = rng.standard_normal((n, cols)).astype(np.float32)
+        q, sa, sums = P.quantize_acts(x)
+        dq, ds, dm = P.DeviceArray.from_host(q), P.DeviceArray.from_host(sa), P.DeviceArray.from_host(sums)
+        out = P.DeviceArray((n, rows), np.float32)
+        for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
+            _marker(P, marker)
+            for i in range(calls):
+                P.check(P.load().prana_matmul_prefill(mats[i % 2].h, None, dq.ptr, ds.ptr, dm.ptr, n, out.ptr, None))
+        _marker(P, marker)
+        P.check(P.load().prana_synchronize())
+        cases.append({"config": "GEMM", "case": f"{tag} {rows}x{cols} N={n}", "calls": TIMED,
+                      "bytes": len(raw) + n * cols + n * rows * 4, "ops": 2 * rows * cols * n})
         del mats
 
     nh, nkv, hd = 32, 8, 128
@@ -218,7 +249,8 @@ def summarize(db, manifest_path):
     if cur is not None:
         segs.append(cur)
     # three segments per case: warmup, timed, then set-up of the next case
-    out = ["| config | case | kernels per call | us per call | GB/s | % of 8 TB/s |", "|---|---|---|---:|---:|---:|"]
+    out = ["| config | case | kernels per call | us per call | GB/s | % of 8 TB/s | int8 TOPS | % of 5 POPS |",
+           "|---|---|---|---:|---:|---:|---:|---:|"]
     for i, cs in enumerate(cases):
         seg = segs[3 * i + 1]
         work = [(n, d) for n, d in seg if "__amd_rocclr" not in n]
@@ -226,20 +258,59 @@ def summarize(db, manifest_path):
                         for n, _ in work})
         us = sum(d for _, d in work) / 1000.0 / cs["calls"]
         gbs = cs["bytes"] / (us * 1e-6) / 1e9
+        tops = cs["ops"] / (us * 1e-6) / 1e12 if "ops" in cs else None
+        ops_cols = f"| {tops:.1f} | {100 * tops / 5000:.1f}% |" if tops else "| | |"
         out.append(f"| {cs['config']} | {cs['case']} | {', '.join('`' + n + '`' for n in names)} | {us:.2f} | {gbs:.0f} "
-                   f"| {100 * gbs / 8000:.1f}% |")
+                   f"| {100 * gbs / 8000:.1f}% {ops_cols}")
+    print("\n".join(out))
+
+
+def summarize_counters(db, cus=256):
+    """Per-kernel MFMA / VALU utilisation from a rocprofv3 --pmc run with
+    SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_I8
+    SQ_ACTIVE_INST_VALU SQ_BUSY_CYCLES: MfmaUtil as rocprofv3 defines it
+    (busy cycles over GRBM active cycles x SIMDs), VALU busy (quad-cycles x 4
+    over active cycles x CUs), and int8 MFMA ops (MOPS x 512) per dispatch."""
+    import collections
+    import re
+    c = sqlite3.connect(db)
+    rows = c.execute("select dispatch_id, kernel_name, grid_size, counter_name, value from counters_collection").fetchall()
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    names = {}
+    for did, kn, gs, cn, v in rows:
+        per[did][cn] = max(per[did][cn], v) if cn == "GRBM_GUI_ACTIVE" else per[did][cn] + v
+        kk = kn.replace("(anonymous namespace)::", "").replace("prana::", "")
+        names[did] = (re.sub(r"^void ", "", kk.split("(")[0]), gs)
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for did, d in per.items():
+        for cn, v in d.items():
+            agg[names[did]][cn].append(v)
+    out = ["| kernel | grid | dispatches | MfmaUtil % | VALUBusy % | int8 MFMA ops / dispatch |", "|---|---:|---:|---:|---:|---:|"]
+    for (k, gs), d in sorted(agg.items()):
+        if "gemm" not in k and "gemv" not in k:
+            continue
+        n = len(d["GRBM_GUI_ACTIVE"])
+        gui = sum(d["GRBM_GUI_ACTIVE"]) / n
+        mfma = sum(d["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
+        valu = 4 * sum(d["SQ_ACTIVE_INST_VALU"]) / n
+        mops = sum(d["SQ_INSTS_VALU_MFMA_MOPS_I8"]) / n * 512
+        out.append(f"| `{k}` | {int(gs)} | {n} | {100 * mfma / (gui * 4 * cus):.2f} | {100 * valu / cus / gui:.1f} "
+                   f"| {mops:.3e} |")
     print("\n".join(out))
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--summarize", metavar="DB")
+    ap.add_argument("--counters", metavar="DB", help="MFMA / VALU utilisation table of a --pmc run")
     ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
-    ap.add_argument("--only", choices=["C1", "C3"], help="run one configuration's sweep")
+    ap.add_argument("--only", choices=["C1", "GEMM", "C3"], help="run one configuration's sweep")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
     if args.models:
         print(models_table(run_models()))
+    elif args.counters:
+        summarize_counters(args.counters)
     elif args.summarize:
         summarize(args.summarize, args.manifest)
     else:
