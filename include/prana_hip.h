@@ -326,6 +326,35 @@ int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t *out);
 /* The configuration a model was created or loaded with. */
 int prana_model_config(prana_model_t m, prana_config *cfg);
 
+/* ---------------------------------------------------------------- sampler
+ * Sampler (prana-model sampler.rs:6-71): greedy for temp <= 0, else
+ * temperature sampling driven by a seeded xorshift64* stream. Sampling runs
+ * on the device: logits / temp, the exact softmax, and the bucket walk
+ * (r -= p[i] until r <= 0) in the reference's f32 order, so the same seed
+ * gives the reference's tokens. */
+typedef struct prana_sampler *prana_sampler_t;
+
+/* Sampler::new (sampler.rs:13-19); XorShift::new maps seed 0 to 1. */
+int prana_sampler_create(float temp, uint64_t seed, prana_sampler_t *out);
+int prana_sampler_destroy(prana_sampler_t s);
+/* The RNG state (advances by one per temperature draw). */
+int prana_sampler_state(prana_sampler_t s, uint64_t *state);
+/* XorShift::next_f32 (sampler.rs:66-70): uniform in [0, 1). */
+int prana_sampler_next_f32(prana_sampler_t s, float *out);
+/* Sampler::sample (sampler.rs:22-39) over device logits [n]; one draw;
+ * *token is host memory; returns when the token is known. */
+int prana_sampler_sample(prana_sampler_t s, const float *logits, size_t n, uint32_t *token, prana_stream_t stream);
+/* The bucket walk alone (sampler.rs:29-36) over device probabilities for a
+ * given r: *out (device) = the first i with (r -= probs[i]) <= 0, else n-1. */
+int prana_sample_pick(const float *probs, size_t n, float r, uint32_t *out, prana_stream_t stream);
+/* generate (infer.rs:696-771) with a sampler: teacher-forced prompt, then one
+ * draw per sampled position (none for temp <= 0, which is prana_generate);
+ * stops on a token of stops; the sampler's state ends where the reference's
+ * would. */
+int prana_generate_sampled(prana_model_t m, const uint32_t *prompt, size_t p, size_t steps, const uint32_t *stops,
+                           size_t n_stops, prana_sampler_t sampler, uint32_t *out, size_t *n_out,
+                           prana_gen_stats *stats);
+
 /* ---------------------------------------------------------------- graph
  * prana-graph (prana-graph/src/lib.rs:25-220) over device buffers: a
  * define-then-run graph whose node values are f32 buffers in device memory

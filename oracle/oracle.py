@@ -83,6 +83,12 @@ _SIGS = {
     "po_forward_batch": (None, [c_vp, c_vp, c_vp, c_size, c_size, c_vp]),
     "po_argmax": (C.c_uint32, [c_vp, c_size]),
     "po_generate": (c_size, [c_vp, c_vp, c_size, c_size, c_vp, c_size, c_vp, C.POINTER(PoStats)]),
+    "po_xorshift_seed": (C.c_uint64, [C.c_uint64]),
+    "po_xorshift_next_f32": (c_float, [C.POINTER(C.c_uint64)]),
+    "po_sample_pick": (C.c_uint32, [c_vp, c_size, c_float]),
+    "po_sampler_sample": (C.c_uint32, [c_float, C.POINTER(C.c_uint64), c_vp, c_size]),
+    "po_generate_sampled": (c_size, [c_vp, c_vp, c_size, c_size, c_vp, c_size, c_float, C.POINTER(C.c_uint64),
+                                     c_vp]),
     "po_generate_speculative": (c_size, [c_vp, c_vp, c_vp, c_size, c_size, c_size, c_vp, c_size, c_vp,
                                          C.POINTER(PoStats)]),
 }
@@ -406,6 +412,36 @@ class Cache:
             lib().po_cache_free(self.h)
         except Exception:
             pass
+
+
+class Sampler:
+    """Sampler (sampler.rs:6-71): greedy for temp <= 0, else temperature
+    sampling with the xorshift64* stream of `seed`."""
+
+    def __init__(self, temp, seed):
+        self.temp = float(temp)
+        self.state = C.c_uint64(lib().po_xorshift_seed(seed))
+
+    def next_f32(self):
+        return lib().po_xorshift_next_f32(C.byref(self.state))
+
+    def sample(self, logits):
+        x = np.ascontiguousarray(logits, np.float32)
+        return int(lib().po_sampler_sample(self.temp, C.byref(self.state), P(x), x.size))
+
+
+def sample_pick(probs, r):
+    x = np.ascontiguousarray(probs, np.float32)
+    return int(lib().po_sample_pick(P(x), x.size, r))
+
+
+def generate_sampled(model, prompt, steps, sampler, stops=()):
+    prompt = np.asarray(prompt, np.uint32)
+    stops = np.asarray(stops, np.uint32)
+    out = np.zeros(max(steps, 1), np.uint32)
+    n = lib().po_generate_sampled(model.h, P(prompt), len(prompt), steps, P(stops) if len(stops) else None, len(stops),
+                                  sampler.temp, C.byref(sampler.state), P(out))
+    return out[:n].copy()
 
 
 def set_tier(tier, threads=0):

@@ -1086,6 +1086,75 @@ size_t po_generate(const po_model *m, const uint32_t *prompt, size_t p, size_t s
   return generated;
 }
 
+/* ---- Sampler (sampler.rs:6-71) ---------------------------------------- */
+/* XorShift::new / next_u64 / next_f32 (sampler.rs:55-71): xorshift64* with
+ * shifts 12, 25, 27 and multiplier 0x2545F4914F6CDD1D; next_f32 takes the
+ * top 24 bits / 2^24. */
+uint64_t po_xorshift_seed(uint64_t seed) { return seed ? seed : 1; }
+float po_xorshift_next_f32(uint64_t *state) {
+  uint64_t x = *state;
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  *state = x;
+  const uint64_t out = x * 0x2545F4914F6CDD1DULL;
+  return (float)(out >> 40) / (float)(1ULL << 24);
+}
+
+/* The bucket walk of Sampler::sample (sampler.rs:29-36): r -= p[i] until
+ * r <= 0; the last index when round-off leaves r above 0. */
+uint32_t po_sample_pick(const float *probs, size_t n, float r) {
+  for (size_t i = 0; i < n; i++) {
+    r -= probs[i];
+    if (r <= 0.0f) return (uint32_t)i;
+  }
+  return (uint32_t)(n - 1);
+}
+
+/* Sampler::sample (sampler.rs:22-39): greedy for temp <= 0, else logits /
+ * temp, softmax, one uniform draw, the bucket walk. */
+uint32_t po_sampler_sample(float temp, uint64_t *state, const float *logits, size_t n) {
+  if (temp <= 0.0f) return po_argmax(logits, n);  /* Sampler::new: greedy iff temp <= 0 */
+  float *scaled = malloc(n * 4), *probs = malloc(n * 4);
+  for (size_t i = 0; i < n; i++) scaled[i] = logits[i] / temp;
+  po_softmax(scaled, n, probs);
+  const float r = po_xorshift_next_f32(state);
+  const uint32_t t = po_sample_pick(probs, n, r);
+  free(scaled);
+  free(probs);
+  return t;
+}
+
+/* generate (infer.rs:696-771) with a Sampler: teacher-forced prompt, then
+ * sampled tokens; *state is the sampler's RNG and advances. */
+size_t po_generate_sampled(const po_model *m, const uint32_t *prompt, size_t p, size_t steps, const uint32_t *stops,
+                           size_t n_stops, float temp, uint64_t *state, uint32_t *out) {
+  size_t max_pos = m->c.seq_len < p + steps ? m->c.seq_len : p + steps;
+  po_cache *cache = po_cache_new(m, max_pos);
+  float *logits = malloc(m->c.vocab_size * 4);
+  uint32_t token = prompt[0];
+  size_t generated = 0, start_pos = 0;
+  if (p > 1 && p <= max_pos) {
+    po_prefill(m, cache, prompt, p - 1);
+    start_pos = p - 1;
+    token = prompt[p - 1];
+  }
+  for (size_t pos = start_pos; pos < max_pos; pos++) {
+    int need = pos + 1 >= p && pos + 1 < max_pos;
+    po_forward(m, cache, token, pos, need, logits);
+    if (pos + 1 >= max_pos) break;
+    uint32_t next = pos + 1 < p ? prompt[pos + 1] : po_sampler_sample(temp, state, logits, m->c.vocab_size);
+    if (pos + 1 >= p) {
+      if (is_stop(next, stops, n_stops)) break;
+      out[generated++] = next;
+    }
+    token = next;
+  }
+  free(logits);
+  po_cache_free(cache);
+  return generated;
+}
+
 /* generate_speculative (infer.rs:581-690) */
 size_t po_generate_speculative(const po_model *target, const po_model *draft, const uint32_t *prompt, size_t p,
                                size_t steps, size_t k, const uint32_t *stops, size_t n_stops, uint32_t *out,

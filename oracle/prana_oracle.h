@@ -181,6 +181,14 @@ typedef struct po_gen_stats {
 size_t po_generate(const po_model *m, const uint32_t *prompt, size_t p, size_t steps,
                    const uint32_t *stops, size_t n_stops, uint32_t *out, po_gen_stats *st);
 /* Greedy speculative decode (infer.rs:581-690). */
+/* Sampler (sampler.rs:6-71): xorshift64* RNG, bucket walk, sample, and
+ * generate driven by a sampler. */
+uint64_t po_xorshift_seed(uint64_t seed);
+float po_xorshift_next_f32(uint64_t *state);
+uint32_t po_sample_pick(const float *probs, size_t n, float r);
+uint32_t po_sampler_sample(float temp, uint64_t *state, const float *logits, size_t n);
+size_t po_generate_sampled(const po_model *m, const uint32_t *prompt, size_t p, size_t steps, const uint32_t *stops,
+                           size_t n_stops, float temp, uint64_t *state, uint32_t *out);
 size_t po_generate_speculative(const po_model *target, const po_model *draft, const uint32_t *prompt,
                                size_t p, size_t steps, size_t k, const uint32_t *stops, size_t n_stops,
                                uint32_t *out, po_gen_stats *st);

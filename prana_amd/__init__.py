@@ -523,6 +523,61 @@ def load_gguf(source, precision="f32"):
     return m
 
 
+class Sampler:
+    """Sampler (sampler.rs:6-71) on the device: greedy for temp <= 0, else
+    temperature sampling with the xorshift64* stream of `seed`."""
+
+    def __init__(self, temp, seed):
+        h = C.c_void_p()
+        check(load().prana_sampler_create(temp, seed, C.byref(h)))
+        self.h, self.temp = h, float(temp)
+
+    @property
+    def state(self):
+        v = C.c_uint64()
+        check(load().prana_sampler_state(self.h, C.byref(v)))
+        return v.value
+
+    def next_f32(self):
+        v = C.c_float()
+        check(load().prana_sampler_next_f32(self.h, C.byref(v)))
+        return v.value
+
+    def sample(self, logits):
+        init()
+        x = DeviceArray.from_host(np.ascontiguousarray(logits, np.float32))
+        t = C.c_uint32()
+        check(load().prana_sampler_sample(self.h, x.ptr, int(np.prod(x.shape)), C.byref(t), None))
+        return t.value
+
+    def generate(self, model, prompt, steps, stops=()):
+        prompt = np.asarray(prompt, np.uint32)
+        stops = np.asarray(stops, np.uint32)
+        out = np.zeros(max(steps, 1), np.uint32)
+        n = C.c_size_t()
+        st = GenStats()
+        check(load().prana_generate_sampled(model.h, _ptr(prompt), len(prompt), steps,
+                                            _ptr(stops) if len(stops) else None, len(stops), self.h, _ptr(out),
+                                            C.byref(n), C.byref(st)))
+        return out[: n.value].copy(), st
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_sampler_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def sample_pick(probs, r):
+    """The bucket walk (sampler.rs:29-36) over probs on the device for a given r."""
+    p = DeviceArray.from_host(np.ascontiguousarray(probs, np.float32))
+    o = DeviceArray((1,), np.uint32)
+    check(load().prana_sample_pick(p.ptr, int(np.prod(p.shape)), r, o.ptr, None))
+    return int(o.to_host()[0])
+
+
 class GraphError(PranaError):
     """GraphError (prana-graph lib.rs:55-63): kind is "UnsetInput",
     "ShapeMismatch" or "NotF32"; node is the unset input or the failing node."""

@@ -132,6 +132,15 @@ _SIGS = {
     "prana_gguf_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
     "prana_model_load_gguf": (c_int, [c_void_p, c_int, C.POINTER(c_void_p)]),
     "prana_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
+    # sampler
+    "prana_sampler_create": (c_int, [c_float, c_u64, C.POINTER(c_void_p)]),
+    "prana_sampler_destroy": (c_int, [c_void_p]),
+    "prana_sampler_state": (c_int, [c_void_p, c_u64p]),
+    "prana_sampler_next_f32": (c_int, [c_void_p, C.POINTER(c_float)]),
+    "prana_sampler_sample": (c_int, [c_void_p, c_void_p, c_size, C.POINTER(C.c_uint32), c_void_p]),
+    "prana_sample_pick": (c_int, [c_void_p, c_size, c_float, c_void_p, c_void_p]),
+    "prana_generate_sampled": (c_int, [c_void_p, c_void_p, c_size, c_size, c_void_p, c_size, c_void_p, c_void_p,
+                                       C.POINTER(c_size), C.POINTER(GenStats)]),
     # graph
     "prana_graph_create": (c_int, [C.POINTER(c_void_p)]),
     "prana_graph_destroy": (c_int, [c_void_p]),

@@ -852,6 +852,86 @@ int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t* out) {
   });
 }
 
+// ------------------------------------------------------------------ sampler
+}  // extern "C"
+
+struct prana_sampler {
+  float temp = 0.0f;
+  uint64_t state = 1;
+  DevBuf work;  // scaled logits, probabilities, the token
+};
+
+extern "C" {
+
+int prana_sampler_create(float temp, uint64_t seed, prana_sampler_t* out) {
+  return guard([&] {
+    PRANA_CHECK(out, "null argument");
+    auto* h = new prana_sampler();
+    h->temp = temp;
+    h->state = xorshift_seed(seed);
+    *out = h;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_sampler_destroy(prana_sampler_t h) {
+  return guard([&] {
+    delete h;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_sampler_state(prana_sampler_t h, uint64_t* state) {
+  return guard([&] {
+    PRANA_CHECK(h && state, "null argument");
+    *state = h->state;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_sampler_next_f32(prana_sampler_t h, float* out) {
+  return guard([&] {
+    PRANA_CHECK(h && out, "null argument");
+    *out = xorshift_next_f32(&h->state);
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_sampler_sample(prana_sampler_t h, const float* logits, size_t n, uint32_t* token, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(h && logits && token && n > 0, "bad argument");
+    hipStream_t s = pick_stream(stream);
+    if (int rc = h->work.ensure((2 * n + 1) * 4)) return rc;
+    float* scaled = h->work.as<float>();
+    uint32_t* dtok = reinterpret_cast<uint32_t*>(scaled + 2 * n);
+    const float r = h->temp <= 0.0f ? 0.0f : xorshift_next_f32(&h->state);
+    if (int rc = launch_sample(logits, n, h->temp, nullptr, 0, r, scaled, scaled + n, dtok, s)) return rc;
+    PRANA_HIP(hipMemcpyAsync(token, dtok, 4, hipMemcpyDeviceToHost, s));
+    PRANA_HIP(hipStreamSynchronize(s));
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_sample_pick(const float* probs, size_t n, float r, uint32_t* out, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(probs && out, "null argument");
+    return launch_sample_pick(probs, n, nullptr, 0, r, out, pick_stream(stream));
+  });
+}
+
+int prana_generate_sampled(prana_model_t m, const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops,
+                           size_t n_stops, prana_sampler_t sampler, uint32_t* out, size_t* n_out,
+                           prana_gen_stats* stats) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(m && prompt && sampler && (out || steps == 0), "bad argument");
+    PRANA_CHECK(m->m.finalized, "model not finalized");
+    return m->m.generate_sampled(prompt, p, steps, stops, n_stops, sampler->temp, &sampler->state, out, n_out, stats);
+  });
+}
+
 // ------------------------------------------------------------------ graph (prana-graph over device buffers)
 int prana_graph_create(prana_graph_t* out) {
   return guard([&] {

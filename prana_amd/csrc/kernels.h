@@ -54,6 +54,29 @@ int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStr
 // state = {pos, 0}, ids[0] = token, tok0[0] = token (each pointer optional).
 int launch_decode_seed(int* state, int pos, uint32_t token, uint32_t* ids, uint32_t* tok0, hipStream_t s);
 
+// ---- sampler.hip
+// Sampler::sample's bucket walk (sampler.rs:29-36) over device probabilities:
+// the first i with (r -= p[i]) <= 0, else n - 1; r from rs[r_index] when rs
+// is non-null, else r_host. One 1024-lane workgroup, exact f32 order.
+int launch_sample_pick(const float* probs, size_t n, const float* rs, int r_index, float r_host, uint32_t* out,
+                       hipStream_t s);
+// Sampler::sample (sampler.rs:22-39): argmax for temp <= 0, else logits /
+// temp -> scaled, softmax -> probs (n floats each), the walk -> out[0].
+int launch_sample(const float* logits, size_t n, float temp, const float* rs, int r_index, float r_host,
+                  float* scaled, float* probs, uint32_t* out, hipStream_t s);
+
+// XorShift (sampler.rs:51-71): xorshift64* (12, 25, 27, 0x2545F4914F6CDD1D),
+// next_f32 = top 24 bits / 2^24; a seed of 0 becomes 1.
+inline uint64_t xorshift_seed(uint64_t seed) { return seed ? seed : 1; }
+inline float xorshift_next_f32(uint64_t* state) {
+  uint64_t x = *state;
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  *state = x;
+  return static_cast<float>((x * 0x2545F4914F6CDD1DULL) >> 40) / static_cast<float>(1ULL << 24);
+}
+
 // ---- gemv.hip
 // Optional dispatch timestamps for the next decode GEMV launch on this
 // thread: when set, the launch records start/stop into these events as part

@@ -712,6 +712,89 @@ int Model::generate(const uint32_t* prompt, size_t p, size_t steps, const uint32
   return kOk;
 }
 
+// generate (infer.rs:696-771) with Sampler::sample for the sampled
+// positions. The steps at positions p-1 .. max_pos-2 run in chunks: the
+// chunk's uniform draws are taken on the host (in the reference's order, one
+// per step) and uploaded, every step samples on the device into the token
+// stream the next step embeds, and the chunk comes back once. Draws of steps
+// after a stop token are given back, so *rng ends where the reference's does.
+int Model::generate_sampled(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
+                            float temp, uint64_t* rng, uint32_t* out, size_t* n_out, prana_gen_stats* st) {
+  if (temp <= 0.0f) return generate(prompt, p, steps, stops, n_stops, out, n_out, st);  // greedy: no draws
+  PRANA_CHECK(p > 0, "prompt encoded to zero tokens");
+  PRANA_CHECK(rng, "sampler state missing");
+  hipStream_t s = ctx().stream;
+  const size_t max_pos = std::min(c.seq_len, p + steps);
+  Cache cache;
+  int rc = cache.create(*this, max_pos);
+  if (rc) return rc;
+  if ((rc = check_tokens(prompt, p))) return rc;
+  const double t0 = now_s();
+  if (p > 1 && p <= max_pos && (rc = prefill(cache, prompt, p - 1))) return rc;
+  const double t1 = now_s();
+  size_t generated = 0;
+  // with p > max_pos every position is teacher-forced and nothing is sampled
+  if (p <= max_pos && max_pos > p) {
+    constexpr size_t kChunk = 16;
+    const size_t V = c.vocab_size;
+    if ((rc = ensure_ws(1, cache.len, false))) return rc;
+    if ((rc = ws.sampling.ensure((2 * V + kChunk) * 4))) return rc;
+    if ((rc = ws.stream_out.ensure(std::max<size_t>((kChunk + 1) * 4, kStreamFloorIds * 4)))) return rc;
+    float* scaled = ws.sampling.as<float>();
+    float* probs = scaled + V;
+    float* draws_dev = probs + V;
+    uint32_t* ids = ws.stream_out.as<uint32_t>();
+    const size_t total = max_pos - p;
+    size_t pos = p - 1, done = 0;
+    uint32_t token = prompt[p - 1];
+    float draws[kChunk];
+    uint32_t got[kChunk];
+    while (done < total) {
+      const size_t n = std::min(kChunk, total - done);
+      const uint64_t state0 = *rng;
+      for (size_t j = 0; j < n; j++) draws[j] = xorshift_next_f32(rng);
+      PRANA_HIP(hipMemcpyAsync(draws_dev, draws, n * 4, hipMemcpyHostToDevice, s));
+      if ((rc = launch_decode_seed(nullptr, 0, token, ids, nullptr, s))) return rc;
+      for (size_t j = 0; j < n; j++) {
+        if ((rc = forward_dev(cache, nullptr, ids + j, pos + j, true, s))) return rc;
+        if ((rc = launch_sample(ws.logits.as<float>(), V, temp, draws_dev, static_cast<int>(j), 0.0f, scaled, probs,
+                                ids + j + 1, s)))
+          return rc;
+      }
+      PRANA_HIP(hipMemcpyAsync(got, ids + 1, n * 4, hipMemcpyDeviceToHost, s));
+      PRANA_HIP(hipStreamSynchronize(s));
+      size_t keep = n;
+      for (size_t j = 0; j < n; j++)
+        if (is_stop(got[j], stops, n_stops)) {
+          keep = j;
+          break;
+        }
+      for (size_t j = 0; j < keep; j++) out[generated + j] = got[j];
+      generated += keep;
+      if (keep < n) {  // the stop token's draw was the last one the reference takes
+        *rng = state0;
+        for (size_t j = 0; j <= keep; j++) (void)xorshift_next_f32(rng);
+        break;
+      }
+      token = got[n - 1];
+      pos += n;
+      done += n;
+    }
+  }
+  PRANA_HIP(hipStreamSynchronize(s));
+  const double t2 = now_s();
+  if (n_out) *n_out = generated;
+  if (st) {
+    st->prompt_tokens = p;
+    st->generated_tokens = generated;
+    st->proposed = st->accepted = 0;
+    st->seconds = t2 - t0;
+    st->prefill_seconds = t1 - t0;
+    st->decode_seconds = t2 - t1;
+  }
+  return kOk;
+}
+
 // generate_speculative (infer.rs:581-690), greedy.
 int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, size_t p, size_t steps, size_t k,
                          const uint32_t* stops, size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* st) {

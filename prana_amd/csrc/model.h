@@ -41,6 +41,7 @@ struct Workspace {
   DevBuf tokens, argmax;
   DevBuf stream_out;  // device-side token stream of decode()
   DevBuf step_state;  // {position, step} of a replayed decode step
+  DevBuf sampling;    // scaled logits, probabilities and uniform draws of sampled steps
   size_t gen = 0;     // bumped whenever a buffer above moves
 };
 
@@ -142,6 +143,10 @@ struct Model {
   int forward_batch(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0, float* logits_host);
   int generate(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
                uint32_t* out, size_t* n_out, prana_gen_stats* st);
+  // generate with a temperature Sampler (sampler.rs): *rng is its xorshift
+  // state and advances by one draw per sampled position, as the reference's.
+  int generate_sampled(const uint32_t* prompt, size_t p, size_t steps, const uint32_t* stops, size_t n_stops,
+                       float temp, uint64_t* rng, uint32_t* out, size_t* n_out, prana_gen_stats* st);
 };
 
 int check_config(const prana_config& c);
