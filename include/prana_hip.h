@@ -326,6 +326,42 @@ int prana_model_load_gguf(prana_gguf_t g, int precision, prana_model_t *out);
 /* The configuration a model was created or loaded with. */
 int prana_model_config(prana_model_t m, prana_config *cfg);
 
+/* ---------------------------------------------------------------- tokenizers
+ * prana-model's tokenizers (tokenizer.rs, bpe.rs), host only: SentencePiece
+ * (greedy highest-score merges over per-code-point seeds with <0xNN> byte
+ * fallback) and GPT-2 byte-level BPE (ranked merges over the byte-unicode
+ * alphabet, the reference's approximate pre-tokenizer, verbatim special
+ * tokens). Text is UTF-8 bytes (invalid UTF-8 is PRANA_ERR_INVALID); id and
+ * byte outputs are caller-sized (PRANA_ERR_SHORT_BUFFER gives the size). */
+typedef struct prana_tokenizer *prana_tokenizer_t;
+
+/* load_tokenizer (gguf.rs:466-537): tokenizer.ggml.model "llama" (default)
+ * or "gpt2", tokens (U+2581 read as a space for llama), scores / merges /
+ * token_type, bos_token_id / eos_token_id (llama defaults 1 / 2), and
+ * add_bos_token (default: llama yes, gpt2 no). */
+int prana_tokenizer_from_gguf(prana_gguf_t g, prana_tokenizer_t *out);
+/* Tokenizer::from_bytes (tokenizer.rs:65-82): llama2.c's tokenizer.bin. */
+int prana_tokenizer_from_llama2c(const void *data, size_t nbytes, size_t vocab_size, prana_tokenizer_t *out);
+int prana_tokenizer_destroy(prana_tokenizer_t t);
+/* kind: 0 SentencePiece, 1 byte-level BPE. */
+int prana_tokenizer_info(prana_tokenizer_t t, int *kind, size_t *vocab_size);
+/* Tokenizer::encode (tokenizer.rs:89-143), SentencePiece only. */
+int prana_tokenizer_encode(prana_tokenizer_t t, const char *text, size_t len, int bos, int eos, uint32_t *ids,
+                           size_t cap, size_t *n);
+/* Tokenize::encode_prompt (tokenizer.rs:19-26; bpe.rs:173-206). */
+int prana_tokenizer_encode_prompt(prana_tokenizer_t t, const char *text, size_t len, uint32_t *ids, size_t cap,
+                                  size_t *n);
+/* Tokenize::decode (tokenizer.rs:147-162; bpe.rs:208-213): the bytes of one
+ * token given the previous one. */
+int prana_tokenizer_decode(prana_tokenizer_t t, uint32_t prev, uint32_t token, char *buf, size_t cap, size_t *len);
+/* Tokenize::is_stop: EOS or BOS. */
+int prana_tokenizer_is_stop(prana_tokenizer_t t, uint32_t token, int *stop);
+/* The ids is_stop accepts, for the stops argument of prana_generate*. */
+int prana_tokenizer_stop_ids(prana_tokenizer_t t, uint32_t *ids, size_t cap, size_t *n);
+/* BpeTokenizer::pre_tokenize (bpe.rs:96-139): piece i is bytes
+ * [bounds[2i], bounds[2i+1]) of text; cap counts size_t slots. */
+int prana_bpe_pre_tokenize(const char *text, size_t len, size_t *bounds, size_t cap, size_t *n);
+
 /* ---------------------------------------------------------------- sampler
  * Sampler (prana-model sampler.rs:6-71): greedy for temp <= 0, else
  * temperature sampling driven by a seeded xorshift64* stream. Sampling runs

@@ -523,6 +523,115 @@ def load_gguf(source, precision="f32"):
     return m
 
 
+class Tokenizer:
+    """prana-model's tokenizers (tokenizer.rs SentencePiece, bpe.rs byte-level
+    BPE) in the library, host side. Build with from_gguf / from_llama2c."""
+
+    def __init__(self, handle):
+        self.h = handle
+        k, n = C.c_int(), C.c_size_t()
+        check(load().prana_tokenizer_info(self.h, C.byref(k), C.byref(n)))
+        self.kind, self.vocab_size = ("spm", "bpe")[k.value], n.value
+
+    @classmethod
+    def from_gguf(cls, g):
+        h = C.c_void_p()
+        check(load().prana_tokenizer_from_gguf(g.h, C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_llama2c(cls, data, vocab_size):
+        buf = np.frombuffer(bytes(data), np.uint8)
+        h = C.c_void_p()
+        check(load().prana_tokenizer_from_llama2c(_ptr(buf) if buf.size else None, buf.size, vocab_size, C.byref(h)))
+        return cls(h)
+
+    @staticmethod
+    def _text(text):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        return C.create_string_buffer(b, len(b) + 1), len(b)
+
+    def _ids(self, call):
+        n = C.c_size_t()
+        rc = call(None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        out = (C.c_uint32 * max(n.value, 1))()
+        check(call(out, n.value, C.byref(n)))
+        return [out[i] for i in range(n.value)]
+
+    def encode(self, text, bos, eos):
+        b, n = self._text(text)
+        return self._ids(lambda o, c, k: load().prana_tokenizer_encode(self.h, b, n, int(bos), int(eos), o, c, k))
+
+    def encode_prompt(self, text):
+        b, n = self._text(text)
+        return self._ids(lambda o, c, k: load().prana_tokenizer_encode_prompt(self.h, b, n, o, c, k))
+
+    def decode(self, prev, token):
+        n = C.c_size_t()
+        rc = load().prana_tokenizer_decode(self.h, prev, token, None, 0, C.byref(n))
+        if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+            check(rc)
+        buf = C.create_string_buffer(max(n.value, 1))
+        check(load().prana_tokenizer_decode(self.h, prev, token, buf, n.value, C.byref(n)))
+        return buf.raw[: n.value]
+
+    def is_stop(self, token):
+        v = C.c_int()
+        check(load().prana_tokenizer_is_stop(self.h, token, C.byref(v)))
+        return bool(v.value)
+
+    def stop_ids(self):
+        return self._ids(lambda o, c, k: load().prana_tokenizer_stop_ids(self.h, o, c, k))
+
+    def __del__(self):
+        try:
+            if getattr(self, "h", None) is not None:
+                load().prana_tokenizer_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def bpe_pre_tokenize(text):
+    """BpeTokenizer::pre_tokenize (bpe.rs:96-139) as a list of strings."""
+    b = text.encode()
+    buf = C.create_string_buffer(b, len(b) + 1)
+    n = C.c_size_t()
+    rc = load().prana_bpe_pre_tokenize(buf, len(b), None, 0, C.byref(n))
+    if rc != 0 and rc != _lib.ERR_SHORT_BUFFER:
+        check(rc)
+    bounds = (C.c_size_t * max(2 * n.value, 1))()
+    check(load().prana_bpe_pre_tokenize(buf, len(b), bounds, 2 * n.value, C.byref(n)))
+    return [b[bounds[2 * i]:bounds[2 * i + 1]].decode() for i in range(n.value)]
+
+
+def generate_text(model, tokenizer, prompt, steps, sampler=None):
+    """generate (infer.rs:696-771) from text: encode_prompt, decode with the
+    tokenizer's stop ids, pieces as the reference streams them: (bytes,
+    in_prompt) for every prompt transition and generated token."""
+    ids = tokenizer.encode_prompt(prompt)
+    if not ids:
+        raise ValueError("prompt encoded to zero tokens")
+    stops = tokenizer.stop_ids()
+    if sampler is None:
+        out, st = model.generate(ids, steps, stops)
+    else:
+        out, st = sampler.generate(model, ids, steps, stops)
+    max_pos = min(model.config["seq_len"], len(ids) + steps)
+    pieces = []
+    if 1 < len(ids) <= max_pos:
+        pieces += [(tokenizer.decode(a, b), True) for a, b in zip(ids[:-1], ids[1:])]
+    elif len(ids) > max_pos:  # all teacher-forced, one step at a time, up to the window
+        pieces += [(tokenizer.decode(ids[i], ids[i + 1]), True) for i in range(max_pos - 1)]
+    prev = ids[-1]
+    for t in out:
+        pieces.append((tokenizer.decode(prev, int(t)), False))
+        prev = int(t)
+    return pieces, st
+
+
 class Sampler:
     """Sampler (sampler.rs:6-71) on the device: greedy for temp <= 0, else
     temperature sampling with the xorshift64* stream of `seed`."""

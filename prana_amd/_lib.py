@@ -132,6 +132,17 @@ _SIGS = {
     "prana_gguf_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
     "prana_model_load_gguf": (c_int, [c_void_p, c_int, C.POINTER(c_void_p)]),
     "prana_model_config": (c_int, [c_void_p, C.POINTER(PranaConfig)]),
+    # tokenizers
+    "prana_tokenizer_from_gguf": (c_int, [c_void_p, C.POINTER(c_void_p)]),
+    "prana_tokenizer_from_llama2c": (c_int, [c_void_p, c_size, c_size, C.POINTER(c_void_p)]),
+    "prana_tokenizer_destroy": (c_int, [c_void_p]),
+    "prana_tokenizer_info": (c_int, [c_void_p, C.POINTER(c_int), C.POINTER(c_size)]),
+    "prana_tokenizer_encode": (c_int, [c_void_p, c_void_p, c_size, c_int, c_int, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_tokenizer_encode_prompt": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_tokenizer_decode": (c_int, [c_void_p, C.c_uint32, C.c_uint32, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_tokenizer_is_stop": (c_int, [c_void_p, C.c_uint32, C.POINTER(c_int)]),
+    "prana_tokenizer_stop_ids": (c_int, [c_void_p, c_void_p, c_size, C.POINTER(c_size)]),
+    "prana_bpe_pre_tokenize": (c_int, [c_void_p, c_size, c_void_p, c_size, C.POINTER(c_size)]),
     # sampler
     "prana_sampler_create": (c_int, [c_float, c_u64, C.POINTER(c_void_p)]),
     "prana_sampler_destroy": (c_int, [c_void_p]),

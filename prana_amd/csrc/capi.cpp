@@ -12,6 +12,7 @@
 #include "gguf.h"
 #include "graph.h"
 #include "model.h"
+#include "tokenizer.h"
 
 namespace prana {
 const char* last_error_cstr();
@@ -929,6 +930,124 @@ int prana_generate_sampled(prana_model_t m, const uint32_t* prompt, size_t p, si
     PRANA_CHECK(m && prompt && sampler && (out || steps == 0), "bad argument");
     PRANA_CHECK(m->m.finalized, "model not finalized");
     return m->m.generate_sampled(prompt, p, steps, stops, n_stops, sampler->temp, &sampler->state, out, n_out, stats);
+  });
+}
+
+// ------------------------------------------------------------------ tokenizers (host only)
+int prana_tokenizer_from_gguf(prana_gguf_t g, prana_tokenizer_t* out) {
+  return guard([&] {
+    PRANA_CHECK(g && out, "null argument");
+    *out = nullptr;
+    auto h = std::make_unique<prana_tokenizer>();
+    if (int rc = tokenizer_from_gguf(*g->g, h->t)) return rc;
+    *out = h.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_tokenizer_from_llama2c(const void* data, size_t nbytes, size_t vocab_size, prana_tokenizer_t* out) {
+  return guard([&] {
+    PRANA_CHECK((data || nbytes == 0) && out, "null argument");
+    *out = nullptr;
+    auto h = std::make_unique<prana_tokenizer>();
+    if (int rc = tokenizer_from_llama2c(static_cast<const uint8_t*>(data), nbytes, vocab_size, h->t)) return rc;
+    *out = h.release();
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_tokenizer_destroy(prana_tokenizer_t t) {
+  return guard([&] {
+    delete t;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_tokenizer_info(prana_tokenizer_t t, int* kind, size_t* vocab_size) {
+  return guard([&] {
+    PRANA_CHECK(t, "null tokenizer");
+    if (kind) *kind = t->t.kind;
+    if (vocab_size) *vocab_size = t->t.vocab_size();
+    return static_cast<int>(kOk);
+  });
+}
+
+static int ids_out(const std::vector<uint32_t>& ids, uint32_t* out, size_t cap, size_t* n) {
+  *n = ids.size();
+  if (!out || cap < ids.size())
+    return fail(kErrShortBuffer, "id buffer of " + std::to_string(cap) + "; " + std::to_string(ids.size()) + " needed");
+  std::copy(ids.begin(), ids.end(), out);
+  return kOk;
+}
+
+int prana_tokenizer_encode(prana_tokenizer_t t, const char* text, size_t len, int bos, int eos, uint32_t* ids,
+                           size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(t && (text || len == 0) && n, "null argument");
+    PRANA_CHECK(t->t.kind == 0, "encode with BOS/EOS flags is the SentencePiece tokenizer's (use encode_prompt)");
+    const std::string s(text ? text : "", len);
+    PRANA_CHECK(utf8_valid(s), "text is not valid UTF-8");
+    return ids_out(t->t.spm.encode(s, bos != 0, eos != 0), ids, cap, n);
+  });
+}
+
+int prana_tokenizer_encode_prompt(prana_tokenizer_t t, const char* text, size_t len, uint32_t* ids, size_t cap,
+                                  size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(t && (text || len == 0) && n, "null argument");
+    const std::string s(text ? text : "", len);
+    PRANA_CHECK(utf8_valid(s), "text is not valid UTF-8");
+    return ids_out(t->t.encode_prompt(s), ids, cap, n);
+  });
+}
+
+int prana_tokenizer_decode(prana_tokenizer_t t, uint32_t prev, uint32_t token, char* buf, size_t cap, size_t* len) {
+  return guard([&] {
+    PRANA_CHECK(t && len, "null argument");
+    const std::string b = t->t.decode(prev, token);
+    *len = b.size();
+    if (!buf || cap < b.size())
+      return fail(kErrShortBuffer, "byte buffer of " + std::to_string(cap) + "; " + std::to_string(b.size()) + " needed");
+    if (!b.empty()) std::memcpy(buf, b.data(), b.size());
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_tokenizer_is_stop(prana_tokenizer_t t, uint32_t token, int* stop) {
+  return guard([&] {
+    PRANA_CHECK(t && stop, "null argument");
+    *stop = t->t.is_stop(token) ? 1 : 0;
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_tokenizer_stop_ids(prana_tokenizer_t t, uint32_t* ids, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK(t && n, "null argument");
+    std::vector<uint32_t> v;
+    if (t->t.kind == 0) {
+      v = {t->t.spm.eos_id, t->t.spm.bos_id};
+    } else {
+      if (t->t.bpe.has_eos) v.push_back(t->t.bpe.eos_id);
+      if (t->t.bpe.has_bos) v.push_back(t->t.bpe.bos_id);
+    }
+    return ids_out(v, ids, cap, n);
+  });
+}
+
+int prana_bpe_pre_tokenize(const char* text, size_t len, size_t* bounds, size_t cap, size_t* n) {
+  return guard([&] {
+    PRANA_CHECK((text || len == 0) && n, "null argument");
+    const std::string s(text ? text : "", len);
+    PRANA_CHECK(utf8_valid(s), "text is not valid UTF-8");
+    const auto pieces = bpe_pre_tokenize(s);
+    *n = pieces.size();
+    if (!bounds || cap < 2 * pieces.size()) return fail(kErrShortBuffer, "bounds buffer too short");
+    for (size_t i = 0; i < pieces.size(); i++) {
+      bounds[2 * i] = pieces[i].first;
+      bounds[2 * i + 1] = pieces[i].second;
+    }
+    return static_cast<int>(kOk);
   });
 }
 

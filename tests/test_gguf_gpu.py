@@ -238,3 +238,30 @@ def test_missing_tensor_and_bad_precision():
             w.tensor(name, dims, 0, data.tobytes())
     with pytest.raises(P.PranaError, match="missing tensor 'blk.1.ffn_up.weight'"):
         P.load_gguf(w.to_bytes())
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.9])
+def test_text_in_text_out(temp):
+    # model and tokenizer from one file (gguf.rs:338-460), then generate from
+    # text (infer.rs:696-771): the token stream equals the oracle's for the
+    # same encoded prompt, stops are the tokenizer's, pieces decode it
+    b, tensors = W.reference_synthetic_model("qwen2", True, 16)
+    g = P.Gguf(data=b)
+    model, tok = P.load_gguf(g), P.Tokenizer.from_gguf(g)
+    prompt = "ab cab"
+    ids = tok.encode_prompt(prompt)
+    o = O.Model(synthetic_config("qwen2", 16), oracle_tensors(tensors, False))
+    sampler = P.Sampler(temp, 17) if temp > 0 else None
+    pieces, st = P.generate_text(model, tok, prompt, 8, sampler)
+    if temp > 0:
+        want = O.generate_sampled(o, ids, 8, O.Sampler(temp, 17), stops=tok.stop_ids())
+    else:
+        want, _ = o.generate(ids, 8, stops=tok.stop_ids())
+    gen = [p for p, in_prompt in pieces if not in_prompt]
+    assert len(gen) == st.generated_tokens == len(want)
+    prev = ids[-1]
+    for piece, t in zip(gen, want):
+        assert piece == tok.decode(prev, int(t))
+        prev = int(t)
+    assert b"".join(p for p, in_prompt in pieces if in_prompt) == b"".join(
+        tok.decode(a, c) for a, c in zip(ids[:-1], ids[1:]))
