@@ -1307,8 +1307,7 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   static const size_t lds_cap = [] {
     const size_t cap = max_dyn_lds() > 16384 ? max_dyn_lds() - 16384 : 0;  // static LDS of the sum
     if (cap > 65536)
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_split_softmax<true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap));
+      (void)set_max_dynamic_lds(reinterpret_cast<const void*>(attn_split_softmax<true>), static_cast<int>(cap));
     return cap;
   }();
   if (lds <= lds_cap)
@@ -1328,10 +1327,9 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
   // several query rows (verify): rows of one head slice share each V chunk,
   // one 128 KB workgroup per CU, when the device grants that much LDS
   constexpr size_t kPvrLds = 2 * kPvrQR * kPvrCH * 64 * sizeof(float);
-  static const bool pvr_ok = max_dyn_lds() >= kPvrLds &&
-                             hipFuncSetAttribute(reinterpret_cast<const void*>(attn_split_pv_rows<HD>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(kPvrLds)) == hipSuccess;
+  static const bool pvr_ok =
+      max_dyn_lds() >= kPvrLds &&
+      set_max_dynamic_lds(reinterpret_cast<const void*>(attn_split_pv_rows<HD>), static_cast<int>(kPvrLds));
   if (n_q >= 2 && pvr_ok)
     hipLaunchKernelGGL(attn_split_pv_rows<HD>, dim3(n_heads * (HD / 64), (n_q + kPvrQR - 1) / kPvrQR),
                        dim3(64 * kPvrQR + kPvrProd), kPvrLds, s, scratch, stride, v, (int)pos0, pos_dev, (int)n_q,

@@ -85,6 +85,26 @@ __device__ __forceinline__ void rotate(float& a, float& b, float2 cs) {
   b = x0 * cs.y + x1 * cs.x;
 }
 
+// ---------------------------------------------------------------- launch attributes
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize). A refusal returns false and
+// is cleared from HIP's last-error state, so that a later launch check does not
+// report it as a failed launch.
+inline bool set_max_dynamic_lds(const void* fn, int bytes) {
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess) return true;
+  (void)hipGetLastError();
+  return false;
+}
+
+// Static LDS bytes of a kernel (0 when the query fails).
+inline size_t static_lds_bytes(const void* fn) {
+  hipFuncAttributes a{};
+  if (hipFuncGetAttributes(&a, fn) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return a.sharedSizeBytes;
+}
+
 // ---------------------------------------------------------------- expf
 // The reference reaches expf through Rust's f32::exp -> glibc expf. glibc
 // (2.28+) computes it with the ARM optimized-routines algorithm: a 32-entry

@@ -685,7 +685,7 @@ __device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
   return group_seq_sum_short<NT, 1>(term, n);
 }
 
-constexpr int kPadSerialMax = 512;
+constexpr int kPadSerialMax = 896;
 template <int NT, bool PADDED, int CMAX = 16>
 __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {
   static_assert(NT % 64 == 0 && NT <= 1024, "whole waves");

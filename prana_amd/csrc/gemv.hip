@@ -750,10 +750,9 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || b <= 65536)
       return size_t{65536};
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, b) == hipSuccess
-               ? static_cast<size_t>(b)
-               : size_t{65536};
+    const void* fn = reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>);
+    const int dyn = b - static_cast<int>(static_lds_bytes(fn));
+    return dyn > 65536 && set_max_dynamic_lds(fn, dyn) ? static_cast<size_t>(dyn) : size_t{65536};
   }();
   size_t group = std::min<size_t>(kDecMaxTok, lds_cap / per_tok);
   group = std::min<size_t>(group, NT / rows_wg);  // one folder lane per (token, row)
@@ -1098,8 +1097,7 @@ int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const in
   using L = MmaLayout<KIND>;
   static const bool attr_ok = [] {
     return L::BYTES * 2 <= 65536 ||
-           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_mfma_kernel<KIND>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_mfma_kernel<KIND>), L::BYTES * 2);
   }();
   PRANA_CHECK(attr_ok, "gemm: LDS size not granted");
   dim3 grid((m.rows + kMmaRows - 1) / kMmaRows, (n_tok + kMmaToks - 1) / kMmaToks);
@@ -1302,8 +1300,7 @@ int launch_skinny_t(const DevMat& m, const int8_t* q, const float* sa, const int
   using L = SkLayout<KIND, RW, TT>;
   static const bool attr_ok = [] {
     return L::BYTES * 2 <= 65536 ||
-           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_skinny_kernel<KIND, RW, TT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_kernel<KIND, RW, TT>), L::BYTES * 2);
   }();
   PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
   hipLaunchKernelGGL((gemm_skinny_kernel<KIND, RW, TT>), dim3((m.rows + L::ROWS - 1) / L::ROWS), dim3(L::NT),
@@ -1552,8 +1549,7 @@ int launch_kq_t(const DevMat& m, const int8_t* q, const float* sa, const int* su
   using L = KqLayout<KIND, RW, TT>;
   static const bool attr_ok = [] {
     return L::BYTES * 2 <= 65536 ||
-           hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kq_kernel<KIND, RW, TT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, L::BYTES * 2) == hipSuccess;
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_kq_kernel<KIND, RW, TT>), L::BYTES * 2);
   }();
   PRANA_CHECK(attr_ok, "gemm_kq: LDS size not granted");
   hipLaunchKernelGGL((gemm_kq_kernel<KIND, RW, TT>),

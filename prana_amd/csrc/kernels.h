@@ -130,7 +130,8 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
                       size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr);
 // gate|up in one launch with the activation fused: h = act(gate) * up
 // (norms.rs:27-41, infer.rs:193-199), quantized for the down projection;
-// act 0 = silu, 1 = gelu_tanh. h (f32) is optional.
+// act 0 = silu, 1 = gelu_tanh. h (f32) is optional when tiles hold whole
+// 32-row blocks; otherwise h is required and a quantize_acts launch follows.
 int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t* q, const float* sa, const int* sums,
                     size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
 // The exact i32 part of every term (debug / bit-exactness entry point):

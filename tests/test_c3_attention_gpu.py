@@ -112,7 +112,7 @@ def test_exact_decode_eight_independent_caches_bitexact():
 
 
 # ------------------------------------------------------------------ adversarial rows around the one-lane fold limit
-@pytest.mark.parametrize("n", [33, 511, 512, 513])
+@pytest.mark.parametrize("n", [33, 511, 512, 513, 896, 897])
 @pytest.mark.parametrize("kind", ["ties", "spread", "nan_q", "inf_q"])
 def test_exact_decode_adversarial_near_fold_limit(n, kind):
     nh, nkv, hd = 8, 2, 64
