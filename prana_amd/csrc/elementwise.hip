@@ -466,6 +466,49 @@ int launch_decode_seed(int* state, int pos, uint32_t token, uint32_t* ids, uint3
   return kOk;
 }
 
+// The accept walk of one speculative round (infer.rs:648-681) on the device:
+// the target's tokens tnext[0..budget] are emitted while each agrees with the
+// draft's; a stop token ends the run unemitted, the step and position limits
+// end it after the token that reaches them. res = {emitted, accepted, done},
+// then the emitted tokens.
+__global__ void spec_accept_kernel(const uint32_t* __restrict__ drafts, const uint32_t* __restrict__ tnext,
+                                   int budget, const uint32_t* __restrict__ stops, int n_stops, long long generated,
+                                   long long steps, long long pos, long long max_pos, int* __restrict__ res) {
+  if (threadIdx.x != 0) return;
+  int n = 0, acc = 0, done = 0;
+  uint32_t* out = reinterpret_cast<uint32_t*>(res + 3);
+  for (int i = 0; i <= budget; i++) {
+    const uint32_t tn = tnext[i];
+    if (i < budget && tn == drafts[i]) acc++;
+    bool stop = false;
+    for (int j = 0; j < n_stops; j++) stop |= stops[j] == tn;
+    if (stop) {
+      done = 1;
+      break;
+    }
+    out[n++] = tn;
+    generated++;
+    pos++;
+    if (generated >= steps || pos + 1 >= max_pos) {
+      done = 1;
+      break;
+    }
+    if (i == budget || tn != drafts[i]) break;
+  }
+  res[0] = n;
+  res[1] = acc;
+  res[2] = done;
+}
+
+int launch_spec_accept(const uint32_t* drafts, const uint32_t* tnext, int budget, const uint32_t* stops, int n_stops,
+                       size_t generated, size_t steps, size_t pos, size_t max_pos, int* res, hipStream_t s) {
+  hipLaunchKernelGGL(spec_accept_kernel, dim3(1), dim3(64), 0, s, drafts, tnext, budget, stops, n_stops,
+                     static_cast<long long>(generated), static_cast<long long>(steps), static_cast<long long>(pos),
+                     static_cast<long long>(max_pos), res);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 // ---------------------------------------------------------------- embedding
 // Embedding::row (checkpoint.rs:169-174): dense copy, or one row of a packed
 // table dequantized (kquant.rs:39-112; Q8_0 tables are f32 rows q*d as

@@ -54,6 +54,11 @@ int launch_decode_advance(int* state, const uint32_t* tok, uint32_t* ids, hipStr
 // state = {pos, 0}, ids[0] = token, tok0[0] = token (each pointer optional).
 int launch_decode_seed(int* state, int pos, uint32_t token, uint32_t* ids, uint32_t* tok0, hipStream_t s);
 
+// One speculative round's accept walk (infer.rs:648-681): drafts[0..budget),
+// target argmaxes tnext[0..budget]; res = {emitted, accepted, done, tokens...}.
+int launch_spec_accept(const uint32_t* drafts, const uint32_t* tnext, int budget, const uint32_t* stops, int n_stops,
+                       size_t generated, size_t steps, size_t pos, size_t max_pos, int* res, hipStream_t s);
+
 // ---- sampler.hip
 // Sampler::sample's bucket walk (sampler.rs:29-36) over device probabilities:
 // the first i with (r -= p[i]) <= 0, else n - 1; r from rs[r_index] when rs

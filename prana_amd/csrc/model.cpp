@@ -434,6 +434,14 @@ int Model::step_graph_ready(Cache& cache, size_t pos, uint32_t* ids, hipStream_t
 
 int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out) {
   hipStream_t s = ctx().stream;
+  uint32_t* ids = nullptr;
+  if (int rc = decode_stream(cache, token, pos, n_steps, s, &ids)) return rc;
+  if (out && n_steps) PRANA_HIP(hipMemcpyAsync(out, ids + 1, n_steps * 4, hipMemcpyDeviceToHost, s));
+  PRANA_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int Model::decode_stream(Cache& cache, uint32_t token, size_t pos, size_t n_steps, hipStream_t s, uint32_t** out_ids) {
   PRANA_CHECK(pos + n_steps <= cache.len, "decode: positions beyond the cache length");
   PRANA_CHECK(cache.len <= 0x7fffffff, "decode: cache length out of range");
   int rc = ensure_ws(1, cache.len, false);
@@ -471,8 +479,7 @@ int Model::decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint
     if ((rc = forward_dev(cache, nullptr, ids + i, pos + i, true, s))) return rc;
     if ((rc = launch_argmax(ws.logits.as<float>(), 1, c.vocab_size, ids + i + 1, s))) return rc;
   }
-  if (out && n_steps) PRANA_HIP(hipMemcpyAsync(out, ids + 1, n_steps * 4, hipMemcpyDeviceToHost, s));
-  PRANA_HIP(hipStreamSynchronize(s));
+  *out_ids = ids;
   return kOk;
 }
 
@@ -600,6 +607,16 @@ int Model::batch_dev(Cache& cache, const uint32_t* tokens, size_t n, size_t pos0
   if ((rc = ensure_ws(n, cache.len, mode == 1))) return rc;
   PRANA_HIP(hipMemcpyAsync(ws.tokens.p, tokens, n * 4, hipMemcpyHostToDevice, s));
   if ((rc = embed_tokens(ws.tokens.as<uint32_t>(), n, s))) return rc;
+  return layers_pass(cache, n, pos0, mode, s);
+}
+
+int Model::batch_dev_ids(Cache& cache, const uint32_t* dev_tokens, size_t n, size_t pos0, int mode, hipStream_t s) {
+  PRANA_CHECK(finalized, "model not finalized");
+  PRANA_CHECK(n > 0, "empty token batch");
+  PRANA_CHECK(pos0 + n <= cache.len, "batch: positions beyond the cache length");
+  int rc = ensure_ws(n, cache.len, mode == 1);
+  if (rc) return rc;
+  if ((rc = embed_tokens(dev_tokens, n, s))) return rc;
   return layers_pass(cache, n, pos0, mode, s);
 }
 
@@ -817,37 +834,38 @@ int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, si
   double t1 = now_s();
   size_t pos = p - 1, generated = 0, proposed = 0, accepted = 0;
   uint32_t last = prompt[p - 1];
-  std::vector<uint32_t> drafts(k), inputs(k + 1), tnext(k + 1);
+  // Rounds stay on the device: the draft's greedy steps write [last, drafts]
+  // to its token stream, the target verifies that stream in place, and the
+  // accept walk runs on the device; the host reads back once per round the
+  // emitted tokens and the counts, which set the next round's positions.
+  DevBuf stops_dev, round;
+  if ((rc = stops_dev.alloc(std::max<size_t>(n_stops, 1) * 4))) return rc;
+  if (n_stops) PRANA_HIP(hipMemcpy(stops_dev.p, stops, n_stops * 4, hipMemcpyHostToDevice));
+  if ((rc = round.alloc((k + 4) * 4))) return rc;
+  std::vector<int> res(k + 4);
   bool done = false;
   while (!done && pos + 1 < max_pos) {
-    size_t budget = std::min(max_pos - 1 - pos, k);
-    // the draft's greedy steps from `last` at pos (one host round trip)
-    if ((rc = draft.decode(dc, last, pos, budget, drafts.data()))) return rc;
+    const size_t budget = std::min(max_pos - 1 - pos, k);
+    uint32_t* ids = nullptr;
+    if ((rc = draft.decode_stream(dc, last, pos, budget, s, &ids))) return rc;
     proposed += budget;
-    inputs[0] = last;
-    for (size_t j = 0; j < budget; j++) inputs[j + 1] = drafts[j];
-    if ((rc = target.batch_dev(tc, inputs.data(), budget + 1, pos, 2, s))) return rc;
+    if ((rc = target.batch_dev_ids(tc, ids, budget + 1, pos, 2, s))) return rc;
     if ((rc = target.logits_pass(budget + 1, s))) return rc;
-    if ((rc = launch_argmax(target.ws.logits.as<float>(), budget + 1, V, target.ws.argmax.as<uint32_t>(), s)))
+    uint32_t* tnext = target.ws.argmax.as<uint32_t>();
+    if ((rc = launch_argmax(target.ws.logits.as<float>(), budget + 1, V, tnext, s))) return rc;
+    if ((rc = launch_spec_accept(ids + 1, tnext, static_cast<int>(budget), stops_dev.as<uint32_t>(),
+                                 static_cast<int>(n_stops), generated, steps, pos, max_pos, round.as<int>(), s)))
       return rc;
-    PRANA_HIP(hipMemcpyAsync(tnext.data(), target.ws.argmax.p, (budget + 1) * 4, hipMemcpyDeviceToHost, s));
+    PRANA_HIP(hipMemcpyAsync(res.data(), round.p, (budget + 4) * 4, hipMemcpyDeviceToHost, s));
     PRANA_HIP(hipStreamSynchronize(s));
-    for (size_t i = 0; i <= budget; i++) {
-      uint32_t tn = tnext[i];
-      if (i < budget && tn == drafts[i]) accepted++;
-      if (is_stop(tn, stops, n_stops)) {
-        done = true;
-        break;
-      }
-      out[generated++] = tn;
-      pos += 1;
-      last = tn;
-      if (generated >= steps || pos + 1 >= max_pos) {
-        done = true;
-        break;
-      }
-      if (i == budget || tn != drafts[i]) break;
-    }
+    const size_t n_emit = static_cast<size_t>(res[0]);
+    const uint32_t* toks = reinterpret_cast<const uint32_t*>(res.data() + 3);
+    for (size_t i = 0; i < n_emit; i++) out[generated + i] = toks[i];
+    generated += n_emit;
+    pos += n_emit;
+    accepted += static_cast<size_t>(res[1]);
+    if (n_emit) last = toks[n_emit - 1];
+    done = res[2] != 0;
   }
   double t2 = now_s();
   if (n_out) *n_out = generated;

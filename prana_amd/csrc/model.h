@@ -136,6 +136,11 @@ struct Model {
 
   int forward(Cache& cache, uint32_t token, size_t pos, bool need_logits, float* logits_host);
   int decode(Cache& cache, uint32_t token, size_t pos, size_t n_steps, uint32_t* out);
+  // decode's steps, queued on s: ids[0] = token, ids[1..n_steps] the greedy
+  // stream (device memory, *ids); nothing is copied back or awaited.
+  int decode_stream(Cache& cache, uint32_t token, size_t pos, size_t n_steps, hipStream_t s, uint32_t** ids);
+  // batch_dev over token ids already in device memory (argmax outputs).
+  int batch_dev_ids(Cache& cache, const uint32_t* dev_tokens, size_t n, size_t pos0, int mode, hipStream_t s);
   // Capture (or reuse) the replayable decode step for the attention path of
   // position pos, writing its tokens to ids.
   int step_graph_ready(Cache& cache, size_t pos, uint32_t* ids, hipStream_t s, hipGraphExec_t* exec);

@@ -76,6 +76,31 @@ def test_tiny_speculative_equals_greedy_and_oracle(draft_arch):
     assert list(spec)[: len(plain)] == list(plain)[: len(spec)]
 
 
+def test_tiny_speculative_limits_and_stops():
+    # The device accept walk against the oracle's host loop (infer.rs:648-681):
+    # step limits inside and at the end of a round, the 16-position window
+    # cutting a round's budget, and a stop token at each place in the stream.
+    cfg, t = fx.synthetic_model("qwen2", True)
+    dcfg, dt = fx.synthetic_model("llama", False)
+    g, o = pair(cfg, t)
+    gd, od = pair(dcfg, dt)
+    prompt = [5, 7, 9]
+    plain, _ = o.generate(prompt, 20)
+    for k in (1, 2, 3, 5, 16):
+        for steps in (1, 2, 5, 13, 20):
+            spec, st = P.generate_speculative(g, gd, prompt, steps, k)
+            spec_o, st_o = O.generate_speculative(o, od, prompt, steps, k)
+            assert list(spec) == list(spec_o), (k, steps)
+            assert (st.proposed, st.accepted, st.generated_tokens) == (st_o.proposed, st_o.accepted,
+                                                                       st_o.generated_tokens), (k, steps)
+        for i in range(0, len(plain), 3):
+            stops = (int(plain[i]),)
+            spec, st = P.generate_speculative(g, gd, prompt, 20, k, stops)
+            spec_o, st_o = O.generate_speculative(o, od, prompt, 20, k, stops)
+            assert list(spec) == list(spec_o), (k, stops)
+            assert (st.proposed, st.accepted) == (st_o.proposed, st_o.accepted), (k, stops)
+
+
 def test_long_window_split_attention_bitexact():
     # Decode and verify steps past 2048 cached rows run the split attention
     # path, whose PV launch also quantizes the output for the wo projection.
