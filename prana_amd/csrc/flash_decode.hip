@@ -12,7 +12,7 @@
 //            holds 8 dims of q for each of them, the G partial dots of a row
 //            are reduced over its hd/8 lanes with DPP, and the tile's max,
 //            sum of exp(s - max) and P.V accumulators are kept per head.
-//   combine: one workgroup per (query head, sequence):
+//   combine: one workgroup per (query head, sequence, 32 dims):
 //            M = max m_s, L = sum l_s exp(m_s - M),
 //            out = sum acc_s exp(m_s - M) / L, in parallel over splits.
 // Every K/V byte is read once, with all of a tile's loads in flight at once,
@@ -241,21 +241,45 @@ struct CombineArgs {
 };
 
 constexpr int kFcNT = 256;
+constexpr int kFcDims = 32;             // output dims per combine workgroup
+constexpr int kFcPG = kFcNT / kFcDims;  // split groups per dim
+constexpr int kFcBatch = 16;            // splits per lane whose loads are in flight together
 
-// One workgroup per (query head, sequence): the split maxima and weights
-// w_s = exp(m_s - M) in parallel over splits, then every dim's weighted sum
-// with the splits divided over kFcNT / HD lane groups (independent loads).
-template <int HD>
-__global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c) {
-  constexpr int PG = kFcNT / HD;  // lane groups per dim
-  extern __shared__ float s_w[];  // max_splits weights
+// One workgroup per (query head, sequence, 32 output dims). Lane (g, d) takes
+// splits g, g+8, ...: a batch of their acc[d] and m values is loaded before
+// the maxima are known, so the kernel waits on memory about twice, not once
+// per split. M = max m_s; L = sum l_s exp(m_s - M);
+// out[d] = (sum_s acc_s[d] exp(m_s - M)) / L.
+__global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c, int hd) {
   __shared__ float s_r[kFcNT / 64];
-  __shared__ float s_o[PG][HD];
-  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* p = c.part + ((size_t)seq * c.n_heads + h) * c.max_splits * (HD + 2);
+  __shared__ float s_o[kFcPG][kFcDims];
+  const int h = blockIdx.x, seq = blockIdx.y, d0 = blockIdx.z * kFcDims;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int dl = tid % kFcDims, pg = tid / kFcDims;
+  const int rec = hd + 2;
+  const float* p = c.part + ((size_t)seq * c.n_heads + h) * c.max_splits * rec;
   const int ns = c.n_splits[seq];
-  float M = -INFINITY;
-  for (int sp = tid; sp < ns; sp += kFcNT) M = fmaxf(M, p[(size_t)sp * (HD + 2) + HD]);
+  float av[kFcBatch], mv[kFcBatch];
+  auto load_batch = [&](int sp0) {
+#pragma unroll
+    for (int k = 0; k < kFcBatch; k++) {
+      const int sp = min(sp0 + k * kFcPG, ns - 1);
+      av[k] = p[(size_t)sp * rec + d0 + dl];
+      mv[k] = p[(size_t)sp * rec + hd];
+    }
+  };
+  load_batch(pg);
+  float M = -INFINITY, lm[4], ll[4];
+  for (int sp0 = tid; sp0 < ns; sp0 += 4 * kFcNT) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int sp = min(sp0 + k * kFcNT, ns - 1);
+      lm[k] = p[(size_t)sp * rec + hd];
+      ll[k] = p[(size_t)sp * rec + hd + 1];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) M = fmaxf(M, lm[k]);
+  }
   for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
   if (lane == 0) s_r[wave] = M;
   __syncthreads();
@@ -264,11 +288,18 @@ __global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c) {
   for (int w = 1; w < kFcNT / 64; w++) M = fmaxf(M, s_r[w]);
   __syncthreads();  // s_r is reused for L
   float L = 0.0f;
-  for (int sp = tid; sp < ns; sp += kFcNT) {
-    const float* ps = p + (size_t)sp * (HD + 2);
-    const float w = __expf(ps[HD] - M);
-    s_w[sp] = w;
-    L = fmaf(ps[HD + 1], w, L);
+  for (int sp0 = tid; sp0 < ns; sp0 += 4 * kFcNT) {
+    if (sp0 != tid || ns > 4 * kFcNT) {  // the first pass's values are still in registers otherwise
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int sp = min(sp0 + k * kFcNT, ns - 1);
+        lm[k] = p[(size_t)sp * rec + hd];
+        ll[k] = p[(size_t)sp * rec + hd + 1];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (sp0 + k * kFcNT < ns) L = fmaf(ll[k], __expf(lm[k] - M), L);
   }
   for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
   if (lane == 0) s_r[wave] = L;
@@ -276,25 +307,20 @@ __global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c) {
   L = 0.0f;
 #pragma unroll
   for (int w = 0; w < kFcNT / 64; w++) L += s_r[w];
-  const int d = tid % HD, pg = tid / HD;
   float o = 0.0f;
-  int sp = pg;
-  for (; sp + 3 * PG < ns; sp += 4 * PG) {  // four independent loads per step
-    const float a0 = p[(size_t)sp * (HD + 2) + d], a1 = p[(size_t)(sp + PG) * (HD + 2) + d];
-    const float a2 = p[(size_t)(sp + 2 * PG) * (HD + 2) + d], a3 = p[(size_t)(sp + 3 * PG) * (HD + 2) + d];
-    o = fmaf(a0, s_w[sp], o);
-    o = fmaf(a1, s_w[sp + PG], o);
-    o = fmaf(a2, s_w[sp + 2 * PG], o);
-    o = fmaf(a3, s_w[sp + 3 * PG], o);
+  for (int sp0 = pg; sp0 < ns; sp0 += kFcBatch * kFcPG) {
+    if (sp0 != pg) load_batch(sp0);
+#pragma unroll
+    for (int k = 0; k < kFcBatch; k++)
+      if (sp0 + k * kFcPG < ns) o = fmaf(av[k], __expf(mv[k] - M), o);
   }
-  for (; sp < ns; sp += PG) o = fmaf(p[(size_t)sp * (HD + 2) + d], s_w[sp], o);
-  s_o[pg][d] = o;
+  s_o[pg][dl] = o;
   __syncthreads();
-  if (tid < HD) {
+  if (tid < kFcDims) {
     float t = 0.0f;
 #pragma unroll
-    for (int g = 0; g < PG; g++) t += s_o[g][tid];
-    c.out[((size_t)seq * c.n_heads + h) * HD + tid] = t / L;
+    for (int g = 0; g < kFcPG; g++) t += s_o[g][tid];
+    c.out[((size_t)seq * c.n_heads + h) * hd + d0 + tid] = t / L;
   }
 }
 
@@ -303,7 +329,7 @@ int launch_flash_t(const FlashArgs& a, const CombineArgs& c, int n_seq, hipStrea
   hipLaunchKernelGGL((flash_split_kernel<HD, G, ITER>), dim3(a.max_splits, a.n_kv_heads, n_seq), dim3(kFdNT), 0, s,
                      a);
   PRANA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(flash_combine_kernel<HD>, dim3(a.n_heads, n_seq), dim3(kFcNT), (size_t)a.max_splits * 4, s, c);
+  hipLaunchKernelGGL(flash_combine_kernel, dim3(a.n_heads, n_seq, HD / kFcDims), dim3(kFcNT), 0, s, c, HD);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
