@@ -224,6 +224,24 @@ def run_models():
     return rows
 
 
+def run_spec(k, tokens):
+    """C4 speculative decode alone (for a kernel trace of its rounds): the C4
+    target and draft of run_models, a 512-token prefill, a warm-up call, then
+    one timed call of `tokens` tokens with k drafts per round."""
+    import prana_amd as P
+    from prana_amd import models as M
+
+    g = P.Model(M.C4, M.c4_tensors(seed=4))
+    dcfg = M.c4_draft_config()
+    draft = P.Model(dcfg, M.synth_tensors(dcfg, M.types_c0, 1))
+    prompt = np.random.default_rng(20261202).integers(0, M.C4["vocab_size"], 512).astype(np.uint32)
+    P.generate_speculative(g, draft, prompt[:64], 8, k)
+    _, st = P.generate_speculative(g, draft, prompt, tokens, k)
+    print(json.dumps({"config": "C4", "k": k, "generated_tokens": st.generated_tokens, "proposed": st.proposed,
+                      "accepted": st.accepted,
+                      "decode_tok_s": round(st.generated_tokens / st.decode_seconds, 1)}), flush=True)
+
+
 def models_table(rows):
     out = ["| config | case | prefill tok/s | decode tok/s | note |", "|---|---|---:|---:|---|"]
     for r in rows:
@@ -305,10 +323,14 @@ def main():
     ap.add_argument("--counters", metavar="DB", help="MFMA / VALU utilisation table of a --pmc run")
     ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
     ap.add_argument("--only", choices=["C1", "GEMM", "C3"], help="run one configuration's sweep")
+    ap.add_argument("--spec", type=int, metavar="K", help="C4 speculative decode alone, K drafts per round")
+    ap.add_argument("--tokens", type=int, default=48, help="tokens of the --spec call")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
     if args.models:
         print(models_table(run_models()))
+    elif args.spec:
+        run_spec(args.spec, args.tokens)
     elif args.counters:
         summarize_counters(args.counters)
     elif args.summarize:
