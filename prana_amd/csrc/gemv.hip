@@ -682,6 +682,167 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   }
 }
 
+// ---- verify batches: 2..8 tokens, 32-element formats
+// Chunk-major units: with W = nb / U blocks per chunk and ROWS = 256 / W rows
+// per tile (gate and up rows together in act mode), lane t's unit i is row
+// t / W, block i*W + t % W, so chunk i of every row of the tile is one unit
+// index. All weights are loaded at once, as in gemv_tile_kernel. The
+// activations of every token are staged in LDS one chunk at a time (two
+// chunk buffers; chunk c+2's loads are issued before chunk c's terms and
+// stored once chunk c's buffer is free) and so are the term rows, so a
+// workgroup holds two chunks of every token instead of whole rows per token
+// and several workgroups fit per CU. The folder lane of (token, row) adds
+// chunk c's W terms after chunk c-1's: the left-to-right block order of the
+// one-token kernel, so both give the same bits.
+constexpr int kKmNT = 256;
+constexpr int kKmQ4 = 4;  // int4 words of one chunk's activations per lane (8 tokens x 64 blocks x 2 / 256)
+constexpr int kKmSc = 2;  // (scale, sum) pairs of one chunk per lane (8 tokens x 64 blocks / 256)
+
+struct KmActs {
+  int4 q[kKmQ4];
+  float s[kKmSc];
+  int m[kKmSc];
+};
+
+template <int KIND, int U, bool ACT>
+__global__ __launch_bounds__(kKmNT) void gemv_km_kernel(DecodeJob job, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ sa,
+                                                        const int* __restrict__ sums, int n_tok) {
+  using R = RegUnit<KIND>;
+  static_assert(R::kElems == 32 && R::kTpu == 1, "32-element formats");
+  extern __shared__ int4 smem4[];
+  const int tid = threadIdx.x;
+  int mi = 0, tile = blockIdx.x;
+  if (!ACT) {
+    while (mi < job.n_mats - 1 && tile >= job.tiles[mi]) tile -= job.tiles[mi++];
+  }
+  const int rt = job.rt;
+  const int ROWS = ACT ? 2 * rt : rt;
+  const int K = static_cast<int>(job.m[0].cols), nb = K / 32;
+  const int W = job.sb;  // blocks per chunk: nb == U * W, ROWS * W == kKmNT
+  const size_t rows_m = job.m[mi].rows;
+  const size_t r0 = (size_t)tile * rt;
+  const int rows_here = static_cast<int>(min((size_t)rt, rows_m - r0));
+  const int lrow = tid / W, loff = tid % W;  // this lane's row in the tile and block in a chunk
+  const bool lup = ACT && lrow >= rt;
+  const int llr = lup ? lrow - rt : lrow;    // its row within its matrix
+  const bool lane_live = llr < rows_here;
+
+  const int CS = W * 40;  // bytes of one token's chunk: W*32 q, W*4 scales, W*4 sums
+  const int TW = W + 1;   // padded term row
+  uint8_t* sm8 = reinterpret_cast<uint8_t*>(smem4);
+  float* tbase = reinterpret_cast<float*>(sm8 + 2 * n_tok * CS);
+  const int G = nb;
+  auto load_acts = [&](KmActs& ar, int c) {
+    const int nq = n_tok * W * 2;
+#pragma unroll
+    for (int i = 0; i < kKmQ4; i++) {
+      const int w = tid + kKmNT * i;
+      if (w < nq) {
+        const int t = w / (2 * W), r = w % (2 * W);
+        ar.q[i] = reinterpret_cast<const int4*>(q + (size_t)t * K)[c * W * 2 + r];
+      }
+    }
+    const int ns = n_tok * W;
+#pragma unroll
+    for (int i = 0; i < kKmSc; i++) {
+      const int e = tid + kKmNT * i;
+      if (e < ns) {
+        const size_t gi = (size_t)(e / W) * G + c * W + e % W;
+        ar.s[i] = sa[gi];
+        ar.m[i] = sums[gi];
+      }
+    }
+  };
+  auto store_acts = [&](const KmActs& ar, int c) {
+    uint8_t* base = sm8 + (c & 1) * n_tok * CS;
+    const int nq = n_tok * W * 2;
+#pragma unroll
+    for (int i = 0; i < kKmQ4; i++) {
+      const int w = tid + kKmNT * i;
+      if (w < nq) reinterpret_cast<int4*>(base + (w / (2 * W)) * CS)[w % (2 * W)] = ar.q[i];
+    }
+    const int ns = n_tok * W;
+#pragma unroll
+    for (int i = 0; i < kKmSc; i++) {
+      const int e = tid + kKmNT * i;
+      if (e < ns) {
+        uint8_t* tb = base + (e / W) * CS;
+        reinterpret_cast<float*>(tb + W * 32)[e % W] = ar.s[i];
+        reinterpret_cast<int*>(tb + W * 36)[e % W] = ar.m[i];
+      }
+    }
+  };
+
+  // chunks 0 and 1 of the activations first (the oldest loads), then every
+  // weight unit of this lane
+  KmActs ar[2];
+  load_acts(ar[0], 0);
+  if (U > 1) load_acts(ar[1], 1);
+  R buf[U];
+  {
+    const uint8_t* qb = ACT ? (lup ? job.m[1].qs : job.m[0].qs) : job.m[mi].qs;
+    const uint8_t* sb = static_cast<const uint8_t*>(ACT ? (lup ? job.m[1].sc : job.m[0].sc) : job.m[mi].sc);
+    const size_t rr = r0 + min(llr, rows_here - 1);
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      const size_t ui = rr * nb + i * W + loff;
+      buf[i].load(qb + ui * R::kQB, sb + ui * R::kSB);
+    }
+  }
+  store_acts(ar[0], 0);
+  if (U > 1) store_acts(ar[1], 1);
+  __syncthreads();
+
+  const int fl_tok = tid / ROWS, fl_row = tid % ROWS;
+  const int fl_lr = ACT ? (fl_row >= rt ? fl_row - rt : fl_row) : fl_row;
+  const bool folder = tid < n_tok * ROWS && fl_lr < rows_here;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < U; c++) {
+    if (c + 2 < U) load_acts(ar[c & 1], c + 2);
+    float* tb = tbase + (c & 1) * n_tok * ROWS * TW;
+    if (lane_live) {
+      const uint8_t* abuf = sm8 + (c & 1) * n_tok * CS;
+      for (int t = 0; t < n_tok; t++) {
+        const uint8_t* ab = abuf + t * CS;
+        Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + W * 32),
+               reinterpret_cast<const int*>(ab + W * 36)};
+        buf[c].terms(a, loff, tb + (t * ROWS + lrow) * TW + loff);
+      }
+    }
+    __syncthreads();  // chunk c's terms are in LDS; its activation buffer is free
+    if (folder) {
+      const float* tr = tb + (fl_tok * ROWS + fl_row) * TW;
+      for (int i = 0; i < W; i++) acc += tr[i];
+    }
+    if (c + 2 < U) store_acts(ar[c & 1], c + 2);  // read by chunk c+2, after the next barrier
+  }
+
+  if (!ACT) {
+    if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
+    return;
+  }
+  // act epilogue: gate lanes (row < rt) pair with up lanes (row + rt) through
+  // LDS; h = act(g) * u goes out in f32 (tiles here hold fewer than 32 rows,
+  // so the caller quantizes h)
+  __syncthreads();  // every fold read of the term buffers is done
+  float* hx = tbase;
+  if (tid < n_tok * ROWS) hx[tid] = acc;
+  __syncthreads();
+  if (tid < n_tok * ROWS && fl_row < rt && fl_row < rows_here) {
+    float g = acc, u = hx[fl_tok * ROWS + rt + fl_row];
+    if (job.act == 2) {
+      const float kS = 0.7978846f;  // norms.rs:36
+      float x3 = g * g * g;
+      g = 0.5f * g * (1.0f + dev_tanhf(kS * (g + 0.044715f * x3)));
+    } else {
+      g = g * (1.0f / (1.0f + dev_expf(-g)));
+    }
+    job.h[fl_tok * rows_m + r0 + fl_row] = g * u;
+  }
+}
+
 // Tile geometry: units per lane per stage U, rows per matrix per tile rt,
 // units per row per stage sb and lanes nt, with rows(tile) * sb == nt * U.
 struct TileGeom {
@@ -786,11 +947,84 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   return kOk;
 }
 
+// Chunk width W (blocks) of the verify-batch kernel for nb blocks per row and
+// a batch of n_tok tokens, or 0 when it does not apply. W is 32 or 64 with
+// nb / W in {2, 4, 7, 14}; rows of up to 128 blocks take W = 32 (eight rows
+// per tile: half the workgroups of W = 64), longer rows W = 64 while two
+// chunks of every token (activations and term rows) stay within 40 KB of LDS.
+// Launches take as many tokens as kKmLdsBudget allows.
+inline size_t km_per_tok(int w) { return 2 * static_cast<size_t>(w) * 40 + 2 * (kKmNT / w) * (w + 1) * 4; }
+constexpr size_t kKmLdsBudget = 49152;  // per launch: three workgroups per CU
+inline int km_chunk(int nb, size_t n_tok) {
+  auto ok = [&](int w) {
+    const int u = nb / w;
+    return nb % w == 0 && (u == 2 || u == 4 || u == 7 || u == 14);
+  };
+  if (nb <= 128 && ok(32)) return 32;
+  if (ok(64) && n_tok * 64 <= 512 && n_tok * km_per_tok(64) <= 40960) return 64;
+  if (ok(32)) return 32;
+  return 0;
+}
+
+template <int KIND, int U, bool ACT>
+int launch_km_u(const DecodeJob& job0, int w, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                hipStream_t s) {
+  DecodeJob job = job0;
+  const int rows_wg = kKmNT / w;
+  job.rt = ACT ? rows_wg / 2 : rows_wg;
+  job.sb = w;
+  const size_t K = job.m[0].cols;
+  PRANA_CHECK(static_cast<int>(K / 32) == U * w, "gemv: verify-batch chunk geometry mismatch");
+  int total = 0;
+  for (int i = 0; i < (ACT ? 1 : job.n_mats); i++) {
+    job.tiles[i] = static_cast<int>((job.m[i].rows + job.rt - 1) / job.rt);
+    total += job.tiles[i];
+  }
+  const size_t per_tok = km_per_tok(w);
+  // one chunk's activations fit the lanes' registers (kKmQ4, kKmSc) for up to
+  // 512 / w tokens; one folder lane per (token, row)
+  const size_t group = std::min<size_t>({static_cast<size_t>(512 / w), static_cast<size_t>(kKmNT / rows_wg),
+                                         std::max<size_t>(1, kKmLdsBudget / per_tok)});
+  const size_t G = K / 32;
+  for (size_t t0 = 0; t0 < n_tok; t0 += group) {
+    const size_t nt = std::min<size_t>(group, n_tok - t0);
+    DecodeJob j = job;
+    for (int i = 0; i < 3; i++)
+      if (j.o[i].out) j.o[i].out += t0 * j.o[i].ldo;
+    if (ACT) j.h += t0 * j.m[0].rows;
+    hipLaunchKernelGGL((gemv_km_kernel<KIND, U, ACT>), dim3(total), dim3(kKmNT), nt * per_tok, s, j, q + t0 * K,
+                       sa + t0 * G, sums + t0 * G, (int)nt);
+    PRANA_LAUNCH_CHECK();
+  }
+  return kOk;
+}
+
+template <int KIND, bool ACT>
+int launch_km(const DecodeJob& job, int w, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+              hipStream_t s) {
+  switch (static_cast<int>(job.m[0].cols / 32) / w) {
+    case 2: return launch_km_u<KIND, 2, ACT>(job, w, q, sa, sums, n_tok, s);
+    case 4: return launch_km_u<KIND, 4, ACT>(job, w, q, sa, sums, n_tok, s);
+    case 7: return launch_km_u<KIND, 7, ACT>(job, w, q, sa, sums, n_tok, s);
+    case 14: return launch_km_u<KIND, 14, ACT>(job, w, q, sa, sums, n_tok, s);
+  }
+  return fail(kErrInvalid, "gemv: no verify-batch chunk geometry");
+}
+
 template <int KIND>
 int launch_decode_t(const DecodeJob& job, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                     hipStream_t s) {
   constexpr bool kSmall = RegUnit<KIND>::kElems == 32;
   const bool act = job.act != 0;
+  if constexpr (kSmall) {
+    // verify batches: the chunk-major kernel, where the act tiles would not
+    // quantize h themselves anyway (tiles of fewer than 32 rows per matrix)
+    const int w = n_tok >= 2 && !job.rk.table ? km_chunk(static_cast<int>(job.m[0].cols / 32), n_tok) : 0;
+    if (w > 0 && (!act || choose_geom<KIND>(job.m[0].cols, true).rt % 32 != 0) && (!act || job.h)) {
+      if (act) return launch_km<KIND, true>(job, w, q, sa, sums, n_tok, s);
+      return launch_km<KIND, false>(job, w, q, sa, sums, n_tok, s);
+    }
+  }
   const TileGeom g = choose_geom<KIND>(job.m[0].cols, act);
   const int nb = static_cast<int>(job.m[0].cols / RegUnit<KIND>::kElems);
   const bool staged = g.sb < nb;
@@ -1683,7 +1917,11 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s) {
   if (n_tok == 0 || m.rows == 0) return kOk;
-  if (gemv_skinny(m.kind, n_tok)) {
+  // batches of up to 16 tokens whose width the chunk-major multi-token kernel
+  // takes stay on the decode path (it beats the skinny matrix-core kernel on
+  // verify-sized batches)
+  const bool km = n_tok <= kDecodeMaxTokens && km_chunk(static_cast<int>(m.cols / 32), n_tok) > 0;
+  if (gemv_skinny(m.kind, n_tok) && !km) {
     switch (m.kind) {
       case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
       case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);

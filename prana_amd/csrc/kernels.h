@@ -105,8 +105,11 @@ struct GemvOut {
 constexpr size_t kGemvDecodeMaxTokens = 16;
 // launch_gemv over block-32 kinds (Q8F, Q8_0, Q4_0) takes batches of
 // kGemvSkinnyMinTokens..kGemvSkinnyMaxTokens tokens to the skinny
-// matrix-core kernel; smaller batches stay on the decode kernel, which also
-// keeps the fused Q|K|V and gate|up launches up to kGemvDecodeMaxTokens.
+// matrix-core kernel, except widths of 2, 4, 7 or 14 chunks of 32/64 blocks,
+// which keep batches of up to kGemvDecodeMaxTokens on the decode path's
+// chunk-major multi-token kernel; smaller batches stay on the decode kernels,
+// which also keep the fused Q|K|V and gate|up launches up to
+// kGemvDecodeMaxTokens.
 constexpr size_t kGemvSkinnyMinTokens = 9;
 constexpr size_t kGemvSkinnyMaxTokens = 64;
 inline bool gemv_skinny(int kind, size_t n_tok) {

@@ -105,6 +105,27 @@ def test_matmul_batched(ty, rows, cols, n_tok):
 
 
 @pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
+@pytest.mark.parametrize("rows,cols,n_tok", [(37, 2048, 2), (300, 4096, 5), (129, 7168, 8), (70, 14336, 3),
+                                             (70, 14336, 6), (4097, 4096, 7)])
+def test_matmul_verify_batch_chunked(ty, rows, cols, n_tok):
+    # 2..8 tokens over widths of 2, 4, 7 or 14 chunks of 32 or 64 blocks: the
+    # chunk-major multi-token kernel (activations and term rows staged one
+    # chunk at a time); ragged last tiles
+    raw, g, o = _mat_pair(ty, rows, cols, 60 + n_tok + cols, real=True)
+    a = rng(n_tok + 3).standard_normal((n_tok, cols)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+def test_matmul_verify_batch_chunked_q8_f32_scales():
+    w = rng(13).standard_normal((70, 4096)).astype(np.float32)
+    q, s = O.quantize_q8(w)
+    g, o = P.Matrix.q8_parts(q, s), O.Mat.q8_parts(q, s)
+    for n_tok in (2, 6):
+        a = rng(19 + n_tok).standard_normal((n_tok, 4096)).astype(np.float32)
+        assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
 @pytest.mark.parametrize("rows,cols,n_tok", [(150, 288, 100), (33, 1312, 97), (129, 96, 65)])
 def test_matmul_prefill_partial_chunks(ty, rows, cols, n_tok):
     # The staged prefill kernel takes blocks in chunks of four: 9, 41 and 3

@@ -243,6 +243,38 @@ def test_kquant_prefill_and_verify_batches_bitexact():
     assert same_bits(gc.forward_batch(batch, 40), oc.forward_batch(batch, 40))
 
 
+@pytest.mark.parametrize("ty", [P.Q4_0, P.Q8_0])
+def test_block32_verify_batches_bitexact(ty):
+    # Verify batches of 2..10 tokens over block-32 weights whose widths take
+    # the chunk-major multi-token kernel: Q|K|V (3 matrices, 2048 wide: 32-block
+    # chunks), gate|up with the activation (2048 wide) and down (4096 wide:
+    # four chunks), and the head; then a model whose down projection is 14336
+    # wide: seven 64-block chunks at five tokens, fourteen 32-block chunks at
+    # seven.
+    cfg = M.config(2048, 4096, 1, 16, 4, 700, 64, head_dim=128)
+    t = M.synth_tensors(cfg, lambda name, cols: ty, 11)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(64), o.cache(64)
+    prompt = np.random.default_rng(11).integers(0, cfg["vocab_size"], 60).astype(np.uint32)
+    gc.prefill(prompt[:20])
+    oc.prefill(prompt[:20])
+    pos = 20
+    for n in (2, 5, 8, 10):
+        batch = [int(x) for x in prompt[pos:pos + n]]
+        assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
+        pos += n
+    cfg = M.config(512, 14336, 1, 4, 2, 300, 32, head_dim=128)
+    t = M.synth_tensors(cfg, lambda name, cols: ty, 12)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(32), o.cache(32)
+    prompt = prompt % cfg["vocab_size"]
+    gc.prefill(prompt[:4])
+    oc.prefill(prompt[:4])
+    for n, pos in ((5, 4), (7, 9)):
+        batch = [int(x) for x in prompt[pos:pos + n]]
+        assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
+
+
 # ------------------------------------------------------------------ config 4: 7B shape, Q4_0
 @pytest.fixture(scope="module")
 def c4():
