@@ -308,6 +308,56 @@ __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k, con
   }
 }
 
+// The same for n consecutive token rows (q [n][q_dim], k and v [n][kv_dim])
+// at positions pos0..pos0+n-1: the batched passes' RoPE of q and k and their
+// f16 cache rows (infer.rs:247-262, 322-338) in one launch.
+__global__ void rope_kv_rows_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+                                    int n, int q_dim, int kv_dim, int hd, const float2* __restrict__ table, int neox,
+                                    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int pos0) {
+  const int half = hd / 2;
+  const int qp = q_dim / 2, kp = kv_dim / 2, per = qp + kp + kv_dim;
+  const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (gid >= (size_t)n * per) return;
+  const int t = static_cast<int>(gid / per), e = static_cast<int>(gid % per);
+  const int pos = pos0 + t;
+  if (e < qp + kp) {
+    float* row = e < qp ? q + (size_t)t * q_dim : k + (size_t)t * kv_dim;
+    const int p = e < qp ? e : e - qp;
+    int i0, i1, m;
+    if (neox) {
+      const int h = p / half, j = p % half;
+      i0 = h * hd + j;
+      i1 = i0 + half;
+      m = j;
+    } else {
+      i0 = 2 * p;
+      i1 = i0 + 1;
+      m = (i0 % hd) / 2;
+    }
+    float a = row[i0], b = row[i1];
+    rotate(a, b, table[(size_t)pos * half + m]);
+    row[i0] = a;
+    row[i1] = b;
+    if (e >= qp) {
+      kc[(size_t)pos * kv_dim + i0] = f32_to_f16(a);
+      kc[(size_t)pos * kv_dim + i1] = f32_to_f16(b);
+    }
+  } else {
+    const int i = e - qp - kp;
+    vc[(size_t)pos * kv_dim + i] = f32_to_f16(v[(size_t)t * kv_dim + i]);
+  }
+}
+
+int launch_rope_kv_rows(float* q, float* k, const float* v, size_t n, size_t q_dim, size_t kv_dim, size_t hd,
+                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t pos0, hipStream_t s) {
+  const size_t total = n * (q_dim / 2 + kv_dim / 2 + kv_dim);
+  if (total == 0) return kOk;
+  hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((total + 255) / 256), dim3(256), 0, s, q, k, v, (int)n, (int)q_dim,
+                     (int)kv_dim, (int)hd, table, neox, kc, vc, (int)pos0);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
                    int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s) {
   size_t n = q_dim / 2 + kv_dim / 2 + kv_dim;

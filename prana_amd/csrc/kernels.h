@@ -39,6 +39,10 @@ int launch_add(float* x, const float* y, size_t n, size_t period, hipStream_t s)
 int launch_rope(float* x, size_t n_rows, size_t row_len, size_t row_stride, size_t hd, const float2* table,
                 size_t pos0, int neox, hipStream_t s);
 int launch_kv_write(uint16_t* cache, size_t first_row, size_t kv_stride, const float* src, size_t n, hipStream_t s);
+// n token rows at positions pos0..pos0+n-1: RoPE of q and k in place, and
+// the f16 cache rows of k and v.
+int launch_rope_kv_rows(float* q, float* k, const float* v, size_t n, size_t q_dim, size_t kv_dim, size_t hd,
+                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t pos0, hipStream_t s);
 int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
                    int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s);
 int launch_f32_to_f16(const float* in, size_t n, uint16_t* out, hipStream_t s);

@@ -523,10 +523,9 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
                                        &quantized)))
         return rc;
     } else {
-      if ((rc = launch_rope(ws.q.as<float>(), n, q_dim, q_dim, hd, tab, pos0, c.rope_neox, s))) return rc;
-      if ((rc = launch_rope(ws.k.as<float>(), n, kv_dim, kv_dim, hd, tab, pos0, c.rope_neox, s))) return rc;
-      if ((rc = launch_kv_write(kc, pos0, kv_dim, ws.k.as<float>(), n * kv_dim, s))) return rc;
-      if ((rc = launch_kv_write(vc, pos0, kv_dim, ws.v.as<float>(), n * kv_dim, s))) return rc;
+      if ((rc = launch_rope_kv_rows(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, q_dim, kv_dim, hd, tab,
+                                    c.rope_neox, kc, vc, pos0, s)))
+        return rc;
       if (mode == 1)
         rc = launch_attention_prefill(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, c.n_heads,
                                       c.n_kv_heads, hd, ws.attn.as<float>(), ws.scratch.as<float>(), s, &aq,
