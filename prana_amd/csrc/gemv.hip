@@ -1017,9 +1017,16 @@ int launch_decode_t(const DecodeJob& job, const int8_t* q, const float* sa, cons
   constexpr bool kSmall = RegUnit<KIND>::kElems == 32;
   const bool act = job.act != 0;
   if constexpr (kSmall) {
-    // verify batches: the chunk-major kernel, where the act tiles would not
-    // quantize h themselves anyway (tiles of fewer than 32 rows per matrix)
-    const int w = n_tok >= 2 && !job.rk.table ? km_chunk(static_cast<int>(job.m[0].cols / 32), n_tok) : 0;
+    // verify batches: the chunk-major kernel for long rows (more than 128
+    // blocks: whole-row staging of several tokens limits the tile kernel to
+    // one workgroup per CU), for the act tiles, and for batches of more than
+    // kDecMaxTok tokens (one launch instead of two); the tile kernel keeps
+    // the other batches of up to kDecMaxTok tokens, where it is faster
+    // (measured on the 7B shapes). Act tiles here have fewer than 32 rows per
+    // matrix, so the caller quantizes h, as it does after the tile kernel.
+    const int nb_k = static_cast<int>(job.m[0].cols / 32);
+    const bool km_pref = nb_k > 128 || act || n_tok > static_cast<size_t>(kDecMaxTok);
+    const int w = n_tok >= 2 && km_pref && !job.rk.table ? km_chunk(nb_k, n_tok) : 0;
     if (w > 0 && (!act || choose_geom<KIND>(job.m[0].cols, true).rt % 32 != 0) && (!act || job.h)) {
       if (act) return launch_km<KIND, true>(job, w, q, sa, sums, n_tok, s);
       return launch_km<KIND, false>(job, w, q, sa, sums, n_tok, s);
@@ -1917,10 +1924,16 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s) {
   if (n_tok == 0 || m.rows == 0) return kOk;
-  // batches of up to 16 tokens whose width the chunk-major multi-token kernel
-  // takes stay on the decode path (it beats the skinny matrix-core kernel on
-  // verify-sized batches)
-  const bool km = n_tok <= kDecodeMaxTokens && km_chunk(static_cast<int>(m.cols / 32), n_tok) > 0;
+  // batches of up to 16 tokens that the chunk-major multi-token kernel takes
+  // stay on the decode path when it beats the skinny matrix-core kernel:
+  // rows of more than 128 blocks, or few rows (the skinny kernel has the
+  // larger fixed cost, the chunk-major one the larger cost per row and token;
+  // on the 7B Q4_0 shapes they cross near 9 tokens x 8192 rows; for the 8-bit
+  // kinds the skinny kernel stays ahead from 9 tokens)
+  const int nb_m = static_cast<int>(m.cols / 32);
+  const bool km = n_tok <= kDecodeMaxTokens && km_chunk(nb_m, n_tok) > 0 &&
+                  (m.kind == kKindQ4_0 || n_tok <= static_cast<size_t>(kDecMaxTok)) &&
+                  (nb_m > 128 || m.rows * n_tok <= size_t{9} * 8192);
   if (gemv_skinny(m.kind, n_tok) && !km) {
     switch (m.kind) {
       case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(m, q, sa, sums, n_tok, o, s);

@@ -56,6 +56,10 @@ GEMM_CASES = [  # (tag, ggml type, rows, cols, N)
 ]
 
 
+VERIFY_SHAPES = [("Q|K|V", 6144, 4096), ("wo", 4096, 4096), ("ffn_down", 4096, 14336), ("head", 32000, 4096)]
+VERIFY_TOKENS = [2, 5, 9, 16]
+
+
 def _marker(P, buf):
     P.check(P.load().prana_memset_d(buf.ptr, 0, 256))
 
@@ -102,6 +106,28 @@ def run(manifest_path, only=None):
         P.check(P.load().prana_synchronize())
         cases.append({"config": "GEMM", "case": f"{tag} {rows}x{cols} N={n}", "calls": TIMED,
                       "bytes": len(raw) + n * cols + n * rows * 4, "ops": 2 * rows * cols * n})
+        del mats
+
+    for tag, rows, cols in (VERIFY_SHAPES if only == "VERIFY" else []):
+        # C4's speculative verify batches: Q4_0 7B shapes at k+1 tokens (and
+        # 2, 16), pre-quantized activations, weight copies past the MALL
+        raw = P.synth_tensor(Q4_0, rows, cols, rows * 3 + cols, 0.02)
+        copies = max(3, -(-2 * MALL // raw.nbytes))
+        mats = [P.Matrix(Q4_0, rows, cols, raw) for _ in range(copies)]
+        print(f"VERIFY {tag}: {copies} copies", file=sys.stderr, flush=True)
+        for n in VERIFY_TOKENS:
+            q, sa, sums = P.quantize_acts(rng.standard_normal((n, cols)).astype(np.float32))
+            dq, ds, dm = P.DeviceArray.from_host(q), P.DeviceArray.from_host(sa), P.DeviceArray.from_host(sums)
+            out = P.DeviceArray((n, rows), np.float32)
+            for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
+                _marker(P, marker)
+                for i in range(calls):
+                    P.check(P.load().prana_matmul_prefill(mats[i % copies].h, None, dq.ptr, ds.ptr, dm.ptr, n,
+                                                          out.ptr, None))
+            _marker(P, marker)
+            P.check(P.load().prana_synchronize())
+            cases.append({"config": "C4 verify", "case": f"{tag} Q4_0 {rows}x{cols} N={n}", "calls": TIMED,
+                          "bytes": len(raw) + n * cols + n * rows * 4})
         del mats
 
     nh, nkv, hd = 32, 8, 128
@@ -317,20 +343,116 @@ def summarize_counters(db, cus=256):
     print("\n".join(out))
 
 
+def decode_trace_summary(db, bench_json, command):
+    """Markdown summary of a kernel trace of bench.py (7B-shape Q4_0 decode):
+    per-kernel time over the run, the decode GEMVs by shape (grid size), and
+    the bench's own event-sampled GEMV figures from its JSON line."""
+    import re
+    from collections import defaultdict
+
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, count(*), avg(duration), min(duration), max(duration), sum(duration) from kernels "
+                     "group by name order by sum(duration) desc").fetchall()
+    tot = sum(r[5] for r in rows)
+
+    def short(n):
+        n = n.replace("prana::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+        return re.sub(r"\(.*$", "", n.replace("prana::", "").replace("void ", ""))
+
+    out = ["# 7B-shape Q4_0 decode: rocprofv3 kernel trace", "",
+           "Command (from the repository root on the GPU box; `$REPO` is that root):", "", "```", command, "```", "",
+           "Kernel time per kernel over the whole run (model upload, 511-token prefill, warmup and timed decode steps).",
+           "", "| kernel | calls | avg us | min us | max us | total ms | share |", "|---|---:|---:|---:|---:|---:|---:|"]
+    for n, cnt, avg, mn, mx, sm in rows[:16]:
+        out.append(f"| `{short(n)}` | {cnt} | {avg / 1000:.2f} | {mn / 1000:.2f} | {mx / 1000:.2f} | {sm / 1e6:.2f} "
+                   f"| {100 * sm / tot:.1f}% |")
+    out.append(f"| (all kernels) | {sum(r[1] for r in rows)} | | | | {tot / 1e6:.2f} | 100% |")
+    shapes = {("gemv_tile_kernel<3, 4, false, false, 256>", 768 * 256): ("Q\\|K\\|V 6144x4096", 14.16),
+              ("gemv_tile_kernel<3, 4, false, false, 256>", 512 * 256): ("wo 4096x4096", 9.44),
+              ("gemv_tile_kernel<3, 4, true, false, 256>", 3584 * 256): ("gate\\|up 2x14336x4096 + SiLU", 66.06),
+              ("gemv_tile_kernel<3, 7, false, false, 256>", 1024 * 256): ("down 4096x14336", 33.03),
+              ("gemv_tile_kernel<3, 4, false, false, 256>", 4000 * 256): ("LM head 32000x4096", 73.73)}
+    d = defaultdict(list)
+    for name, dur, gx in c.execute("select name, duration, grid_x from kernels where name like '%gemv_tile_kernel%'"):
+        d[(short(name), gx)].append(dur / 1000)
+    out += ["", "Decode GEMVs by shape (the grid size identifies the shape; MB = GGUF Q4_0 block bytes streamed):", "",
+            "| kernel instance | shape | launches | avg us | MB | GB/s | % of 8 TB/s |", "|---|---|---:|---:|---:|---:|---:|"]
+    tok_us = tok_mb = 0.0
+    for key, (label, mb) in shapes.items():
+        v = d.get(key)
+        if not v:
+            continue
+        a = sum(v) / len(v)
+        gbs = mb * 1e3 / a
+        mult = 1 if "head" in label else 32
+        tok_us += a * mult
+        tok_mb += mb * mult
+        out.append(f"| `{key[0]}` | {label} | {len(v)} | {a:.2f} | {mb:.2f} | {gbs:.0f} | {100 * gbs / 8000:.1f}% |")
+    if tok_us:
+        gbs = tok_mb * 1e3 / tok_us
+        out.append(f"| per token (32 layers + head, 129 launches) | | | {tok_us:.1f} | {tok_mb:.1f} | {gbs:.0f} "
+                   f"| {100 * gbs / 8000:.1f}% |")
+    b = json.loads(open(bench_json).read().strip().splitlines()[-1])
+    r = b["roofline"]
+    out += ["", "The bench itself (no profiler attached) samples every 8th GEMV dispatch with HIP dispatch-timestamp "
+            f"events inside its timed region: {r['avg_launch_us']} us average over {r['timed_launches']} launches, "
+            f"{r['achieved']:.0f} GB/s ({100 * r['frac']:.1f} % of 8 TB/s); {b['value']} tok/s "
+            f"({b['config']['tok_s_without_events']} tok/s with no events)."]
+    if r.get("traffic"):
+        out[-1] += (f" HBM traffic per GEMV launch from the counter runs is "
+                    f"{r['traffic'] / r['bytes_per_launch']:.3f} x the algorithmic bytes "
+                    f"(q4_0_gemv_7b_decode_traffic.json).")
+    print("\n".join(out))
+
+
+def round_trace_summary(db):
+    """Per-kernel table of the last timed call in a kernel trace of --spec:
+    every kernel after the call's prefill (the last prefill-GEMM or prefill
+    attention launch), grouped by kernel, grid and LDS size."""
+    from collections import defaultdict
+
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, start, end, grid_x, workgroup_x, lds_size from kernels order by start").fetchall()
+    last = max(i for i, r in enumerate(rows) if "attn_prefill" in r[0] or "gemm_mfma" in r[0])
+    tail = rows[last + 1:]
+    d = defaultdict(lambda: [0, 0.0])
+    for n, st, en, gx, wx, lds in tail:
+        n = n.replace("(anonymous namespace)::", "").replace("void ", "").replace("prana::", "")
+        key = (n.split("(")[0], gx // wx, wx, lds)
+        d[key][0] += 1
+        d[key][1] += (en - st) / 1000
+    tot = sum(v[1] for v in d.values())
+    out = [f"Kernel time {tot / 1000:.1f} ms over a {(tail[-1][2] - tail[0][1]) / 1e6:.1f} ms span, "
+           f"{len(tail)} launches.", "",
+           "| kernel | grid | lanes | LDS bytes | launches | avg us | total ms | share |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for k, v in sorted(d.items(), key=lambda kv: -kv[1][1])[:18]:
+        out.append(f"| `{k[0]}` | {k[1]} | {k[2]} | {k[3]} | {v[0]} | {v[1] / v[0]:.2f} | {v[1] / 1000:.2f} "
+                   f"| {100 * v[1] / tot:.1f}% |")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--summarize", metavar="DB")
     ap.add_argument("--counters", metavar="DB", help="MFMA / VALU utilisation table of a --pmc run")
     ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
-    ap.add_argument("--only", choices=["C1", "GEMM", "C3"], help="run one configuration's sweep")
+    ap.add_argument("--only", choices=["C1", "GEMM", "C3", "VERIFY"], help="run one configuration's sweep")
     ap.add_argument("--spec", type=int, metavar="K", help="C4 speculative decode alone, K drafts per round")
     ap.add_argument("--tokens", type=int, default=48, help="tokens of the --spec call")
+    ap.add_argument("--round-trace", metavar="DB", help="per-kernel table of a kernel trace of --spec")
+    ap.add_argument("--decode-trace", nargs=3, metavar=("DB", "BENCH_JSON", "COMMAND"),
+                    help="summary of a kernel trace of bench.py (with the bench's JSON line and the trace command)")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
     if args.models:
         print(models_table(run_models()))
     elif args.spec:
         run_spec(args.spec, args.tokens)
+    elif args.round_trace:
+        round_trace_summary(args.round_trace)
+    elif args.decode_trace:
+        decode_trace_summary(*args.decode_trace)
     elif args.counters:
         summarize_counters(args.counters)
     elif args.summarize:

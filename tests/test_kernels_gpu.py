@@ -105,23 +105,25 @@ def test_matmul_batched(ty, rows, cols, n_tok):
 
 
 @pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
-@pytest.mark.parametrize("rows,cols,n_tok", [(37, 2048, 2), (300, 4096, 5), (129, 7168, 8), (70, 14336, 3),
-                                             (70, 14336, 6), (4097, 4096, 7)])
+@pytest.mark.parametrize("rows,cols,n_tok", [(37, 2048, 10), (300, 4096, 12), (129, 7168, 8), (70, 14336, 3),
+                                             (70, 14336, 6), (4097, 4096, 9), (515, 14336, 16)])
 def test_matmul_verify_batch_chunked(ty, rows, cols, n_tok):
-    # 2..8 tokens over widths of 2, 4, 7 or 14 chunks of 32 or 64 blocks: the
-    # chunk-major multi-token kernel (activations and term rows staged one
-    # chunk at a time); ragged last tiles
+    # Widths of 2, 4, 7 or 14 chunks of 32 or 64 blocks: the chunk-major
+    # multi-token kernel (activations and term rows staged one chunk at a
+    # time) takes rows of more than 128 blocks from 2 tokens and, for Q4_0,
+    # narrower rows from 9 tokens (16 tokens: two launches); Q8_0 takes the
+    # skinny matrix-core kernel from 9 tokens. Ragged last tiles.
     raw, g, o = _mat_pair(ty, rows, cols, 60 + n_tok + cols, real=True)
     a = rng(n_tok + 3).standard_normal((n_tok, cols)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
 
 
 def test_matmul_verify_batch_chunked_q8_f32_scales():
-    w = rng(13).standard_normal((70, 4096)).astype(np.float32)
+    w = rng(13).standard_normal((70, 14336)).astype(np.float32)
     q, s = O.quantize_q8(w)
     g, o = P.Matrix.q8_parts(q, s), O.Mat.q8_parts(q, s)
-    for n_tok in (2, 6):
-        a = rng(19 + n_tok).standard_normal((n_tok, 4096)).astype(np.float32)
+    for n_tok in (3, 6):
+        a = rng(19 + n_tok).standard_normal((n_tok, 14336)).astype(np.float32)
         assert same_bits(g.apply(a), o.apply(a))
 
 
