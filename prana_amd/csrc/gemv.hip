@@ -433,19 +433,22 @@ constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: on
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
 // STAGED: more than one stage (double-buffered registers and terms);
 // otherwise the whole row tile is one stage. NT lanes per workgroup.
+// The workgroup's tile: matrix mi (tiles are numbered matrix after matrix)
+// and its row tile.
+__device__ __forceinline__ void job_tile(const DecodeJob& job, int* mi, int* tile) {
+  *mi = 0;
+  *tile = blockIdx.x;
+  while (*mi < job.n_mats - 1 && *tile >= job.tiles[*mi]) *tile -= job.tiles[(*mi)++];
+}
+
 template <int KIND, int U, bool ACT, bool STAGED, int NT>
-__global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
-                                                        const float* __restrict__ sa,
-                                                        const int* __restrict__ sums, int n_tok) {
+__device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_t* __restrict__ q,
+                                               const float* __restrict__ sa, const int* __restrict__ sums,
+                                               int n_tok, int mi, int tile) {
   extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
   constexpr int TPU = R::kTpu;
   const int tid = threadIdx.x;
-
-  int mi = 0, tile = blockIdx.x;
-  if (!ACT) {
-    while (mi < job.n_mats - 1 && tile >= job.tiles[mi]) tile -= job.tiles[mi++];
-  }
   const int rt = job.rt, SB = job.sb;
   const int ROWS = ACT ? 2 * rt : rt;
   const int K = static_cast<int>(job.m[0].cols);
@@ -682,6 +685,31 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   }
 }
 
+template <int KIND, int U, bool ACT, bool STAGED, int NT>
+__global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ sa,
+                                                        const int* __restrict__ sums, int n_tok) {
+  int mi = 0, tile = blockIdx.x;
+  if (!ACT) job_tile(job, &mi, &tile);
+  gemv_tile_body<KIND, U, ACT, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+}
+
+// Matrices of two formats with the same unit width and tile geometry in one
+// launch (a fused Q|K|V whose v projection is stored in another format, as
+// K-quant-mixture GGUF files store it): each workgroup runs the body of its
+// matrix's format.
+template <int KA, int KB, int U, bool STAGED, int NT>
+__global__ __launch_bounds__(NT) void gemv_tile_mixed_kernel(DecodeJob job, const int8_t* __restrict__ q,
+                                                              const float* __restrict__ sa,
+                                                              const int* __restrict__ sums, int n_tok) {
+  int mi, tile;
+  job_tile(job, &mi, &tile);
+  if (job.m[mi].kind == KA)
+    gemv_tile_body<KA, U, false, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+  else
+    gemv_tile_body<KB, U, false, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+}
+
 // ---- verify batches: 2..8 tokens, 32-element formats
 // Chunk-major units: with W = nb / U blocks per chunk and ROWS = 256 / W rows
 // per tile (gate and up rows together in act mode), lane t's unit i is row
@@ -883,10 +911,17 @@ TileGeom choose_geom(size_t K, bool act) {
   return TileGeom{1, 32, 8, 256};
 }
 
-template <int KIND, int U, bool ACT, bool STAGED, int NT>
+// KB >= 0: the matrices come in two formats, KIND and KB, with the same tile
+// geometry (gemv_tile_mixed_kernel; not in act mode).
+template <int KIND, int U, bool ACT, bool STAGED, int NT, int KB = -1>
 int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, const float* sa, const int* sums,
                   size_t n_tok, hipStream_t s) {
   using R = RegUnit<KIND>;
+  static_assert(KB < 0 || !ACT, "two formats only outside act mode");
+  constexpr int kTpuMax = KB < 0 ? R::kTpu : std::max(R::kTpu, RegUnit<(KB < 0 ? KIND : KB)>::kTpu);
+  const void* const fn = KB < 0 ? reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>)
+                                : reinterpret_cast<const void*>(
+                                      gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>);
   DecodeJob job = job0;
   job.rt = g.rt;
   job.sb = g.sb;
@@ -896,7 +931,7 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   const int n_stages = (nb + g.sb - 1) / g.sb;
   PRANA_CHECK(STAGED || n_stages == 1, "gemv: single-stage tile with several stages");
   const size_t astride = ((K + 8 * (K / 32)) + 15) & ~static_cast<size_t>(15);
-  const size_t term_bytes = (size_t)(n_stages > 1 ? 2 : 1) * rows_wg * (g.sb * R::kTpu + 1) * 4;
+  const size_t term_bytes = (size_t)(n_stages > 1 ? 2 : 1) * rows_wg * (g.sb * kTpuMax + 1) * 4;
   int total = 0;
   for (int i = 0; i < (ACT ? 1 : job.n_mats); i++) {
     job.tiles[i] = static_cast<int>((job.m[i].rows + g.rt - 1) / g.rt);
@@ -906,12 +941,11 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   // verify batches of up to kDecMaxTok tokens stream the weights once; the
   // activations and term rows of every token sit in LDS, beyond 64 KB when
   // the device grants it
-  static const size_t lds_cap = [] {
+  static const size_t lds_cap = [fn] {
     int dev = 0, b = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || b <= 65536)
       return size_t{65536};
-    const void* fn = reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>);
     const int dyn = b - static_cast<int>(static_lds_bytes(fn));
     return dyn > 65536 && set_max_dynamic_lds(fn, dyn) ? static_cast<size_t>(dyn) : size_t{65536};
   }();
@@ -934,7 +968,10 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     }
     const size_t G = K / 32;
     LaunchEvents& le = launch_events();
-    if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
+    if constexpr (KB >= 0) {
+      hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>), dim3(total), dim3(NT),
+                         nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+    } else if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
       hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s,
                             le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
       le = LaunchEvents{};
@@ -1067,6 +1104,51 @@ int launch_decode_t(const DecodeJob& job, const int8_t* q, const float* sa, cons
     }
   }
   return fail(kErrInvalid, "gemv: no tile geometry");
+}
+
+// Two formats in one decode launch (non-act): the tile geometry of KA, which
+// the caller has checked KB shares.
+template <int KA, int KB>
+int launch_decode_mixed(const DecodeJob& job, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                        hipStream_t s) {
+  constexpr bool kSmall = RegUnit<KA>::kElems == 32;
+  static_assert(RegUnit<KA>::kElems == RegUnit<KB>::kElems, "one unit width");
+  const TileGeom g = choose_geom<KA>(job.m[0].cols, false);
+  const int nb = static_cast<int>(job.m[0].cols / RegUnit<KA>::kElems);
+  if (g.sb < nb) {
+    if constexpr (kSmall) return launch_tile_u<KA, 2, false, true, 256, KB>(job, g, q, sa, sums, n_tok, s);
+    else return launch_tile_u<KA, 1, false, true, 256, KB>(job, g, q, sa, sums, n_tok, s);
+  }
+  switch (g.u) {
+    case 1: return launch_tile_u<KA, 1, false, false, 256, KB>(job, g, q, sa, sums, n_tok, s);
+    case 2: return launch_tile_u<KA, 2, false, false, 256, KB>(job, g, q, sa, sums, n_tok, s);
+  }
+  if constexpr (kSmall) {
+    switch (g.u) {
+      case 4: return launch_tile_u<KA, 4, false, false, 256, KB>(job, g, q, sa, sums, n_tok, s);
+      case 7: return launch_tile_u<KA, 7, false, false, 256, KB>(job, g, q, sa, sums, n_tok, s);
+      case 8: return launch_tile_u<KA, 8, false, false, 256, KB>(job, g, q, sa, sums, n_tok, s);
+    }
+  }
+  return fail(kErrInvalid, "gemv: no tile geometry");
+}
+
+// The supported pair of two formats among ms[0..n) (same cols), as (KA, KB)
+// in canonical order, or {-1, -1}: Q4_0 with Q8_0 (block-32), Q4_K with Q6_K.
+std::pair<int, int> mixed_pair(const DevMat* ms, int n) {
+  int a = ms[0].kind, b = -1;
+  for (int i = 1; i < n; i++) {
+    if (ms[i].kind == a || ms[i].kind == b) continue;
+    if (b >= 0) return {-1, -1};
+    b = ms[i].kind;
+  }
+  if (b < 0) return {-1, -1};
+  if (a > b) std::swap(a, b);
+  const bool ok = (a == kKindQ4_0 && b == kKindQ8_0) || (a == kKindQ8_0 && b == kKindQ4_0) ||
+                  (a == kKindQ4_K && b == kKindQ6_K) || (a == kKindQ6_K && b == kKindQ4_K);
+  if (!ok) return {-1, -1};
+  // canonical: the 4-bit format first
+  return a == kKindQ4_0 || a == kKindQ4_K ? std::make_pair(a, b) : std::make_pair(b, a);
 }
 
 template <int KIND>
@@ -1861,8 +1943,11 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
   PRANA_CHECK(n >= 1 && n <= 3, "gemv_multi: 1..3 matrices");
   if (fused) *fused = false;
   if (n_tok == 0) return kOk;
-  for (int i = 1; i < n; i++)
-    PRANA_CHECK(ms[i].kind == ms[0].kind && ms[i].cols == ms[0].cols, "gemv_multi: matrices must share kind and cols");
+  for (int i = 1; i < n; i++) PRANA_CHECK(ms[i].cols == ms[0].cols, "gemv_multi: matrices must share cols");
+  bool one_kind = true;
+  for (int i = 1; i < n; i++) one_kind = one_kind && ms[i].kind == ms[0].kind;
+  const std::pair<int, int> pair = one_kind ? std::make_pair(-1, -1) : mixed_pair(ms, n);
+  PRANA_CHECK(one_kind || gemv_multi_fusable(ms, n), "gemv_multi: matrices must share a kind or form a fusable pair");
   if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
@@ -1892,7 +1977,30 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
       if (fused) *fused = true;
     }
   }
+  if (!one_kind) {
+    if (pair.first == kKindQ4_0) return launch_decode_mixed<kKindQ4_0, kKindQ8_0>(job, q, sa, sums, n_tok, s);
+    return launch_decode_mixed<kKindQ4_K, kKindQ6_K>(job, q, sa, sums, n_tok, s);
+  }
   return dispatch_kind(ms[0].kind, [&](auto k) { return launch_decode_t<decltype(k)::value>(job, q, sa, sums, n_tok, s); });
+}
+
+bool gemv_multi_fusable(const DevMat* ms, int n) {
+  if (n < 2 || n > 3) return n == 1;
+  for (int i = 1; i < n; i++)
+    if (ms[i].cols != ms[0].cols) return false;
+  bool one_kind = true;
+  for (int i = 1; i < n; i++) one_kind = one_kind && ms[i].kind == ms[0].kind;
+  if (one_kind) return true;
+  const std::pair<int, int> p = mixed_pair(ms, n);
+  if (p.first < 0) return false;
+  // the two formats must give the same tile geometry
+  auto geom = [&](int kind) {
+    return dispatch_kind(kind, [&](auto k) {
+      const TileGeom g = choose_geom<decltype(k)::value>(ms[0].cols, false);
+      return g.u * 1000000 + g.rt * 1000 + g.sb;
+    });
+  };
+  return geom(p.first) == geom(p.second);
 }
 
 int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t* q, const float* sa, const int* sums,

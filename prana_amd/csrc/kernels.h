@@ -140,6 +140,11 @@ struct RopeKv {
 };
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
                       size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr);
+// Whether launch_gemv_multi takes these matrices in one launch: same cols and
+// either one kind, or two kinds of the same unit width and tile geometry
+// (Q4_0 with Q8_0, Q4_K with Q6_K: a Q|K|V whose v is stored in another
+// format).
+bool gemv_multi_fusable(const DevMat* ms, int n);
 // gate|up in one launch with the activation fused: h = act(gate) * up
 // (norms.rs:27-41, infer.rs:193-199), quantized for the down projection;
 // act 0 = silu, 1 = gelu_tanh. h (f32) is optional when tiles hold whole

@@ -299,10 +299,20 @@ int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipS
 int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s,
                        const RopeKv* rk, bool* fused) {
   if (fused) *fused = false;
+  // three quantized matrices that one launch takes (one format, or a fusable
+  // pair of formats) go together; otherwise runs of one format
+  bool fuse3 = n_mats == 3;
+  for (int k = 0; fuse3 && k < 3; k++) fuse3 = w[k]->d.kind != kKindF32;
+  if (fuse3) {
+    const DevMat d3[3] = {w[0]->d, w[1]->d, w[2]->d};
+    fuse3 = gemv_multi_fusable(d3, 3);
+  }
   int i = 0;
   while (i < n_mats) {
     int j = i + 1;
-    while (j < n_mats && j - i < 3 && w[j]->d.kind == w[i]->d.kind && w[j]->d.cols == w[i]->d.cols) j++;
+    if (fuse3) j = 3;
+    else
+      while (j < n_mats && j - i < 3 && w[j]->d.kind == w[i]->d.kind && w[j]->d.cols == w[i]->d.cols) j++;
     if (j - i == 1 || w[i]->d.kind == kKindF32) {
       for (int k = i; k < j; k++)
         if (int rc = apply(*w[k], n, xf, o[k], s)) return rc;

@@ -275,6 +275,33 @@ def test_block32_verify_batches_bitexact(ty):
         assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
 
 
+@pytest.mark.parametrize("dim", [512, 896])
+def test_mixed_format_qkv_one_launch_bitexact(dim):
+    # The K-quant mixture stores v in another format than q and k: Q4_K with
+    # Q6_K (512 wide), and their block-32 fallbacks Q4_0 with Q8_0 (896 wide,
+    # C2's widths); Q|K|V then runs as one launch with RoPE and the cache rows
+    # in its epilogue (decode) or over a verify batch.
+    cfg = M.config(dim, 1024, 2, dim // 64, 2, 500, 64, head_dim=64, rope_theta=1e6, norm_eps=1e-6, rope_neox=1)
+    t = M.synth_tensors(cfg, M.types_c2, 6 + dim, biases=True)
+    kinds = {t[f"blk.0.attn_{x}.weight"][0] for x in "qkv"}
+    assert len(kinds) == 2, kinds
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(64), o.cache(64)
+    prompt = np.random.default_rng(dim).integers(0, cfg["vocab_size"], 30).astype(np.uint32)
+    gc.prefill(prompt[:8])
+    oc.prefill(prompt[:8])
+    tok = int(prompt[8])
+    for pos in range(8, 12):
+        lg, lo = gc.forward(tok, pos), oc.forward(tok, pos)
+        assert same_bits(lg, lo), pos
+        tok = int(np.argmax(lo))
+    batch = [int(x) for x in prompt[12:17]]
+    assert same_bits(gc.forward_batch(batch, 12), oc.forward_batch(batch, 12))
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, 17), oc.read(layer, which, 17)), (layer, which)
+
+
 # ------------------------------------------------------------------ config 4: 7B shape, Q4_0
 @pytest.fixture(scope="module")
 def c4():
