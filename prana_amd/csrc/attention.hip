@@ -342,13 +342,13 @@ __device__ __forceinline__ int logical_block(int nb) {
 //   softmax: one 1024-lane workgroup per (query row, head): max, expf, the
 //            exact left-to-right sum, probabilities -> scratch (in place)
 //   PV     : one workgroup per (query row, head, 64-dim slice): one folder
-//            wave adds the products of its dims in row order while four
+//            wave adds the products of its dims in row order while eight
 //            producer waves stream V and form the products of the next chunk
 // Scratch rows are (query row, head) major with a stride of
 // split_stride(ctx_cap) floats.
 constexpr int kSplitRows = 256;     // K rows per scores workgroup
 constexpr int kSmNT = 1024;         // softmax lanes
-constexpr int kPvProd = 256;        // producer lanes
+constexpr int kPvProd = 512;        // producer lanes (their V loads, not the fold, set the pace)
 constexpr int kPvNT = 64 + kPvProd; // one folder wave + producers
 // cache windows from this many rows on take the split path
 constexpr size_t kSplitMinRows = 2048;
