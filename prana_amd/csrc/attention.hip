@@ -21,10 +21,10 @@ namespace prana {
 
 namespace {
 
-constexpr int kNT = 256;             // lanes per workgroup
+constexpr int kNT = 512;             // lanes per workgroup
 constexpr int kScoreLds = 4096;      // probabilities kept in LDS up to this length
 constexpr int kPieces = 2 * kNT;     // 16-byte V pieces per PV chunk (two per lane)
-constexpr int kProdFloats = 512 * 8 + 4 * 256;  // one product buffer: dw*(rows+4) <= this
+constexpr int kProdFloats = kPieces * 8 + 4 * 256;  // one product buffer: dw*(rows+4) <= this
 
 template <bool F16>
 struct Elem;
