@@ -50,6 +50,7 @@ int launch_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, flo
 // normalise + optional quantize is parallel.
 constexpr int kNormMaxDim = 16320;  // row and weights staged in LDS (about 132 KB)
 constexpr int kNormSmallDim = 2048;
+constexpr int kNormSerialMax = 512;  // rows up to this fold their squares on one lane
 template <int kNormNT>
 __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                           int dim, float eps, float* __restrict__ out,
@@ -82,12 +83,28 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restric
   }
   __syncthreads();
   // sum of squares in the reference's left-to-right order (norms.rs:15)
-  const float ss = exact::block_seq_sum_short<kNormNT>(
-      [xs](int i) {
-        const float v = xs[exact::run_pad(i)];
-        return v * v;
-      },
-      dim);
+  float ss;
+  if (dim <= kNormSerialMax) {
+    // short rows: one lane folds the squares from a zero-padded LDS row at
+    // the add latency, which beats the parallel scan's fixed cost
+    __shared__ __align__(16) float sq[exact::lane_pad(kNormSerialMax)];
+    __shared__ float s_ss;
+    for (int i = tid; i < exact::lane_pad(dim); i += kNormNT) {
+      const float v = i < dim ? xs[exact::run_pad(i)] : 0.0f;
+      sq[i] = v * v;
+    }
+    __syncthreads();
+    if (tid == 0) s_ss = exact::lane_seq_sum_padded(sq, dim);
+    __syncthreads();
+    ss = s_ss;
+  } else {
+    ss = exact::block_seq_sum_short<kNormNT>(
+        [xs](int i) {
+          const float v = xs[exact::run_pad(i)];
+          return v * v;
+        },
+        dim);
+  }
   const float mean_sq = ss / static_cast<float>(dim);
   const float inv = 1.0f / sqrtf(mean_sq + eps);
   // four elements per lane at a time; dim is a multiple of 32 whenever
