@@ -4,8 +4,11 @@
 A step is one decoded token: the full forward pass (32 layers, untied Q4_0 LM
 head) plus the device argmax feeding the next step, after a 512-token prefill.
 Inside the timed steps every 8th weight-GEMV dispatch records start/stop HIP
-events as part of the dispatch (on its stream); their average gives the
-roofline figure against the 8 TB/s HBM peak. The same number of steps is also
+events as part of the dispatch (on its stream). Per projection (the launches
+split by the weight bytes they stream) their average duration gives achieved
+GB/s against the 8 TB/s HBM peak; the roofline object is the projection with
+the most time per token. The Q|K|V and gate|up launches also compute their
+input's rmsnorm (one fewer launch each), so their duration includes it. The same number of steps is also
 timed without any events (reported beside). The
 HBM traffic per GEMV launch comes from the committed rocprofv3 counter
 summary (profiles/q4_0_gemv_7b_decode_traffic.json) when present. The
@@ -114,6 +117,7 @@ def main():
     toks = cache.decode(last, pos, K)
     P.check(P.load().prana_synchronize())
     dt = time.perf_counter() - t0
+    shapes = P.gemv_profile_shapes()
     n_launch, gsec, gbytes = P.gemv_profile_read(reset=True)
     P.gemv_profile(False)
     pos += K
@@ -130,11 +134,32 @@ def main():
     dt_plain = time.perf_counter() - t0
     log(f"run without events: {K / dt_plain:.1f} tok/s")
 
+    # the projections by the Q4_0 bytes they stream (18 bytes per 32 weights)
+    d, hid, kv, voc = cfg["dim"], cfg["hidden_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["vocab_size"]
+    q4 = lambda rows, cols: rows * cols // 32 * 18
+    names = {q4(d + 2 * kv, d): ("Q|K|V + attention rmsnorm", cfg["n_layers"]),
+             q4(d, d): ("wo", cfg["n_layers"]),
+             2 * q4(hid, d): ("gate|up + SiLU + FFN rmsnorm", cfg["n_layers"]),
+             q4(d, hid): ("down", cfg["n_layers"]),
+             q4(voc, d): ("LM head", 1)}
+    per = []
+    for b, n, sec in shapes:
+        name, per_tok = names.get(b, (f"{b} bytes", 0))
+        us = sec / max(n, 1) * 1e6
+        gbs = b / (sec / n) / 1e9 if sec > 0 else 0.0
+        per.append({"name": name, "bytes": b, "launches": n, "avg_us": round(us, 3), "gbs": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "per_token": per_tok,
+                    "us_per_token": round(us * per_tok, 1)})
+    dom = max(per, key=lambda r: r["us_per_token"]) if per else None
+    for r in per:
+        log(f"  {r['name']:<30} {r['avg_us']:8.2f} us  {r['gbs']:8.1f} GB/s  ({r['frac'] * 100:.1f} %)")
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "q4_0_gemv_7b_decode_traffic.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and dom is not None:
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            t = json.load(f).get("hbm_bytes_per_launch")
+        traffic = t.get(dom["name"]) if isinstance(t, dict) else None
 
     cpu, match = None, None
     if not args.no_cpu:
@@ -217,15 +242,19 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gemv_gbs, 2),
+            "achieved": dom["gbs"] if dom else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+            "frac": dom["frac"] if dom else None,
             "traffic": traffic,
-            "kernel": "Q4_0 GEMV (all decode projections + head)",
-            "timed_launches": n_launch,
-            "avg_launch_us": round(gsec / max(n_launch, 1) * 1e6, 3),
-            "bytes_per_launch": round(gbytes / max(n_launch, 1)),
+            "kernel": f"Q4_0 decode {dom['name']} (gemv_tile_kernel)" if dom else None,
+            "timed_launches": dom["launches"] if dom else 0,
+            "avg_launch_us": dom["avg_us"] if dom else None,
+            "bytes_per_launch": dom["bytes"] if dom else None,
+            "per_projection": per,
+            "all_gemv_launches": {"timed_launches": n_launch,
+                                  "avg_launch_us": round(gsec / max(n_launch, 1) * 1e6, 3),
+                                  "gbs": round(gemv_gbs, 1), "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
         },
         "cpu_baseline": cpu,
     }

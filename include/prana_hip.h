@@ -240,6 +240,12 @@ int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, s
  * No counterpart in the reference (its timing is PRANA_TIMING, infer.rs:81-130). */
 int prana_gemv_profile(int on);
 int prana_gemv_profile_read(size_t *launches, double *seconds, double *bytes, int reset);
+/* The same timed launches split by shape: one entry per distinct weight-byte
+ * count streamed by a launch (which tells the projections apart), in
+ * ascending byte order; up to cap entries are written and *n_out gets the
+ * number of shapes. Cleared by prana_gemv_profile_read with reset set.
+ * No counterpart in the reference (a measurement hook for the benchmark). */
+int prana_gemv_profile_shapes(size_t cap, size_t *bytes, size_t *launches, double *seconds, size_t *n_out);
 
 typedef struct prana_gen_stats {
   size_t prompt_tokens, generated_tokens, proposed, accepted;

@@ -808,6 +808,17 @@ def gemv_profile_read(reset=True):
     return n.value, s.value, b.value
 
 
+def gemv_profile_shapes():
+    """[(weight bytes per launch, timed launches, seconds)] since the last reset,
+    ascending by bytes (read before gemv_profile_read(reset=True))."""
+    n = C.c_size_t()
+    check(load().prana_gemv_profile_shapes(0, None, None, None, C.byref(n)))
+    cap = n.value
+    b, l, s = (C.c_size_t * max(cap, 1))(), (C.c_size_t * max(cap, 1))(), (C.c_double * max(cap, 1))()
+    check(load().prana_gemv_profile_shapes(cap, b, l, s, C.byref(n)))
+    return [(int(b[i]), int(l[i]), float(s[i])) for i in range(min(cap, n.value))]
+
+
 def generate_speculative(target, draft, prompt, steps, k, stops=()):
     prompt = np.asarray(prompt, np.uint32)
     stops = np.asarray(stops, np.uint32)

@@ -621,7 +621,29 @@ int prana_gemv_profile_read(size_t* launches, double* seconds, double* bytes, in
     if (reset) {
       gp.launches = 0;
       gp.seconds = gp.bytes = 0.0;
+      gp.shapes.clear();
     }
+    return static_cast<int>(kOk);
+  });
+}
+
+int prana_gemv_profile_shapes(size_t cap, size_t* bytes, size_t* launches, double* seconds, size_t* n_out) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    GemvProfile& gp = gemv_profile();
+    int rc = gp.collect();
+    if (rc) return rc;
+    PRANA_CHECK(n_out && (cap == 0 || (bytes && launches && seconds)), "gemv_profile_shapes: null output");
+    size_t i = 0;
+    for (const auto& kv : gp.shapes) {
+      if (i < cap) {
+        bytes[i] = kv.first;
+        launches[i] = kv.second.launches;
+        seconds[i] = kv.second.seconds;
+      }
+      i++;
+    }
+    *n_out = gp.shapes.size();
     return static_cast<int>(kOk);
   });
 }

@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "exact_sum.h"
 #include "kernels.h"
 
 namespace prana {
@@ -425,10 +426,15 @@ struct DecodeJob {
   // one-token Q|K|V (m = q, k, v): rope and the cache rows in the epilogue
   // when rk.table is set (tiles then hold whole rotation pairs)
   RopeKv rk;
+  // one token: the activations are rmsnorm(nin.x) quantized, computed by
+  // every workgroup (NORM kernels) instead of read from q / sa / sums
+  NormIn nin;
 };
 
 constexpr int kDecMaxTok = 8;   // tokens per launch (LDS and folder lanes permitting)
 constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: one quantization block
+constexpr int kNormNT = 1024;    // lanes of a NORM workgroup (one per CU: the norm runs once per CU)
+constexpr int kNormMaxK = 4096;  // NORM rows: four values per lane
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
 // STAGED: more than one stage (double-buffered registers and terms);
@@ -441,10 +447,15 @@ __device__ __forceinline__ void job_tile(const DecodeJob& job, int* mi, int* til
   while (*mi < job.n_mats - 1 && *tile >= job.tiles[*mi]) *tile -= job.tiles[(*mi)++];
 }
 
-template <int KIND, int U, bool ACT, bool STAGED, int NT>
+// NORM (one token, NT == kNormNT): the activations are rmsnorm(job.nin.x)
+// quantized, as launch_rmsnorm would produce them, computed in the prologue
+// while this workgroup's first weight loads are in flight; the row and the
+// sum's terms use the term region of LDS, which the fold reuses afterwards.
+template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false>
 __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_t* __restrict__ q,
                                                const float* __restrict__ sa, const int* __restrict__ sums,
                                                int n_tok, int mi, int tile) {
+  static_assert(!NORM || NT == kNormNT, "NORM workgroups have kNormNT lanes");
   extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
   constexpr int TPU = R::kTpu;
@@ -467,18 +478,42 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     sbase[j] = static_cast<const uint8_t*>(job.m[ACT ? j : mi].sc);
   }
   // unit i of this lane: v = tid + NT*i -> (row, block offset) = divmod(v, SB),
-  // recomputed where needed (cheaper in registers than keeping U pairs).
-  auto unit_row = [&](int i) { return (tid + NT * i) / SB; };
-  auto unit_off = [&](int i) { return (tid + NT * i) % SB; };
+  // recomputed where needed (cheaper in registers than keeping U pairs),
+  // except in NORM launches, which work out the pairs before the norm so
+  // that the divisions stay off the path from the norm to the terms.
+  int urow[NORM ? U : 1], uoff[NORM ? U : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      urow[i] = (tid + NT * i) / SB;
+      uoff[i] = (tid + NT * i) % SB;
+    }
+  }
+  auto unit_row = [&](int i) {
+    if constexpr (NORM) return urow[i];
+    else return (tid + NT * i) / SB;
+  };
+  auto unit_off = [&](int i) {
+    if constexpr (NORM) return uoff[i];
+    else return (tid + NT * i) % SB;
+  };
   auto unit_up = [&](int i) { return ACT && unit_row(i) >= rt; };
   auto unit_lr = [&](int i) { return unit_up(i) ? unit_row(i) - rt : unit_row(i); };
   auto load_stage = [&](R* buf, int s) {
 #pragma unroll
     for (int i = 0; i < U; i++) {
-      const int blk = min(s * SB + unit_off(i), nb - 1);
-      const size_t rr = r0 + min(unit_lr(i), rows_here - 1);
+      int row = unit_row(i), off = unit_off(i);
+      if constexpr (NORM) {
+        // rebuild each stage's addresses from the 32-bit unit indices: kept
+        // across the norm, the hoisted 64-bit pointers would spill
+        asm volatile("" : "+v"(row), "+v"(off));
+      }
+      const bool up = ACT && row >= rt;
+      const int lr = up ? row - rt : row;
+      const int blk = min(s * SB + off, nb - 1);
+      const size_t rr = r0 + min(lr, rows_here - 1);
       const size_t ui = rr * nb + blk;
-      const int j = unit_up(i) ? 1 : 0;
+      const int j = up ? 1 : 0;
       buf[i].load(qbase[ACT ? j : 0] + ui * R::kQB, sbase[ACT ? j : 0] + ui * R::kSB);
     }
   };
@@ -488,10 +523,18 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   const int astride = ((K + 8 * G) + 15) & ~15;
   constexpr int kAw4 = (16384 / 16 + NT - 1) / NT;  // int4 words per lane, K <= 16384
   constexpr int kAg = (512 + NT - 1) / NT;          // block scales per lane
-  int4 a0w[kAw4];
-  float a0s[kAg];
-  int a0m[kAg];
-  {
+  int4 a0w[NORM ? 1 : kAw4];
+  float a0s[NORM ? 1 : kAg];
+  int a0m[NORM ? 1 : kAg];
+  // NORM: elements 4*tid .. 4*tid+3 of the row (K <= 4*NT, K % 32 == 0)
+  const bool nlive = NORM && 4 * tid < K;
+  float4 nx4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nw4 = nx4;
+  if constexpr (NORM) {
+    if (nlive) {
+      nx4 = reinterpret_cast<const float4*>(job.nin.x)[tid];
+      nw4 = reinterpret_cast<const float4*>(job.nin.w)[tid];
+    }
+  } else {
     const int4* qw = reinterpret_cast<const int4*>(q);
 #pragma unroll
     for (int i = 0; i < kAw4; i++) {
@@ -507,11 +550,55 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   }
   R buf0[U];
   R buf1[STAGED ? U : 1];
-  load_stage(buf0, 0);
-  if (STAGED && n_stages > 1) load_stage(buf1, 1);
-
   uint8_t* sm8 = reinterpret_cast<uint8_t*>(smem4);
-  {
+  if (!NORM) {
+    load_stage(buf0, 0);
+    if (STAGED && n_stages > 1) load_stage(buf1, 1);
+  }
+  if constexpr (NORM) {
+    // norms.rs:9-23 on this workgroup: the sum of squares in the reference's
+    // left-to-right order (evaluated exactly), ms = ss/dim, inv =
+    // 1/sqrt(ms+eps), y = (x*inv)*w, then quantize_acts' 32-blocks. The
+    // weight loads go out once the row is here: issued with it, they would
+    // queue ahead of it, and the norm outlasts them either way.
+    float* xs = reinterpret_cast<float*>(sm8 + astride);
+    const float nx[4] = {nx4.x, nx4.y, nx4.z, nx4.w}, nw[4] = {nw4.x, nw4.y, nw4.z, nw4.w};
+    if (nlive) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) xs[exact::run_pad(4 * tid + j)] = nx[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_stage(buf0, 0);
+    __syncthreads();
+    const float ss = exact::block_seq_sum_short<NT>(
+        [xs](int i) {
+          const float v = xs[exact::run_pad(i)];
+          return v * v;
+        },
+        K);
+    const float mean_sq = ss / static_cast<float>(K);
+    const float inv = 1.0f / sqrtf(mean_sq + job.nin.eps);
+    float y[4], sc;
+    int qi[4], sm;
+#pragma unroll
+    for (int j = 0; j < 4; j++) y[j] = nlive ? nx[j] * inv * nw[j] : 0.0f;
+    quantize_quad8(y, qi, &sc, &sm);  // K % 32 == 0: 8-lane groups are all live or all past K
+    // The second stage goes out only now: its registers are needed by the
+    // sum, and a second stage of loads issued before the norm stalls the
+    // waves at issue (the CU's outstanding loads are full), which delays the
+    // norm by more than the earlier loads save (measured on the 7B gate|up).
+    if (STAGED && n_stages > 1) load_stage(buf1, 1);
+    float* as = reinterpret_cast<float*>(sm8 + K);
+    int* am = reinterpret_cast<int*>(as + G);
+    if (nlive) {
+      reinterpret_cast<int*>(sm8)[tid] =
+          (qi[0] & 0xff) | ((qi[1] & 0xff) << 8) | ((qi[2] & 0xff) << 16) | (static_cast<int>(qi[3]) << 24);
+      if ((tid & 7) == 0) {
+        as[tid >> 3] = sc;
+        am[tid >> 3] = sm;
+      }
+    }
+  } else {
     int4* aw = reinterpret_cast<int4*>(sm8);
     float* as = reinterpret_cast<float*>(sm8 + K);
     int* am = reinterpret_cast<int*>(as + G);
@@ -554,13 +641,16 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     float* tb = terms + (s & 1) * buf_floats;
 #pragma unroll
     for (int i = 0; i < U; i++) {
-      const int blk = s * SB + unit_off(i);
-      if (blk < nb && unit_lr(i) < rows_here) {
+      int row = unit_row(i), off = unit_off(i);
+      if constexpr (NORM) asm volatile("" : "+v"(row), "+v"(off));  // as in load_stage
+      const int lr = ACT && row >= rt ? row - rt : row;
+      const int blk = s * SB + off;
+      if (blk < nb && lr < rows_here) {
         for (int t = 0; t < n_tok; t++) {
           const uint8_t* ab = sm8 + t * astride;
           Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
                  reinterpret_cast<const int*>(ab + K) + G};
-          buf[i].terms(a, blk, tb + (t * ROWS + unit_row(i)) * TS + unit_off(i) * TPU);
+          buf[i].terms(a, blk, tb + (t * ROWS + row) * TS + off * TPU);
         }
       }
     }
@@ -685,13 +775,13 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   }
 }
 
-template <int KIND, int U, bool ACT, bool STAGED, int NT>
+template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false>
 __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
                                                         const float* __restrict__ sa,
                                                         const int* __restrict__ sums, int n_tok) {
   int mi = 0, tile = blockIdx.x;
   if (!ACT) job_tile(job, &mi, &tile);
-  gemv_tile_body<KIND, U, ACT, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+  gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
 }
 
 // Matrices of two formats with the same unit width and tile geometry in one
@@ -911,15 +1001,39 @@ TileGeom choose_geom(size_t K, bool act) {
   return TileGeom{1, 32, 8, 256};
 }
 
+// Tile geometry of a NORM launch (kNormNT lanes, whole rows per tile, 8..64
+// rows), or u == 0 when none fits. Block-32 kinds only.
+template <int KIND>
+TileGeom norm_geom(size_t K) {
+  const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
+  if (RegUnit<KIND>::kElems != 32 || nb < 1) return TileGeom{0, 0, 0, 0};
+  for (int u : {4, 2}) {
+    const int units = kNormNT * u;
+    if (units % nb == 0 && units / nb >= 8 && units / nb <= 64) return TileGeom{u, units / nb, nb, kNormNT};
+  }
+  return TileGeom{0, 0, 0, 0};
+}
+
+// Act-mode (gate|up) geometry of a NORM launch: 64 rows of each matrix per
+// tile (whole 32-row blocks, so h is quantized in the epilogue), stages of 32
+// blocks, four units per lane; u == 0 when the rows do not split so.
+template <int KIND>
+TileGeom norm_act_geom(size_t K) {
+  const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
+  if (RegUnit<KIND>::kElems != 32 || nb < 64 || nb % 32 != 0) return TileGeom{0, 0, 0, 0};
+  return TileGeom{4, 64, 32, kNormNT};
+}
+
 // KB >= 0: the matrices come in two formats, KIND and KB, with the same tile
 // geometry (gemv_tile_mixed_kernel; not in act mode).
-template <int KIND, int U, bool ACT, bool STAGED, int NT, int KB = -1>
+template <int KIND, int U, bool ACT, bool STAGED, int NT, int KB = -1, bool NORM = false>
 int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, const float* sa, const int* sums,
                   size_t n_tok, hipStream_t s) {
   using R = RegUnit<KIND>;
   static_assert(KB < 0 || !ACT, "two formats only outside act mode");
+  static_assert(!NORM || KB < 0, "NORM launches take one format");
   constexpr int kTpuMax = KB < 0 ? R::kTpu : std::max(R::kTpu, RegUnit<(KB < 0 ? KIND : KB)>::kTpu);
-  const void* const fn = KB < 0 ? reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT>)
+  const void* const fn = KB < 0 ? reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>)
                                 : reinterpret_cast<const void*>(
                                       gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>);
   DecodeJob job = job0;
@@ -937,7 +1051,13 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     job.tiles[i] = static_cast<int>((job.m[i].rows + g.rt - 1) / g.rt);
     total += job.tiles[i];
   }
-  const size_t per_tok = astride + term_bytes;
+  // NORM: the row staged for the sum of squares shares the term region
+  const size_t norm_bytes = NORM ? (static_cast<size_t>(exact::run_pad(static_cast<int>(K) - 1)) + 1) * 4 : 0;
+  const size_t per_tok = astride + std::max(term_bytes, norm_bytes);
+  PRANA_CHECK(!NORM || (n_tok == 1 && K <= static_cast<size_t>(kNormMaxK) && K % 32 == 0 && job.nin.x &&
+                        job.nin.w && reinterpret_cast<uintptr_t>(job.nin.x) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(job.nin.w) % 16 == 0),
+              "gemv: a fused rmsnorm takes one 16-byte-aligned token of at most 4096 values (a multiple of 32)");
   // verify batches of up to kDecMaxTok tokens stream the weights once; the
   // activations and term rows of every token sit in LDS, beyond 64 KB when
   // the device grants it
@@ -972,12 +1092,12 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
       hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>), dim3(total), dim3(NT),
                          nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     } else if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
-      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s,
-                            le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>), dim3(total), dim3(NT), nt * per_tok,
+                            s, le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
       le = LaunchEvents{};
     } else {
-      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT>), dim3(total), dim3(NT), nt * per_tok, s, j,
-                         q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>), dim3(total), dim3(NT), nt * per_tok, s,
+                         j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     }
     PRANA_LAUNCH_CHECK();
   }
@@ -1938,11 +2058,75 @@ int dispatch_kind(int kind, F&& f) {
 
 constexpr size_t kDecodeMaxTokens = kGemvDecodeMaxTokens;
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = c;
+  }
+  return cus[dev];
+}
+
+// A fused rmsnorm pays the norm once per workgroup, so it is taken when one
+// kNormNT-lane workgroup per compute unit covers every tile: one format of
+// block-32 units, rows of 1024 < cols <= kNormMaxK (a multiple of 32) that
+// norm_geom tiles.
+bool gemv_norm_fusable(const DevMat* ms, int n) {
+  if (n < 1 || n > 3) return false;
+  const size_t K = ms[0].cols;
+  for (int i = 0; i < n; i++)
+    if (ms[i].kind != ms[0].kind || ms[i].cols != K) return false;
+  if (K <= 1024 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
+  const int kind = ms[0].kind;
+  if (kind != kKindQ8F && kind != kKindQ8_0 && kind != kKindQ4_0) return false;
+  size_t tiles = 0;
+  int rt = 0;
+  dispatch_kind(kind, [&](auto k) {
+    rt = norm_geom<decltype(k)::value>(K).rt;
+    return 0;
+  });
+  if (rt == 0) return false;
+  for (int i = 0; i < n; i++) tiles += (ms[i].rows + rt - 1) / rt;
+  const int cus = device_cus();
+  return cus > 0 && tiles <= static_cast<size_t>(cus);
+}
+
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
-                      size_t n_tok, hipStream_t s, const RopeKv* rk, bool* fused) {
+                      size_t n_tok, hipStream_t s, const RopeKv* rk, bool* fused, const NormIn* norm) {
   PRANA_CHECK(n >= 1 && n <= 3, "gemv_multi: 1..3 matrices");
   if (fused) *fused = false;
   if (n_tok == 0) return kOk;
+  if (norm) {
+    PRANA_CHECK(n_tok == 1 && norm->x && norm->w && gemv_norm_fusable(ms, n),
+                "gemv_multi: these matrices cannot take a fused rmsnorm");
+    DecodeJob job{};
+    for (int i = 0; i < n; i++) {
+      job.m[i] = ms[i];
+      job.o[i] = os[i];
+    }
+    job.n_mats = n;
+    job.nin = *norm;
+    return dispatch_kind(ms[0].kind, [&](auto k) {
+      constexpr int KIND = decltype(k)::value;
+      if constexpr (RegUnit<KIND>::kElems == 32) {
+        const TileGeom g = norm_geom<KIND>(ms[0].cols);
+        // RoPE and the cache rows ride along when the tiles hold whole pairs
+        if (rk && n == 3 && ms[1].rows == ms[2].rows && rk->hd > 0 && rk->hd % 2 == 0 &&
+            ms[0].rows % rk->hd == 0 && ms[1].rows % rk->hd == 0 && !os[0].residual && !os[1].residual &&
+            !os[2].residual && (rk->neox ? g.rt % rk->hd == 0 : g.rt % 2 == 0)) {
+          job.rk = *rk;
+          if (fused) *fused = true;
+        }
+        if (g.u == 4) return launch_tile_u<KIND, 4, false, false, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+        if (g.u == 2) return launch_tile_u<KIND, 2, false, false, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+      }
+      return fail(kErrInvalid, "gemv_multi: no fused-rmsnorm tile geometry");
+    });
+  }
   for (int i = 1; i < n; i++) PRANA_CHECK(ms[i].cols == ms[0].cols, "gemv_multi: matrices must share cols");
   bool one_kind = true;
   for (int i = 1; i < n; i++) one_kind = one_kind && ms[i].kind == ms[0].kind;
@@ -2003,8 +2187,22 @@ bool gemv_multi_fusable(const DevMat* ms, int n) {
   return geom(p.first) == geom(p.second);
 }
 
+bool gemv_norm_act_fusable(const DevMat& gate, const DevMat& up) {
+  if (gate.kind != up.kind || gate.rows != up.rows || gate.cols != up.cols) return false;
+  const size_t K = gate.cols;
+  if (K <= 1024 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
+  if (gate.kind != kKindQ8F && gate.kind != kKindQ8_0 && gate.kind != kKindQ4_0) return false;
+  int rt = 0;
+  dispatch_kind(gate.kind, [&](auto k) {
+    rt = norm_act_geom<decltype(k)::value>(K).rt;
+    return 0;
+  });
+  const int cus = device_cus();
+  return rt > 0 && gate.rows % rt == 0 && cus > 0 && gate.rows / rt <= static_cast<size_t>(cus);
+}
+
 int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t* q, const float* sa, const int* sums,
-                    size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s) {
+                    size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s, const NormIn* norm) {
   PRANA_CHECK(gate.kind == up.kind && gate.rows == up.rows && gate.cols == up.cols, "gemv_act: gate/up mismatch");
   PRANA_CHECK(gate.rows % 32 == 0 && hq && hsa && hsum, "gemv_act: rows must be a multiple of 32");
   PRANA_CHECK(gate.kind != kKindF32 && n_tok <= kDecodeMaxTokens, "gemv_act: decode-sized quantized inputs only");
@@ -2018,6 +2216,19 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
   job.hq = hq;
   job.hsa = hsa;
   job.hsum = hsum;
+  if (norm) {
+    PRANA_CHECK(n_tok == 1 && norm->x && norm->w && gemv_norm_act_fusable(gate, up),
+                "gemv_act: these matrices cannot take a fused rmsnorm");
+    job.nin = *norm;
+    return dispatch_kind(gate.kind, [&](auto k) {
+      constexpr int KIND = decltype(k)::value;
+      if constexpr (RegUnit<KIND>::kElems == 32) {
+        const TileGeom g = norm_act_geom<KIND>(gate.cols);
+        return launch_tile_u<KIND, 4, true, true, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+      }
+      return fail(kErrInvalid, "gemv_act: no fused-rmsnorm tile geometry");
+    });
+  }
   bool in_kernel = false;
   int rc = dispatch_kind(gate.kind, [&](auto k) {
     constexpr int KIND = decltype(k)::value;

@@ -138,8 +138,20 @@ struct RopeKv {
   uint16_t* kc;
   uint16_t* vc;
 };
+// rmsnorm (norms.rs:9-23) folded into a one-token GEMV launch: every
+// workgroup normalises the row x with the weights w itself (the exact
+// left-to-right sum of squares, then (x*inv)*w) and quantizes the result into
+// its own activation buffer, as launch_rmsnorm followed by the GEMV would.
+struct NormIn {
+  const float* x;
+  const float* w;
+  float eps;
+};
+// Whether launch_gemv_multi can take these matrices with a NormIn (one token).
+bool gemv_norm_fusable(const DevMat* ms, int n);
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
-                      size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr);
+                      size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr,
+                      const NormIn* norm = nullptr);
 // Whether launch_gemv_multi takes these matrices in one launch: same cols and
 // either one kind, or two kinds of the same unit width and tile geometry
 // (Q4_0 with Q8_0, Q4_K with Q6_K: a Q|K|V whose v is stored in another
@@ -149,8 +161,12 @@ bool gemv_multi_fusable(const DevMat* ms, int n);
 // (norms.rs:27-41, infer.rs:193-199), quantized for the down projection;
 // act 0 = silu, 1 = gelu_tanh. h (f32) is optional when tiles hold whole
 // 32-row blocks; otherwise h is required and a quantize_acts launch follows.
+// norm: one token whose rmsnorm the launch computes itself (the caller has
+// checked gemv_norm_act_fusable); h is then always quantized in the kernel.
+bool gemv_norm_act_fusable(const DevMat& gate, const DevMat& up);
 int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t* q, const float* sa, const int* sums,
-                    size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
+                    size_t n_tok, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s,
+                    const NormIn* norm = nullptr);
 // The exact i32 part of every term (debug / bit-exactness entry point):
 // isums[t][r][term] with T terms per row (cols/32, or cols/16 for Q6_K).
 int launch_block_isums(const DevMat& m, const int8_t* q, const int* sums, size_t n_tok, int* isums, hipStream_t s);

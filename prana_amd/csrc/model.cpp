@@ -297,8 +297,20 @@ int Model::apply(const Mat& w, size_t n, const float* xf, const GemvOut& o, hipS
 }
 
 int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s,
-                       const RopeKv* rk, bool* fused) {
+                       const RopeKv* rk, bool* fused, const NormIn* norm) {
   if (fused) *fused = false;
+  if (norm) {  // one launch over all matrices, which normalises its own input
+    PRANA_CHECK(n == 1 && n_mats >= 1 && n_mats <= 3, "apply_multi: a fused rmsnorm takes one token");
+    DevMat d[3];
+    size_t bytes = 0;
+    for (int k = 0; k < n_mats; k++) {
+      d[k] = w[k]->d;
+      bytes += w[k]->stream_bytes;
+    }
+    return timed(bytes, n, s, [&] {
+      return launch_gemv_multi(d, o, n_mats, nullptr, nullptr, nullptr, n, s, rk, fused, norm);
+    });
+  }
   // three quantized matrices that one launch takes (one format, or a fusable
   // pair of formats) go together; otherwise runs of one format
   bool fuse3 = n_mats == 3;
@@ -335,13 +347,15 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
   return kOk;
 }
 
-int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s) {
+int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm) {
   const size_t H = c.hidden_dim;
   const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens;
+  PRANA_CHECK(!norm || (fuse && n == 1), "apply_gate_up: a fused rmsnorm takes one token of fusable matrices");
   if (fuse) {
     return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {
       return launch_gemv_act(gate.d, up.d, c.act, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n,
-                             ws.gate.as<float>(), ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s);
+                             ws.gate.as<float>(), ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s,
+                             norm);
     });
   }
   GemvOut og{ws.gate.as<float>(), H, nullptr, 0};
@@ -377,6 +391,9 @@ int GemvProfile::collect() {
     launches += 1;
     seconds += ms * 1e-3;
     bytes += static_cast<double>(r.bytes);
+    Shape& sh = shapes[r.bytes];
+    sh.launches += 1;
+    sh.seconds += ms * 1e-3;
   }
   pending.clear();
   used = 0;
@@ -511,16 +528,25 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     uint16_t* kc = cache.k(l);
     uint16_t* vc = cache.v(l);
     // --- attention block (infer.rs:163-188)
-    if ((rc = norm_quant(x, L.vec[kRmsAtt], n, s))) return rc;
+    // decode: the Q|K|V launch normalises x itself when its matrices allow it
+    const Mat* wqkv[3] = {L.w[kWq].get(), L.w[kWk].get(), L.w[kWv].get()};
+    const NormIn nin{x, L.vec[kRmsAtt].as<float>(), c.norm_eps};
+    bool norm_fused = false;
+    if (mode == 0 && n == 1) {
+      const DevMat d3[3] = {wqkv[0]->d, wqkv[1]->d, wqkv[2]->d};
+      norm_fused = gemv_norm_fusable(d3, 3);
+    }
+    if (!norm_fused && (rc = norm_quant(x, L.vec[kRmsAtt], n, s))) return rc;
     GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
     GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
     GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
     bool roped = false;  // the decode Q|K|V launch also did RoPE and the cache rows
     {
-      const Mat* w[3] = {L.w[kWq].get(), L.w[kWk].get(), L.w[kWv].get()};
       const GemvOut o[3] = {oq, ok, ov};
       const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), pos_dev, kc, vc};
-      if ((rc = apply_multi(w, o, 3, n, ws.xb.as<float>(), s, mode == 0 ? &rk : nullptr, &roped))) return rc;
+      if ((rc = apply_multi(wqkv, o, 3, n, ws.xb.as<float>(), s, mode == 0 ? &rk : nullptr, &roped,
+                            norm_fused ? &nin : nullptr)))
+        return rc;
     }
     const ActQuant aq{ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>()};
     bool quantized = false;
@@ -555,8 +581,11 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     GemvOut ores{x, c.dim, nullptr, 1};
     if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
     // --- gated MLP block (infer.rs:191-203)
-    if ((rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
-    if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s))) return rc;
+    // decode: the gate|up launch normalises x itself when its matrices allow it
+    const NormIn nin_ffn{x, L.vec[kRmsFfn].as<float>(), c.norm_eps};
+    const bool ffn_fused = mode == 0 && n == 1 && gemv_norm_act_fusable(L.w[kW1]->d, L.w[kW3]->d);
+    if (!ffn_fused && (rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
+    if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s, ffn_fused ? &nin_ffn : nullptr))) return rc;
     if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s, true))) return rc;
   }
   return kOk;

@@ -2,6 +2,7 @@
 // infer.rs:25-45) and the forward passes.
 #pragma once
 
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -80,6 +81,11 @@ struct GemvProfile {
   std::vector<Rec> pending;
   double seconds = 0.0, bytes = 0.0;
   size_t launches = 0, skipped = 0;
+  struct Shape {
+    size_t launches = 0;
+    double seconds = 0.0;
+  };
+  std::map<size_t, Shape> shapes;  // by weight bytes per launch
   int next_pair(size_t* ev);
   int collect();
 };
@@ -115,12 +121,15 @@ struct Model {
   // Several matrices over the same input (Q|K|V); runs of equal kind share a launch.
   // rk: one-token Q|K|V glue (rope, cache rows) the launch may fold in;
   // *fused tells whether it did.
+  // norm: one token whose rmsnorm the single launch computes itself (the
+  // caller has checked gemv_norm_fusable on all n_mats matrices).
   int apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t n, const float* xf, hipStream_t s,
-                  const RopeKv* rk = nullptr, bool* fused = nullptr);
+                  const RopeKv* rk = nullptr, bool* fused = nullptr, const NormIn* norm = nullptr);
   // gate/up projections with the activation and the down projection's
   // quantization fused when both share a kind; h lands in ws.gate (f32) and
   // ws.hq/hsa/hsum (quantized).
-  int apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s);
+  // norm: one token whose rmsnorm the launch computes (gemv_norm_act_fusable).
+  int apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm = nullptr);
   template <class F>
   int timed(size_t bytes, size_t n, hipStream_t s, F&& launch);
   int norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s);

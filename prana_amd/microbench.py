@@ -367,11 +367,13 @@ def decode_trace_summary(db, bench_json, command):
         out.append(f"| `{short(n)}` | {cnt} | {avg / 1000:.2f} | {mn / 1000:.2f} | {mx / 1000:.2f} | {sm / 1e6:.2f} "
                    f"| {100 * sm / tot:.1f}% |")
     out.append(f"| (all kernels) | {sum(r[1] for r in rows)} | | | | {tot / 1e6:.2f} | 100% |")
-    shapes = {("gemv_tile_kernel<3, 4, false, false, 256>", 768 * 256): ("Q\\|K\\|V 6144x4096", 14.16),
-              ("gemv_tile_kernel<3, 4, false, false, 256>", 512 * 256): ("wo 4096x4096", 9.44),
-              ("gemv_tile_kernel<3, 4, true, false, 256>", 3584 * 256): ("gate\\|up 2x14336x4096 + SiLU", 66.06),
-              ("gemv_tile_kernel<3, 7, false, false, 256>", 1024 * 256): ("down 4096x14336", 33.03),
-              ("gemv_tile_kernel<3, 4, false, false, 256>", 4000 * 256): ("LM head 32000x4096", 73.73)}
+    shapes = {("gemv_tile_kernel<3, 4, false, false, 1024, true>", 192 * 1024):
+              ("rmsnorm + Q\\|K\\|V 6144x4096 + RoPE", 14.16),
+              ("gemv_tile_kernel<3, 4, false, false, 256, false>", 512 * 256): ("wo 4096x4096", 9.44),
+              ("gemv_tile_kernel<3, 4, true, true, 1024, true>", 224 * 1024):
+              ("rmsnorm + gate\\|up 2x14336x4096 + SiLU + quantize", 66.06),
+              ("gemv_tile_kernel<3, 7, false, false, 256, false>", 1024 * 256): ("down 4096x14336", 33.03),
+              ("gemv_tile_kernel<3, 4, false, false, 256, false>", 4000 * 256): ("LM head 32000x4096", 73.73)}
     d = defaultdict(list)
     for name, dur, gx in c.execute("select name, duration, grid_x from kernels where name like '%gemv_tile_kernel%'"):
         d[(short(name), gx)].append(dur / 1000)
@@ -395,11 +397,16 @@ def decode_trace_summary(db, bench_json, command):
     b = json.loads(open(bench_json).read().strip().splitlines()[-1])
     r = b["roofline"]
     out += ["", "The bench itself (no profiler attached) samples every 8th GEMV dispatch with HIP dispatch-timestamp "
-            f"events inside its timed region: {r['avg_launch_us']} us average over {r['timed_launches']} launches, "
-            f"{r['achieved']:.0f} GB/s ({100 * r['frac']:.1f} % of 8 TB/s); {b['value']} tok/s "
-            f"({b['config']['tok_s_without_events']} tok/s with no events)."]
+            f"events inside its timed region ({b['value']} tok/s, {b['config']['tok_s_without_events']} tok/s with no "
+            "events):", "", "| projection | launches | avg us | GB/s | % of 8 TB/s | us per token |",
+            "|---|---:|---:|---:|---:|---:|"]
+    for p in r.get("per_projection", []):
+        out.append(f"| {p['name'].replace('|', chr(92) + '|')} | {p['launches']} | {p['avg_us']} | {p['gbs']} "
+                   f"| {100 * p['frac']:.1f}% | {p['us_per_token']} |")
+    out += ["", f"The roofline object names the projection with the most time per token: {r['kernel']}, "
+            f"{r['avg_launch_us']} us, {r['achieved']} GB/s ({100 * r['frac']:.1f} % of 8 TB/s)."]
     if r.get("traffic"):
-        out[-1] += (f" HBM traffic per GEMV launch from the counter runs is "
+        out[-1] += (f" Its HBM traffic per launch from the counter runs is "
                     f"{r['traffic'] / r['bytes_per_launch']:.3f} x the algorithmic bytes "
                     f"(q4_0_gemv_7b_decode_traffic.json).")
     print("\n".join(out))

@@ -302,6 +302,35 @@ def test_mixed_format_qkv_one_launch_bitexact(dim):
             assert np.array_equal(gc.read(layer, which, 17), oc.read(layer, which, 17)), (layer, which)
 
 
+@pytest.mark.parametrize("ty,dim,hd,neox", [("Q4_0", 2048, 64, 1), ("Q8_0", 4096, 128, 1), ("Q8_0", 4096, 128, 0)])
+def test_fused_norm_decode_bitexact(ty, dim, hd, neox):
+    # Decode rows of 1024 < dim <= 4096 let the Q|K|V and gate|up launches
+    # normalise x themselves (one 1024-lane workgroup per tile; Q|K|V tiles of
+    # 64 rows at 2048 and 32 rows at 4096, gate|up tiles of 64 rows of each
+    # matrix, h quantized in the epilogue). NeoX pairs span whole heads, so at
+    # hd 128 the 32-row tiles leave RoPE to its own launch; at hd 64, and for
+    # adjacent pairs, it rides in the same launch.
+    kind = {"Q4_0": M.Q4_0, "Q8_0": M.Q8_0}[ty]
+    cfg = M.config(dim, 1024, 2, dim // hd, 4, 500, 64, head_dim=hd, rope_neox=neox)
+    t = M.synth_tensors(cfg, lambda name, cols: kind, 90 + dim + neox, biases=True)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(64), o.cache(64)
+    prompt = np.random.default_rng(dim + hd).integers(0, cfg["vocab_size"], 16).astype(np.uint32)
+    gc.prefill(prompt[:6])
+    oc.prefill(prompt[:6])
+    tok = int(prompt[6])
+    for pos in range(6, 10):
+        lg, lo = gc.forward(tok, pos), oc.forward(tok, pos)
+        assert same_bits(lg, lo), pos
+        tok = int(np.argmax(lo))
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, 10), oc.read(layer, which, 10)), (layer, which)
+    go, _ = g.generate(prompt[:5], 6)
+    oo, _ = o.generate(prompt[:5], 6)
+    assert list(go) == list(oo)
+
+
 # ------------------------------------------------------------------ config 4: 7B shape, Q4_0
 @pytest.fixture(scope="module")
 def c4():
