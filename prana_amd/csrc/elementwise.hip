@@ -107,6 +107,35 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restric
   }
   const float mean_sq = ss / static_cast<float>(dim);
   const float inv = 1.0f / sqrtf(mean_sq + eps);
+  if (dim <= 4 * kNormNT) {
+    // rows of up to four values per lane: lane t takes elements 4t..4t+3, so
+    // a 32-block of the quantization is eight lanes (quantize_quad8: one
+    // scale per lane, three DPP steps per reduction); dim is a multiple of
+    // 32 whenever q != nullptr, so 8-lane groups are all live or all past it
+    const int i0 = 4 * tid;
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = i0 + j;
+      y[j] = i < dim ? xs[exact::run_pad(i)] * inv * wl[i] : 0.0f;
+      if (i < dim && out) out[(size_t)blockIdx.x * dim + i] = y[j];
+    }
+    if (q) {
+      float scale;
+      int qi[4], sum;
+      quantize_quad8(y, qi, &scale, &sum);
+      if (i0 < dim) {
+        const size_t gi = (size_t)blockIdx.x * dim + i0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) q[gi + j] = static_cast<int8_t>(qi[j]);
+        if ((tid & 7) == 0) {
+          sa[gi >> 5] = scale;
+          sums[gi >> 5] = sum;
+        }
+      }
+    }
+    return;
+  }
   // four elements per lane at a time; dim is a multiple of 32 whenever
   // q != nullptr, so every 32-lane group is then all live or all past the end
   // and reduces together.
