@@ -456,6 +456,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
                                                const float* __restrict__ sa, const int* __restrict__ sums,
                                                int n_tok, int mi, int tile) {
   static_assert(!NORM || NT == kNormNT, "NORM workgroups have kNormNT lanes");
+  if constexpr (NORM) n_tok = 1;  // a constant the token loops fold away
   extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
   constexpr int TPU = R::kTpu;
@@ -578,16 +579,18 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
         K);
     const float mean_sq = ss / static_cast<float>(K);
     const float inv = 1.0f / sqrtf(mean_sq + job.nin.eps);
+    // The second stage goes out once the sum is done: its registers are
+    // needed by the sum, and a second stage of loads issued before the norm
+    // stalls the waves at issue (the CU's outstanding loads are full), which
+    // delays the norm by more than the earlier loads save; issued by the idle
+    // waves during the sum's final one-wave walk it was slower too (measured
+    // on the 7B gate|up).
+    if (STAGED && n_stages > 1) load_stage(buf1, 1);
     float y[4], sc;
     int qi[4], sm;
 #pragma unroll
     for (int j = 0; j < 4; j++) y[j] = nlive ? nx[j] * inv * nw[j] : 0.0f;
     quantize_quad8(y, qi, &sc, &sm);  // K % 32 == 0: 8-lane groups are all live or all past K
-    // The second stage goes out only now: its registers are needed by the
-    // sum, and a second stage of loads issued before the norm stalls the
-    // waves at issue (the CU's outstanding loads are full), which delays the
-    // norm by more than the earlier loads save (measured on the 7B gate|up).
-    if (STAGED && n_stages > 1) load_stage(buf1, 1);
     float* as = reinterpret_cast<float*>(sm8 + K);
     int* am = reinterpret_cast<int*>(as + G);
     if (nlive) {
