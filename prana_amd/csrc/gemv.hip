@@ -784,7 +784,10 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
                                                         const int* __restrict__ sums, int n_tok) {
   int mi = 0, tile = blockIdx.x;
   if (!ACT) job_tile(job, &mi, &tile);
-  gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
+  // decode's one-token launches get a copy of the body in which the token
+  // loops fold away (the branch is uniform)
+  if (n_tok == 1) gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, 1, mi, tile);
+  else gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
 }
 
 // Matrices of two formats with the same unit width and tile geometry in one
