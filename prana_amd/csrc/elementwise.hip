@@ -97,6 +97,19 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restric
     if (tid == 0) s_ss = exact::lane_seq_sum_padded(sq, dim);
     __syncthreads();
     ss = s_ss;
+  } else if (dim <= 4 * kNormNT) {
+    // four consecutive squares per lane, folded from registers
+    float t4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = 4 * tid + j;
+      const float v = i < dim ? xs[exact::run_pad(i)] : 0.0f;
+      t4[j] = v * v;
+    }
+    ss = exact::quad_seq_sum<kNormNT>(t4, dim, [xs](int i) {
+      const float v = xs[exact::run_pad(i)];
+      return v * v;
+    });
   } else {
     ss = exact::block_seq_sum_short<kNormNT>(
         [xs](int i) {

@@ -685,6 +685,180 @@ __device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
   return group_seq_sum_short<NT, 1>(term, n);
 }
 
+// The predicted-binade fold for terms held in registers, four consecutive
+// terms per lane: lane t holds t4[k] = term(4t + k), zero past n, with
+// n <= 4 * NT (blockDim.x == NT, NT a multiple of 64, all lanes call it).
+// Lanes 0..7 hold the kPredHead = 32 head terms, which wave 0 folds serially
+// (read lane by lane); lane t >= 8 owns steps 4t .. 4t+3. Differences from
+// group_seq_sum_pred: no term is read from memory; the binade code of the
+// partial sum between two lanes is taken from one value both of them compute
+// with the same operations (the later lane's approximate entry sum), so the
+// lanes need not exchange their last codes (one barrier fewer); and the lane
+// that owns a crossing records the segment ending before it. The walk and
+// its verification are the same, and so is the fallback: non-finite terms,
+// more than kPredMaxCross crossings or a failed check fold term(0..n) on one
+// lane (term reads memory the whole workgroup sees). Every lane returns the
+// fold; four workgroup barriers (five on the fallback).
+template <int NT, class Term>
+__device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term term) {
+  static_assert(NT % 64 == 0 && NT / 64 <= 16, "whole waves, at most 16");
+  constexpr int W = NT / 64;
+  __shared__ float s_fw[W];
+  __shared__ int s_sw[3 * W];
+  __shared__ int s_tot[2 * (kPredMaxCross + 1)];
+  __shared__ float s_ct[kPredMaxCross + 1];
+  __shared__ int s_ce[kPredMaxCross + 1];
+  __shared__ float s_head, s_res;
+  __shared__ int s_ok;
+  const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < 4; k++) bad |= !(t4[k] <= 3.4028234663852886e38f);  // zero past n: finite
+  // the head: term(0 .. min(n, 32)) left to right, read from lanes 0..7
+  if (wave == 0) {
+    float h = -0.0f;
+#pragma unroll
+    for (int j = 0; j < kPredHead / 4; j++)
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t4[k]), j));
+        if (4 * j + k < n) h += v;
+      }
+    if (lane == 0) s_head = h;
+  }
+  const int nv = tid < kPredHead / 4 ? 0 : max(0, min(4, n - 4 * tid));
+  // pass 1: approximate prefix sums (only the grids depend on them)
+  const float ls = nv > 0 ? (t4[0] + t4[1]) + (t4[2] + t4[3]) : 0.0f;
+  const float inc = scan_add_f32(ls);
+  if (lane == 63) s_fw[wave] = inc;
+  const bool any_bad = group_or<1>(bad);  // barrier 1: also publishes s_fw and s_head
+  const float sH = s_head;
+  float result = sH;
+  bool ok = !any_bad;
+  if (ok && n > kPredHead) {
+    const int R = pred_margin(n);
+    const float tw = row_scan_add_f32(lane < W ? s_fw[lane] : 0.0f);
+    const float pre = wave > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), wave - 1)) : 0.0f;
+    const float P0 = sH + (pre + __int_as_float(wave_shr1(__float_as_int(inc))));
+    // the next lane's entry, by the same operations as that lane computes it
+    const float pre_n = wave + 1 < W ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), wave)) : 0.0f;
+    const float P0n = lane < 63 ? sH + (pre + inc) : sH + (pre_n + 0.0f);
+    const bool next_steps = 4 * (tid + 1) < n;  // the next lane owns steps (tid + 1 >= 8 here when nv > 0)
+    // pass 2: codes, crossings and increment pairs of this lane's steps
+    int ec[4];
+    bool cross[4];
+    Pair pr[4];
+    SegAcc loc{Pair{0, 0}, 0};
+    {
+      float P = P0;
+      int ein = binade_code(P0, R);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        P += t4[k];
+        const bool last = k == nv - 1;
+        ec[k] = last && next_steps ? binade_code(P0n, R) : binade_code(P, R);
+        cross[k] = k < nv && seg_break(ec[k], ein);
+        pr[k] = k < nv && !cross[k] ? term_pair_fast(t4[k], ec[k]) : Pair{0, 0};
+        if (k < nv) {
+          if (cross[k]) {
+            loc.p = Pair{0, 0};
+            loc.c += 1;
+          } else {
+            loc.p = compose(loc.p, pr[k]);
+          }
+        }
+        ein = ec[k];
+      }
+    }
+    const SegAcc incs = scan_seg(loc);
+    if (lane == 63) {
+      s_sw[3 * wave] = incs.p.e;
+      s_sw[3 * wave + 1] = incs.p.o;
+      s_sw[3 * wave + 2] = incs.c;
+    }
+    __syncthreads();  // barrier 2
+    SegAcc run{Pair{0, 0}, 0}, all;
+    {
+      const SegAcc tws = row_scan_seg(lane < W ? SegAcc{Pair{s_sw[3 * lane], s_sw[3 * lane + 1]}, s_sw[3 * lane + 2]}
+                                              : SegAcc{Pair{0, 0}, 0});
+      auto pick = [&](int w) {
+        return SegAcc{Pair{__builtin_amdgcn_readlane(tws.p.e, w), __builtin_amdgcn_readlane(tws.p.o, w)},
+                      __builtin_amdgcn_readlane(tws.c, w)};
+      };
+      if (wave > 0) run = pick(wave - 1);
+      all = pick(W - 1);
+    }
+    run = seg_combine(run, SegAcc{Pair{wave_shr1(incs.p.e), wave_shr1(incs.p.o)}, wave_shr1(incs.c)});
+    // records: a crossing closes the segment before it; the lane of the last
+    // step closes the last segment
+    if (all.c <= kPredMaxCross && nv > 0) {
+      SegAcc r = run;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if (k < nv) {
+          if (cross[k]) {
+            s_tot[2 * r.c] = r.p.e;
+            s_tot[2 * r.c + 1] = r.p.o;
+            r.c += 1;
+            s_ct[r.c] = t4[k];
+            s_ce[r.c] = ec[k];
+            r.p = Pair{0, 0};
+          } else {
+            r.p = compose(r.p, pr[k]);
+          }
+        }
+      }
+      if (4 * tid + nv == n) {
+        s_tot[2 * r.c] = r.p.e;
+        s_tot[2 * r.c + 1] = r.p.o;
+      }
+    }
+    __syncthreads();  // barrier 3
+    // the walk (group_seq_sum_pred's): wave 0 holds segment j in lane j
+    if (wave == 0) {
+      const int K = all.c;
+      bool good = K <= kPredMaxCross;
+      const int jl = min(lane, kPredMaxCross);
+      const int te = s_tot[2 * jl], to = s_tot[2 * jl + 1], ce = s_ce[jl];
+      const float ct = s_ct[jl];
+      float val = sH;
+      int E = binade_fast(sH);
+      for (int j = 0; good && j <= K; j++) {
+        if (j > 0) {
+          val = val + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct), j));
+          E = __builtin_amdgcn_readlane(ce, j);
+          good = val <= 3.4028234663852886e38f;
+        }
+        if (E == kPredAmb) continue;  // an ambiguous crossing: its segment is empty
+        int e;
+        int32_t m;
+        decompose(val, &e, &m);
+        const int32_t me = apply(Pair{__builtin_amdgcn_readlane(te, j), __builtin_amdgcn_readlane(to, j)}, m);
+        good = good && e == E && me < (1 << 24);
+        val = static_cast<float>(me) * ldexpf(1.0f, E - 23);
+      }
+      if (lane == 0) {
+        s_res = val;
+        s_ok = good;
+      }
+    }
+    __syncthreads();  // barrier 4
+    ok = s_ok != 0;
+    result = s_res;
+  }
+  if (!ok) {  // non-finite terms or a failed prediction: one lane's chain
+    __syncthreads();  // every read of s_res above is done
+    if (tid == 0) {
+      float s = -0.0f;
+      for (int i = 0; i < n; i++) s += term(i);
+      s_res = s;
+    }
+    __syncthreads();
+    result = s_res;
+  }
+  return result;
+}
+
 constexpr int kPadSerialMax = 896;
 template <int NT, bool PADDED, int CMAX = 16>
 __device__ __forceinline__ float block_seq_sum_nonneg(const float* a, int n) {

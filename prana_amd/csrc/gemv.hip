@@ -570,13 +570,15 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     }
     __builtin_amdgcn_sched_barrier(0);
     load_stage(buf0, 0);
-    __syncthreads();
-    const float ss = exact::block_seq_sum_short<NT>(
-        [xs](int i) {
-          const float v = xs[exact::run_pad(i)];
-          return v * v;
-        },
-        K);
+    // the squares from registers; the staged row serves the sum's one-lane
+    // fallback only (its first barrier publishes it)
+    float t4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) t4[j] = nlive && 4 * tid + j < K ? nx[j] * nx[j] : 0.0f;
+    const float ss = exact::quad_seq_sum<NT>(t4, K, [xs](int i) {
+      const float v = xs[exact::run_pad(i)];
+      return v * v;
+    });
     const float mean_sq = ss / static_cast<float>(K);
     const float inv = 1.0f / sqrtf(mean_sq + job.nin.eps);
     // The second stage goes out once the sum is done: its registers are
