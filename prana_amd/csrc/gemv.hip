@@ -1478,7 +1478,6 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
     const uint8_t* wrow = b + wr_row * L::WSTR + 8 * h;
     const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + wr_row * L::DSTR;
     const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + 4 * h;
-    const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + 4 * h;
     const int nlive = min(L::CB, G - c * L::CB);  // uniform
 #pragma unroll
     for (int bb = 0; bb < L::CB; bb++) {
@@ -1487,9 +1486,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
       const long a2 = *reinterpret_cast<const long*>(arow + bb * 32 + 16);
       long b1, b2;
       if constexpr (KIND == kKindQ4_0) {
+        // nibbles n -> signed bytes n - 8, so the matrix cores give
+        // isum - 8*sum_a itself: ((n | 0x80) - 8) ^ 0x80 per byte, with no
+        // borrow between bytes (every byte is >= 0x80 before the subtract)
+        constexpr long kLo = 0x0F0F0F0F0F0F0F0FL, kHi = static_cast<long>(0x8080808080808080UL),
+                       k8 = 0x0808080808080808L;
         const long w = *reinterpret_cast<const long*>(wrow + bb * 16);
-        b1 = w & 0x0F0F0F0F0F0F0F0FL;
-        b2 = (w >> 4) & 0x0F0F0F0F0F0F0F0FL;
+        b1 = (((w & kLo) | kHi) - k8) ^ kHi;
+        b2 = ((((w >> 4) & kLo) | kHi) - k8) ^ kHi;
       } else {
         b1 = *reinterpret_cast<const long*>(wrow + bb * 32);
         b2 = *reinterpret_cast<const long*>(wrow + bb * 32 + 16);
@@ -1501,13 +1505,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
 #pragma unroll
       for (int g = 0; g < 4; g++) {  // tokens 8g + 4h + e of the tile hold values v = 4g + e
         const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * kMmaToks + 8 * g);
-        const int4 m4 = *reinterpret_cast<const int4*>(smb + bb * kMmaToks + 8 * g);
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-        const int mv[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          int isum = cc[4 * g + e];
-          if constexpr (KIND == kKindQ4_0) isum -= 8 * mv[e];
+          const int isum = cc[4 * g + e];  // Q4_0: already less 8*sum_a (signed weights)
           acc[4 * g + e] += d * sv[e] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
         }
       }
@@ -1686,29 +1687,27 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
     const uint8_t* wrow = b + (rtile * 16 + j) * L::WSTR + (KIND == kKindQ4_0 ? 8 * (kg & 1) : 8 * kg);
     const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + (rtile * 16 + j) * L::DSTR;
     const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + ttile * 16 + 4 * kg;
-    const int* smb = reinterpret_cast<const int*>(b + L::SM_OFF) + ttile * 16 + 4 * kg;
     const int nlive = min(kSkCB, G - c * kSkCB);  // uniform
 #pragma unroll
     for (int bb = 0; bb < kSkCB; bb++) {
       const long av = *reinterpret_cast<const long*>(arow + bb * 32);
       long wb = *reinterpret_cast<const long*>(wrow + bb * L::QB);
-      if constexpr (KIND == kKindQ4_0)
-        wb = kg < 2 ? (wb & 0x0F0F0F0F0F0F0F0FL) : ((wb >> 4) & 0x0F0F0F0F0F0F0F0FL);
+      if constexpr (KIND == kKindQ4_0) {
+        // signed nibbles n - 8 (as gemm_mfma_kernel): the product is isum - 8*sum_a
+        constexpr long kLo = 0x0F0F0F0F0F0F0F0FL, kHi = static_cast<long>(0x8080808080808080UL),
+                       k8 = 0x0808080808080808L;
+        wb = kg < 2 ? (wb & kLo) : ((wb >> 4) & kLo);
+        wb = ((wb | kHi) - k8) ^ kHi;
+      }
       const v4i_t z = {0, 0, 0, 0};
       const v4i_t cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wb, z, 0, 0, 0);
       const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
       const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * L::TOKS);
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-      int mv[4] = {0, 0, 0, 0};
-      if constexpr (KIND == kKindQ4_0) {
-        const int4 m4 = *reinterpret_cast<const int4*>(smb + bb * L::TOKS);
-        mv[0] = m4.x, mv[1] = m4.y, mv[2] = m4.z, mv[3] = m4.w;
-      }
       const bool live = bb < nlive;
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        int isum = cc[v];
-        if constexpr (KIND == kKindQ4_0) isum -= 8 * mv[v];
+        const int isum = cc[v];
         const float t = acc[v] + d * sv[v] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
         acc[v] = live ? t : acc[v];
       }
