@@ -131,15 +131,15 @@ __device__ __forceinline__ VPieces fetch_v(const HeadJob& J, int t0, int nr, int
 }
 
 template <bool F16>
-__device__ __forceinline__ void make_products(const VPieces& v, const float* sc, int t0, int nr, int ppr, int ch,
-                                              float* prod) {
+__device__ __forceinline__ void make_products(const VPieces& v, const float* sc, float inv, int t0, int nr, int ppr,
+                                              int ch, float* prod) {
   using T = typename Elem<F16>::T;
   constexpr int EPV = 16 / sizeof(T);
   const int stride = ch + 4;
   auto one = [&](const uint4& w, int p) {
     const int row = p / ppr, col = p - (p / ppr) * ppr;
     if (row >= nr) return;
-    const float pt = sc[t0 + row];
+    const float pt = sc[t0 + row] * inv;  // the softmax's p_t = e_t * (1/sum)
     float x[EPV];
     if constexpr (F16) {
       const uint32_t u[4] = {w.x, w.y, w.z, w.w};
@@ -264,8 +264,7 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
   // softmax sum in the reference's left-to-right order (norms.rs:53)
   const float sum = exact::block_seq_sum_nonneg<kNT, SC_LDS>(sc, n);
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  for (int t = tid; t < n; t += kNT) sc[t] = sc[t] * inv;
-  __syncthreads();
+  // p_t = e_t * inv is formed where the P.V products use it (no pass of its own)
 
   // ---- PV over dims [d0, d0+dw): lane d folds dim d0 + d
   const int d = tid;
@@ -274,7 +273,7 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
   if (J.vec) {
     const int stride = ch + 4;
     const int n_chunks = (n + ch - 1) / ch;
-    make_products<F16>(v, sc, 0, min(ch, n), ppr, ch, L.prod);
+    make_products<F16>(v, sc, inv, 0, min(ch, n), ppr, ch, L.prod);
     if (n_chunks > 1) v = fetch_v<F16>(J, ch, min(ch, n - ch), ppr);
     __syncthreads();
     for (int c = 0; c < n_chunks; c++) {
@@ -293,14 +292,14 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
       }
       if (c + 1 < n_chunks) {
         const int t1 = t0 + ch;
-        make_products<F16>(v, sc, t1, min(ch, n - t1), ppr, ch, L.prod + ((c + 1) & 1) * kProdFloats);
+        make_products<F16>(v, sc, inv, t1, min(ch, n - t1), ppr, ch, L.prod + ((c + 1) & 1) * kProdFloats);
         if (c + 2 < n_chunks) v = fetch_v<F16>(J, t1 + ch, min(ch, n - t1 - ch), ppr);
       }
       __syncthreads();
     }
   } else if (folder) {
     const T* vb = static_cast<const T*>(J.v) + (size_t)J.kvh * J.hd + J.d0 + d;
-    for (int t = 0; t < n; t++) acc += sc[t] * Elem<F16>::get(vb[(size_t)t * J.kv_stride]);
+    for (int t = 0; t < n; t++) acc += (sc[t] * inv) * Elem<F16>::get(vb[(size_t)t * J.kv_stride]);
   }
   if (folder) J.dst[J.h * J.hd + J.d0 + d] = acc;
   if (J.qd && folder) {  // the folders are whole 32-lane groups here
