@@ -433,7 +433,8 @@ struct DecodeJob {
 
 constexpr int kDecMaxTok = 8;   // tokens per launch (LDS and folder lanes permitting)
 constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: one quantization block
-constexpr int kNormNT = 1024;    // lanes of a NORM workgroup (one per CU: the norm runs once per CU)
+constexpr int kNormNT = 1024;    // lanes of a NORM workgroup for rows of 1025..4096 values (one per CU)
+constexpr int kNormNTSmall = 256;  // ... for rows of 513..1024 values
 constexpr int kNormMaxK = 4096;  // NORM rows: four values per lane
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
@@ -447,7 +448,7 @@ __device__ __forceinline__ void job_tile(const DecodeJob& job, int* mi, int* til
   while (*mi < job.n_mats - 1 && *tile >= job.tiles[*mi]) *tile -= job.tiles[(*mi)++];
 }
 
-// NORM (one token, NT == kNormNT): the activations are rmsnorm(job.nin.x)
+// NORM (one token, K <= 4 * NT): the activations are rmsnorm(job.nin.x)
 // quantized, as launch_rmsnorm would produce them, computed in the prologue
 // while this workgroup's first weight loads are in flight; the row and the
 // sum's terms use the term region of LDS, which the fold reuses afterwards.
@@ -455,7 +456,7 @@ template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false>
 __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_t* __restrict__ q,
                                                const float* __restrict__ sa, const int* __restrict__ sums,
                                                int n_tok, int mi, int tile) {
-  static_assert(!NORM || NT == kNormNT, "NORM workgroups have kNormNT lanes");
+  static_assert(!NORM || NT == kNormNT || NT == kNormNTSmall, "NORM workgroups of 256 or 1024 lanes");
   if constexpr (NORM) n_tok = 1;  // a constant the token loops fold away
   extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
@@ -527,7 +528,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   int4 a0w[NORM ? 1 : kAw4];
   float a0s[NORM ? 1 : kAg];
   int a0m[NORM ? 1 : kAg];
-  // NORM: elements 4*tid .. 4*tid+3 of the row (K <= 4*NT, K % 32 == 0)
+  // NORM: elements 4*tid .. 4*tid+3 of the row (K <= 4 * NT, K % 32 == 0)
   const bool nlive = NORM && 4 * tid < K;
   float4 nx4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), nw4 = nx4;
   if constexpr (NORM) {
@@ -796,16 +797,16 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
 // launch (a fused Q|K|V whose v projection is stored in another format, as
 // K-quant-mixture GGUF files store it): each workgroup runs the body of its
 // matrix's format.
-template <int KA, int KB, int U, bool STAGED, int NT>
+template <int KA, int KB, int U, bool STAGED, int NT, bool NORM = false>
 __global__ __launch_bounds__(NT) void gemv_tile_mixed_kernel(DecodeJob job, const int8_t* __restrict__ q,
                                                               const float* __restrict__ sa,
                                                               const int* __restrict__ sums, int n_tok) {
   int mi, tile;
   job_tile(job, &mi, &tile);
   if (job.m[mi].kind == KA)
-    gemv_tile_body<KA, U, false, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+    gemv_tile_body<KA, U, false, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
   else
-    gemv_tile_body<KB, U, false, STAGED, NT>(job, q, sa, sums, n_tok, mi, tile);
+    gemv_tile_body<KB, U, false, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
 }
 
 // ---- verify batches: 2..8 tokens, 32-element formats
@@ -1014,10 +1015,12 @@ TileGeom choose_geom(size_t K, bool act) {
 template <int KIND>
 TileGeom norm_geom(size_t K) {
   const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
-  if (RegUnit<KIND>::kElems != 32 || nb < 1) return TileGeom{0, 0, 0, 0};
-  for (int u : {4, 2}) {
-    const int units = kNormNT * u;
-    if (units % nb == 0 && units / nb >= 8 && units / nb <= 64) return TileGeom{u, units / nb, nb, kNormNT};
+  if (RegUnit<KIND>::kElems != 32 || nb < 1 || K <= 512 || K > static_cast<size_t>(kNormMaxK)) return TileGeom{0, 0, 0, 0};
+  const int nt = K > 1024 ? kNormNT : kNormNTSmall;
+  for (int u : {4, 2, 7}) {
+    if (nt == kNormNT && u == 7) continue;  // not instantiated at 1024 lanes
+    const int units = nt * u;
+    if (units % nb == 0 && units / nb >= 8 && units / nb <= 64) return TileGeom{u, units / nb, nb, nt};
   }
   return TileGeom{0, 0, 0, 0};
 }
@@ -1028,8 +1031,10 @@ TileGeom norm_geom(size_t K) {
 template <int KIND>
 TileGeom norm_act_geom(size_t K) {
   const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
-  if (RegUnit<KIND>::kElems != 32 || nb < 64 || nb % 32 != 0) return TileGeom{0, 0, 0, 0};
-  return TileGeom{4, 64, 32, kNormNT};
+  if (RegUnit<KIND>::kElems != 32 || K <= 512 || K > static_cast<size_t>(kNormMaxK)) return TileGeom{0, 0, 0, 0};
+  if (K > 1024) return nb % 32 == 0 ? TileGeom{4, 64, 32, kNormNT} : TileGeom{0, 0, 0, 0};
+  // 256 lanes, one stage of whole 64-row tiles: nb/2 units per lane
+  return nb == 28 || nb == 32 ? TileGeom{nb / 2, 64, nb, kNormNTSmall} : TileGeom{0, 0, 0, 0};
 }
 
 // KB >= 0: the matrices come in two formats, KIND and KB, with the same tile
@@ -1039,11 +1044,10 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
                   size_t n_tok, hipStream_t s) {
   using R = RegUnit<KIND>;
   static_assert(KB < 0 || !ACT, "two formats only outside act mode");
-  static_assert(!NORM || KB < 0, "NORM launches take one format");
   constexpr int kTpuMax = KB < 0 ? R::kTpu : std::max(R::kTpu, RegUnit<(KB < 0 ? KIND : KB)>::kTpu);
   const void* const fn = KB < 0 ? reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>)
                                 : reinterpret_cast<const void*>(
-                                      gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>);
+                                      gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT, NORM>);
   DecodeJob job = job0;
   job.rt = g.rt;
   job.sb = g.sb;
@@ -1062,7 +1066,7 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   // NORM: the row staged for the sum of squares shares the term region
   const size_t norm_bytes = NORM ? (static_cast<size_t>(exact::run_pad(static_cast<int>(K) - 1)) + 1) * 4 : 0;
   const size_t per_tok = astride + std::max(term_bytes, norm_bytes);
-  PRANA_CHECK(!NORM || (n_tok == 1 && K <= static_cast<size_t>(kNormMaxK) && K % 32 == 0 && job.nin.x &&
+  PRANA_CHECK(!NORM || (n_tok == 1 && K <= static_cast<size_t>(4 * NT) && K % 32 == 0 && job.nin.x &&
                         job.nin.w && reinterpret_cast<uintptr_t>(job.nin.x) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(job.nin.w) % 16 == 0),
               "gemv: a fused rmsnorm takes one 16-byte-aligned token of at most 4096 values (a multiple of 32)");
@@ -1097,8 +1101,8 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     const size_t G = K / 32;
     LaunchEvents& le = launch_events();
     if constexpr (KB >= 0) {
-      hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT>), dim3(total), dim3(NT),
-                         nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT, NORM>), dim3(total),
+                         dim3(NT), nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     } else if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
       hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>), dim3(total), dim3(NT), nt * per_tok,
                             s, le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
@@ -2085,9 +2089,16 @@ static int device_cus() {
 bool gemv_norm_fusable(const DevMat* ms, int n) {
   if (n < 1 || n > 3) return false;
   const size_t K = ms[0].cols;
-  for (int i = 0; i < n; i++)
-    if (ms[i].kind != ms[0].kind || ms[i].cols != K) return false;
-  if (K <= 1024 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
+  bool one_kind = true;
+  for (int i = 0; i < n; i++) {
+    if (ms[i].cols != K) return false;
+    one_kind = one_kind && ms[i].kind == ms[0].kind;
+  }
+  if (K <= 512 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
+  // two formats: the block-32 pair, at 256 lanes (rows of at most 1024 values)
+  if (!one_kind && (K > 1024 || mixed_pair(ms, n) != std::make_pair(static_cast<int>(kKindQ4_0),
+                                                                     static_cast<int>(kKindQ8_0))))
+    return false;
   const int kind = ms[0].kind;
   if (kind != kKindQ8F && kind != kKindQ8_0 && kind != kKindQ4_0) return false;
   size_t tiles = 0;
@@ -2117,6 +2128,8 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
     }
     job.n_mats = n;
     job.nin = *norm;
+    bool mixed = false;
+    for (int i = 1; i < n; i++) mixed = mixed || ms[i].kind != ms[0].kind;
     return dispatch_kind(ms[0].kind, [&](auto k) {
       constexpr int KIND = decltype(k)::value;
       if constexpr (RegUnit<KIND>::kElems == 32) {
@@ -2128,8 +2141,19 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
           job.rk = *rk;
           if (fused) *fused = true;
         }
-        if (g.u == 4) return launch_tile_u<KIND, 4, false, false, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
-        if (g.u == 2) return launch_tile_u<KIND, 2, false, false, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+        constexpr int B = kNormNT, S = kNormNTSmall;
+        if (mixed) {  // Q4_0 with Q8_0 (gemv_norm_fusable), 256 lanes
+          constexpr int KA = kKindQ4_0, KB = kKindQ8_0;
+          if (g.nt == S && g.u == 7) return launch_tile_u<KA, 7, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 4) return launch_tile_u<KA, 4, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 2) return launch_tile_u<KA, 2, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+        } else {
+          if (g.nt == B && g.u == 4) return launch_tile_u<KIND, 4, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == B && g.u == 2) return launch_tile_u<KIND, 2, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 7) return launch_tile_u<KIND, 7, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 4) return launch_tile_u<KIND, 4, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 2) return launch_tile_u<KIND, 2, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+        }
       }
       return fail(kErrInvalid, "gemv_multi: no fused-rmsnorm tile geometry");
     });
@@ -2197,7 +2221,7 @@ bool gemv_multi_fusable(const DevMat* ms, int n) {
 bool gemv_norm_act_fusable(const DevMat& gate, const DevMat& up) {
   if (gate.kind != up.kind || gate.rows != up.rows || gate.cols != up.cols) return false;
   const size_t K = gate.cols;
-  if (K <= 1024 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
+  if (K <= 512 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0) return false;
   if (gate.kind != kKindQ8F && gate.kind != kKindQ8_0 && gate.kind != kKindQ4_0) return false;
   int rt = 0;
   dispatch_kind(gate.kind, [&](auto k) {
@@ -2231,7 +2255,9 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
       constexpr int KIND = decltype(k)::value;
       if constexpr (RegUnit<KIND>::kElems == 32) {
         const TileGeom g = norm_act_geom<KIND>(gate.cols);
-        return launch_tile_u<KIND, 4, true, true, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+        if (g.nt == kNormNT) return launch_tile_u<KIND, 4, true, true, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
+        if (g.u == 14) return launch_tile_u<KIND, 14, true, false, kNormNTSmall, -1, true>(job, g, q, sa, sums, 1, s);
+        if (g.u == 16) return launch_tile_u<KIND, 16, true, false, kNormNTSmall, -1, true>(job, g, q, sa, sums, 1, s);
       }
       return fail(kErrInvalid, "gemv_act: no fused-rmsnorm tile geometry");
     });

@@ -302,16 +302,20 @@ def test_mixed_format_qkv_one_launch_bitexact(dim):
             assert np.array_equal(gc.read(layer, which, 17), oc.read(layer, which, 17)), (layer, which)
 
 
-@pytest.mark.parametrize("ty,dim,hd,neox", [("Q4_0", 2048, 64, 1), ("Q8_0", 4096, 128, 1), ("Q8_0", 4096, 128, 0)])
+@pytest.mark.parametrize("ty,dim,hd,neox", [("Q4_0", 2048, 64, 1), ("Q8_0", 4096, 128, 1), ("Q8_0", 4096, 128, 0),
+                                             ("Q4_0", 896, 64, 1), ("Q8_0", 1024, 64, 0)])
 def test_fused_norm_decode_bitexact(ty, dim, hd, neox):
     # Decode rows of 1024 < dim <= 4096 let the Q|K|V and gate|up launches
     # normalise x themselves (one 1024-lane workgroup per tile; Q|K|V tiles of
     # 64 rows at 2048 and 32 rows at 4096, gate|up tiles of 64 rows of each
     # matrix, h quantized in the epilogue). NeoX pairs span whole heads, so at
     # hd 128 the 32-row tiles leave RoPE to its own launch; at hd 64, and for
-    # adjacent pairs, it rides in the same launch.
+    # adjacent pairs, it rides in the same launch. Rows of 513-1024 values take
+    # 256-lane workgroups (Q|K|V tiles of 64 rows at 896 and 32 at 1024,
+    # gate|up tiles of 64 rows with 14 or 16 units per lane).
     kind = {"Q4_0": M.Q4_0, "Q8_0": M.Q8_0}[ty]
-    cfg = M.config(dim, 1024, 2, dim // hd, 4, 500, 64, head_dim=hd, rope_neox=neox)
+    n_kv = 4 if (dim // hd) % 4 == 0 else 2
+    cfg = M.config(dim, 1024, 2, dim // hd, n_kv, 500, 64, head_dim=hd, rope_neox=neox)
     t = M.synth_tensors(cfg, lambda name, cols: kind, 90 + dim + neox, biases=True)
     g, o = pair(cfg, t)
     gc, oc = g.cache(64), o.cache(64)
