@@ -2083,9 +2083,10 @@ static int device_cus() {
 }
 
 // A fused rmsnorm pays the norm once per workgroup, so it is taken when one
-// kNormNT-lane workgroup per compute unit covers every tile: one format of
-// block-32 units, rows of 1024 < cols <= kNormMaxK (a multiple of 32) that
-// norm_geom tiles.
+// workgroup per compute unit covers every tile: block-32 units of one format
+// (or the Q4_0 / Q8_0 pair for rows of at most 1024 values), rows of
+// 512 < cols <= kNormMaxK (a multiple of 32) that norm_geom tiles, with 256
+// lanes up to 1024 values and kNormNT lanes beyond.
 bool gemv_norm_fusable(const DevMat* ms, int n) {
   if (n < 1 || n > 3) return false;
   const size_t K = ms[0].cols;

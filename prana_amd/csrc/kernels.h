@@ -147,7 +147,8 @@ struct NormIn {
   const float* w;
   float eps;
 };
-// Whether launch_gemv_multi can take these matrices with a NormIn (one token).
+// Whether launch_gemv_multi can take these matrices with a NormIn (one token):
+// block-32 formats, 512 < cols <= 4096, every tile's workgroup resident at once.
 bool gemv_norm_fusable(const DevMat* ms, int n);
 int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* q, const float* sa, const int* sums,
                       size_t n_tok, hipStream_t s, const RopeKv* rk = nullptr, bool* fused = nullptr,
