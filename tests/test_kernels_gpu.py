@@ -427,6 +427,31 @@ def test_attention_decode(nh, nkv, hd, pos):
     assert same_bits(P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd))
 
 
+@pytest.mark.parametrize("pos", [32, 510, 511, 512])
+def test_attention_decode_adversarial_softmax(pos):
+    # Around the softmax sum's one-lane / scan boundary (33 and 511-513 rows):
+    # a wide score spread (q scaled by 8: most exponentials underflow or are
+    # tiny beside a few large ones), a third of the K rows repeating row 0
+    # (equal terms meeting the running sum again and again: the tie-prone
+    # case of the exact sum) and zero K rows (scores of exactly 0); then an
+    # infinite q entry, whose head turns NaN: NaN in the same places, every
+    # other bit equal.
+    nh, nkv, hd = 32, 8, 128
+    kv = nkv * hd
+    kc, vc = _cache(pos + 1, nkv, hd, pos + 40)
+    r = rng(pos + 41)
+    krows = kc.reshape(pos + 1, kv)
+    krows[r.choice(pos + 1, (pos + 1) // 3, replace=False)] = krows[0].copy()
+    krows[r.choice(pos + 1, 4, replace=False)] = 0
+    q = (rng(pos + 42).standard_normal(nh * hd) * 8).astype(np.float32)
+    assert same_bits(P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd))
+    q[5] = np.inf
+    got, want = P.attention_decode(q, kc, vc, pos, nh, nkv, hd), O.attention_decode(q, kc, vc, pos, nh, nkv, hd)
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    assert np.array_equal(nan_g, nan_w) and nan_g[:hd].all()
+    assert same_bits(got[~nan_g], want[~nan_w])
+
+
 @pytest.mark.parametrize("pos", [300, 2500])
 def test_attention_decode_special_values(pos):
     # f16 K/V holding NaNs (quiet and signalling payloads), infinities, the
