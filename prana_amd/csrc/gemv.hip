@@ -1010,12 +1010,14 @@ TileGeom choose_geom(size_t K, bool act) {
   return TileGeom{1, 32, 8, 256};
 }
 
-// Tile geometry of a NORM launch (kNormNT lanes, whole rows per tile, 8..64
-// rows), or u == 0 when none fits. Block-32 kinds only.
+// Tile geometry of a NORM launch (kNormNT lanes for rows of more than 1024
+// values, kNormNTSmall up to 1024; whole rows per tile, 8..64 rows), or u == 0
+// when none fits. Block-32 kinds only.
 template <int KIND>
 TileGeom norm_geom(size_t K) {
   const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
-  if (RegUnit<KIND>::kElems != 32 || nb < 1 || K <= 512 || K > static_cast<size_t>(kNormMaxK)) return TileGeom{0, 0, 0, 0};
+  if (RegUnit<KIND>::kElems != 32 || nb < 1 || K <= 512 || K > static_cast<size_t>(kNormMaxK))
+    return TileGeom{0, 0, 0, 0};
   const int nt = K > 1024 ? kNormNT : kNormNTSmall;
   for (int u : {4, 2, 7}) {
     if (nt == kNormNT && u == 7) continue;  // not instantiated at 1024 lanes
@@ -1026,8 +1028,10 @@ TileGeom norm_geom(size_t K) {
 }
 
 // Act-mode (gate|up) geometry of a NORM launch: 64 rows of each matrix per
-// tile (whole 32-row blocks, so h is quantized in the epilogue), stages of 32
-// blocks, four units per lane; u == 0 when the rows do not split so.
+// tile (whole 32-row blocks, so h is quantized in the epilogue); beyond 1024
+// values kNormNT lanes in stages of 32 blocks, four units per lane, up to
+// 1024 values kNormNTSmall lanes in one stage (rows of 28 or 32 blocks); u == 0
+// when the rows do not split so.
 template <int KIND>
 TileGeom norm_act_geom(size_t K) {
   const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
@@ -2145,15 +2149,23 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
         constexpr int B = kNormNT, S = kNormNTSmall;
         if (mixed) {  // Q4_0 with Q8_0 (gemv_norm_fusable), 256 lanes
           constexpr int KA = kKindQ4_0, KB = kKindQ8_0;
-          if (g.nt == S && g.u == 7) return launch_tile_u<KA, 7, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == S && g.u == 4) return launch_tile_u<KA, 4, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == S && g.u == 2) return launch_tile_u<KA, 2, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 7)
+            return launch_tile_u<KA, 7, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 4)
+            return launch_tile_u<KA, 4, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 2)
+            return launch_tile_u<KA, 2, false, false, S, KB, true>(job, g, q, sa, sums, 1, s);
         } else {
-          if (g.nt == B && g.u == 4) return launch_tile_u<KIND, 4, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == B && g.u == 2) return launch_tile_u<KIND, 2, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == S && g.u == 7) return launch_tile_u<KIND, 7, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == S && g.u == 4) return launch_tile_u<KIND, 4, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
-          if (g.nt == S && g.u == 2) return launch_tile_u<KIND, 2, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == B && g.u == 4)
+            return launch_tile_u<KIND, 4, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == B && g.u == 2)
+            return launch_tile_u<KIND, 2, false, false, B, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 7)
+            return launch_tile_u<KIND, 7, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 4)
+            return launch_tile_u<KIND, 4, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
+          if (g.nt == S && g.u == 2)
+            return launch_tile_u<KIND, 2, false, false, S, -1, true>(job, g, q, sa, sums, 1, s);
         }
       }
       return fail(kErrInvalid, "gemv_multi: no fused-rmsnorm tile geometry");
