@@ -367,3 +367,28 @@ def test_c4_speculative_equals_plain_greedy(c4, k):
     spec2, st2 = P.generate_speculative(g, g, prompt, 12, k)
     assert list(spec2) == list(plain[:12])
     assert 0 < st2.accepted <= st2.proposed
+
+
+def test_gemv_profile_shapes_add_up():
+    # prana_gemv_profile_shapes splits the sampled decode GEMV launches by the
+    # weight bytes they stream; the split adds up to prana_gemv_profile_read's
+    # totals, and a reset clears it.
+    cfg = M.config(2048, 1024, 2, 32, 4, 500, 64, head_dim=64, rope_neox=1)
+    g = P.Model(cfg, M.synth_tensors(cfg, lambda name, cols: M.Q4_0, 77))
+    c = g.cache(32)
+    prompt = np.random.default_rng(77).integers(0, cfg["vocab_size"], 8).astype(np.uint32)
+    c.prefill(prompt[:4])
+    P.gemv_profile(True, period=1)
+    P.gemv_profile_read(reset=True)
+    tok = int(prompt[4])
+    for pos in range(4, 8):
+        tok = int(np.argmax(c.forward(tok, pos)))
+    shapes = P.gemv_profile_shapes()
+    n, sec, total_bytes = P.gemv_profile_read(reset=True)
+    P.gemv_profile(False)
+    assert n > 0 and sum(k for _, k, _ in shapes) == n
+    assert sum(b * k for b, k, _ in shapes) == total_bytes
+    assert abs(sum(t for _, _, t in shapes) - sec) <= 1e-9 * max(sec, 1.0)
+    assert len({b for b, _, _ in shapes}) == len(shapes) >= 4
+    assert all(k > 0 and t > 0 for _, k, t in shapes)
+    assert P.gemv_profile_shapes() == []
