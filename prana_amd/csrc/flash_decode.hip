@@ -10,8 +10,9 @@
 //            or V row of one KV head is read once, coalesced (hd/8 lanes x 16
 //            bytes), and serves the G query heads of its group: every lane
 //            holds 8 dims of q for each of them, the G partial dots of a row
-//            are reduced over its hd/8 lanes with DPP, and the tile's max,
-//            sum of exp(s - max) and P.V accumulators are kept per head.
+//            are reduced over its hd/8 lanes with DPP; each wave keeps its own
+//            max, sum of exp(s - max) and P.V per head in registers, and the
+//            four waves are merged once at the end of the tile.
 //   combine: one workgroup per (query head, sequence, 32 dims):
 //            M = max m_s, L = sum l_s exp(m_s - M),
 //            out = sum acc_s exp(m_s - M) / L, in parallel over splits.
@@ -99,8 +100,7 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
   constexpr int LPR = HD / 8;      // lanes per cache row
   constexpr int RPI = 64 / LPR;    // rows per wave per iteration
   constexpr int T = 4 * ITER * RPI;
-  __shared__ float s_p[G][T];
-  __shared__ float s_red[4][G];
+  __shared__ float s_m[4][G], s_l[4][G];
   __shared__ float s_acc[4][G][HD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = lane / LPR, sub = lane % LPR;
@@ -137,99 +137,97 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
     for (int k = 0; k < 8; k++) qv[g][k] *= a.scale;  // (q/sqrt(hd)).k
   }
   const bool full = r0 + T <= n;  // uniform: no row of the tile lies past the window
-  // scores
-  float mx[G];
+  // scores: after the group sum every lane of a row's group holds its G dots
+  float sc[G][ITER], mx[G];
 #pragma unroll
   for (int g = 0; g < G; g++) mx[g] = -INFINITY;
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     float k8[8];
     halves8(kr[it], k8);
-    const int row = wrow0 + it * RPI;
-    const int lr = row - r0;
+    const bool valid = full || wrow0 + it * RPI < n;
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float d = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; k++) d = fmaf(qv[g][k], k8[k], d);
       d = group_sum<LPR>(d);
-      const bool valid = full || row < n;
-      if (sub == 0) s_p[g][lr] = valid ? d : -INFINITY;
-      mx[g] = valid ? fmaxf(mx[g], d) : mx[g];
+      sc[g][it] = valid ? d : -INFINITY;
+      mx[g] = fmaxf(mx[g], sc[g][it]);
     }
   }
+  // each wave keeps its own softmax state (max, sum of exp(s - max), P.V);
+  // the four are merged once at the end
+  float ls[G], acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    float m = mx[g];
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if (lane == 0) s_red[wave][g] = m;
-  }
-  __syncthreads();
-  float m_g[G];
 #pragma unroll
-  for (int g = 0; g < G; g++) m_g[g] = fmaxf(fmaxf(s_red[0][g], s_red[1][g]), fmaxf(s_red[2][g], s_red[3][g]));
-  // probabilities of the tile (relative to its own max) and their sums
-  float lsum[G];
+    for (int o = LPR; o < 64; o <<= 1) mx[g] = fmaxf(mx[g], __shfl_xor(mx[g], o, 64));
+    // a wave whose rows all lie past the window has max -inf: its
+    // probabilities are exp(-inf) = 0 against a reference of 0
+    const float mref = mx[g] == -INFINITY ? 0.0f : mx[g];
+    ls[g] = 0.0f;
 #pragma unroll
-  for (int g = 0; g < G; g++) {
-    float l = 0.0f;
-    for (int r = tid; r < T; r += kFdNT) {
-      const float p = __expf(s_p[g][r] - m_g[g]);  // exp(-inf) = 0 past the window
-      s_p[g][r] = p;
-      l += p;
+    for (int it = 0; it < ITER; it++) {
+      sc[g][it] = __expf(sc[g][it] - mref);
+      ls[g] += sc[g][it];
     }
-    lsum[g] = l;
-  }
-  __syncthreads();  // s_red is reused below, s_p holds probabilities
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    float l = lsum[g];
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-    if (lane == 0) s_red[wave][g] = l;
-  }
-  // P.V over this lane group's rows
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; g++)
 #pragma unroll
     for (int k = 0; k < 8; k++) acc[g][k] = 0.0f;
+  }
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
-    const int row = wrow0 + it * RPI;
-    if (full || row < n) {
+    if (full || wrow0 + it * RPI < n) {
       float v8[8];
       halves8(vr[it], v8);
-      const int lr = row - r0;
 #pragma unroll
-      for (int g = 0; g < G; g++) {
-        const float p = s_p[g][lr];
+      for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc[g][k] = fmaf(p, v8[k], acc[g][k]);
-      }
+        for (int k = 0; k < 8; k++) acc[g][k] = fmaf(sc[g][it], v8[k], acc[g][k]);
     }
   }
-  // sum the wave's lane groups (lanes LPR apart), then the four waves
+  // sum the wave's lane groups (lanes LPR apart)
 #pragma unroll
   for (int o = LPR; o < 64; o <<= 1)
 #pragma unroll
-    for (int g = 0; g < G; g++)
+    for (int g = 0; g < G; g++) {
+      ls[g] += __shfl_xor(ls[g], o, 64);
 #pragma unroll
       for (int k = 0; k < 8; k++) acc[g][k] += __shfl_xor(acc[g][k], o, 64);
+    }
   if (rg == 0)
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
       for (int k = 0; k < 8; k++) s_acc[wave][g][sub * 8 + k] = acc[g][k];
+  if (lane == 0)
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      s_m[wave][g] = mx[g];
+      s_l[wave][g] = ls[g];
+    }
   __syncthreads();
+  // merge the waves: M = max m_w, each state scaled by exp(m_w - M) (0 for a
+  // wave past the window; wave 0 holds row r0 < n, so M is finite)
   float* base = a.part + (((size_t)seq * a.n_heads + h0) * a.max_splits + split) * (HD + 2);
   const size_t hstride = (size_t)a.max_splits * (HD + 2);
   for (int e = tid; e < G * HD; e += kFdNT) {
     const int g = e / HD, d = e % HD;
-    base[g * hstride + d] = (s_acc[0][g][d] + s_acc[1][g][d]) + (s_acc[2][g][d] + s_acc[3][g][d]);
+    const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+      if (s_m[w][g] != -INFINITY) o = fmaf(s_acc[w][g][d], __expf(s_m[w][g] - M), o);
+    base[g * hstride + d] = o;
   }
   if (tid < G) {
-    base[tid * hstride + HD] = m_g[tid];
-    base[tid * hstride + HD + 1] = (s_red[0][tid] + s_red[1][tid]) + (s_red[2][tid] + s_red[3][tid]);
+    const float M = fmaxf(fmaxf(s_m[0][tid], s_m[1][tid]), fmaxf(s_m[2][tid], s_m[3][tid]));
+    float l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+      if (s_m[w][tid] != -INFINITY) l = fmaf(s_l[w][tid], __expf(s_m[w][tid] - M), l);
+    base[tid * hstride + HD] = M;
+    base[tid * hstride + HD + 1] = l;
   }
 }
 
