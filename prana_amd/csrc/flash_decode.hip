@@ -69,6 +69,14 @@ struct FlashArgs {
   float* part;  // [n_seq][n_heads][max_splits][hd + 2]: acc[hd], m, l
 };
 
+// 16 bytes of the cache, loaded non-temporally: every K/V byte is read once,
+// so the lines are not kept for reuse.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -118,12 +126,12 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     const int row = min(wrow0 + it * RPI, n - 1);
-    kr[it] = *reinterpret_cast<const uint4*>(kb + (size_t)row * kv_stride);
+    kr[it] = ld_stream(kb + (size_t)row * kv_stride);
   }
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     const int row = min(wrow0 + it * RPI, n - 1);
-    vr[it] = *reinterpret_cast<const uint4*>(vb + (size_t)row * kv_stride);
+    vr[it] = ld_stream(vb + (size_t)row * kv_stride);
   }
   float qv[G][8];
   const int h0 = kvh * G;
