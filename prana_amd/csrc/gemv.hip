@@ -1752,6 +1752,157 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
   }
 }
 
+// ---- one 16-row x 16-token tile per workgroup, blocks split over 4 waves
+// Below 512 tiles (fewer than 8192 rows, at most 16 tokens) a one-wave
+// workgroup per tile leaves three SIMDs of each CU idle, and each wave walks
+// its row tile's blocks alone. Here the 4 waves of a workgroup take
+// consecutive chunks of kSkCB blocks (wave w: chunk 4i + w), each staged in
+// the wave's own LDS region and multiplied on the matrix cores as in
+// gemm_skinny_kernel; each block's term (d*sa)*float(isum) goes to LDS, and
+// lane (row, token) of the workgroup then adds the 4*kSkCB terms of its output
+// in block order: the same left-to-right fold as every other kernel.
+constexpr int kKsWaves = 4;
+
+template <int KIND>
+__global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m, const int8_t* __restrict__ q,
+                                                                      const float* __restrict__ sa,
+                                                                      const int* __restrict__ sums, int n_tok,
+                                                                      GemvOut o) {
+  static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
+  using L = SkLayout<KIND, 1, 1>;  // one wave's staging: 16 rows x 16 tokens x kSkCB blocks
+  static_assert(L::NT == 64, "one wave per staged chunk");
+  // terms of one block: token t, row r at (t + t/4)*16 + r (the 4 tokens of a
+  // lane's MFMA result land 16 banks apart from the next lane group's)
+  constexpr int kTermStride = 20 * 16;
+  extern __shared__ int4 sk_smem[];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(sk_smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, kg = lane >> 4;
+  const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
+  const int row0 = static_cast<int>(blockIdx.x) * 16;
+  const int n_chunks = (G + kSkCB - 1) / kSkCB;
+  uint8_t* stage = lds + wave * L::BYTES;
+  float* terms = reinterpret_cast<float*>(lds + kKsWaves * L::BYTES);
+
+  auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
+    SkRegs<KIND, 1, 1> r;
+    const int cb0 = c * kSkCB;
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = min(lane + 64 * i, L::WP - 1);
+      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int blk = min(cb0 + pr / (L::QB / 16), G - 1);
+      const uint8_t* src = m.qs + (size_t)rr * G * L::QB + (size_t)blk * L::QB + (pr % (L::QB / 16)) * 16;
+      r.w[i] = *reinterpret_cast<const sk_i4*>(src);
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = min(lane + 64 * i, L::AP - 1);
+      const int t = min(p / (2 * kSkCB), n_tok - 1), pr = p % (2 * kSkCB);
+      const int blk = min(cb0 + pr / 2, G - 1);
+      r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = min(lane + 64 * i, L::DP - 1);
+      const size_t gi = (size_t)min(row0 + p / kSkCB, R - 1) * G + min(cb0 + p % kSkCB, G - 1);
+      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
+                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = min(lane + 64 * i, L::SP - 1);
+      const size_t gi = (size_t)min(p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
+      r.sa[i] = sa[gi];
+      r.sm[i] = sums[gi];
+    }
+    return r;
+  };
+  auto store = [&](const SkRegs<KIND, 1, 1>& r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < L::WPL; i++) {
+      const int p = lane + 64 * i;
+      if (p < L::WP) *reinterpret_cast<sk_i4*>(stage + (p / L::WPR) * L::WSTR + (p % L::WPR) * 16) = r.w[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::APL; i++) {
+      const int p = lane + 64 * i;
+      if (p < L::AP)
+        *reinterpret_cast<sk_i4*>(stage + L::A_OFF + (p / (2 * kSkCB)) * L::ASTR + (p % (2 * kSkCB)) * 16) = r.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::DPL; i++) {
+      const int p = lane + 64 * i;
+      if (p < L::DP) reinterpret_cast<uint32_t*>(stage + L::D_OFF)[(p / kSkCB) * L::DSTR + p % kSkCB] = r.d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::SPL; i++) {
+      const int p = lane + 64 * i;
+      if (p < L::SP) reinterpret_cast<float*>(stage + L::SA_OFF)[(p % kSkCB) * L::TOKS + p / kSkCB] = r.sa[i];
+    }
+  };
+  // block terms of this wave's staged chunk -> terms[wave][bb]
+  auto products = [&]() __attribute__((always_inline)) {
+    const uint8_t* arow = stage + L::A_OFF + j * L::ASTR + 8 * kg;
+    const uint8_t* wrow = stage + j * L::WSTR + (KIND == kKindQ4_0 ? 8 * (kg & 1) : 8 * kg);
+    const uint32_t* drow = reinterpret_cast<const uint32_t*>(stage + L::D_OFF) + j * L::DSTR;
+    const float* sab = reinterpret_cast<const float*>(stage + L::SA_OFF) + 4 * kg;
+    float* tw = terms + wave * kSkCB * kTermStride + 5 * kg * 16 + j;
+#pragma unroll
+    for (int bb = 0; bb < kSkCB; bb++) {
+      const long av = *reinterpret_cast<const long*>(arow + bb * 32);
+      long wb = *reinterpret_cast<const long*>(wrow + bb * L::QB);
+      if constexpr (KIND == kKindQ4_0) {
+        // signed nibbles n - 8: the product is isum - 8*sum_a
+        constexpr long kLo = 0x0F0F0F0F0F0F0F0FL, kHi = static_cast<long>(0x8080808080808080UL),
+                       k8 = 0x0808080808080808L;
+        wb = kg < 2 ? (wb & kLo) : ((wb >> 4) & kLo);
+        wb = ((wb | kHi) - k8) ^ kHi;
+      }
+      const v4i_t z = {0, 0, 0, 0};
+      const v4i_t cc = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wb, z, 0, 0, 0);
+      const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
+      const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * L::TOKS);
+      const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+      for (int v = 0; v < 4; v++) tw[bb * kTermStride + v * 16] = d * sv[v] * static_cast<float>(cc[v]);
+    }
+  };
+
+  const int fr = tid & 15, ft = tid >> 4;  // the output this lane folds: row fr, token ft
+  const float* tf = terms + (ft + (ft >> 2)) * 16 + fr;
+  float acc = 0.0f;
+  SkRegs<KIND, 1, 1> r = load(wave);
+  for (int c0 = 0; c0 < n_chunks; c0 += kKsWaves) {
+    store(r);
+    if (c0 + kKsWaves + wave < n_chunks) r = load(c0 + kKsWaves + wave);
+    __syncthreads();  // staged chunks visible; the previous group's terms all folded
+    products();
+    __syncthreads();  // terms visible
+    const int nb = min(kKsWaves * kSkCB, G - c0 * kSkCB);  // uniform: live blocks of this group
+    for (int b = 0; b < nb; b++) acc = acc + tf[b * kTermStride];
+  }
+  const int n_row = row0 + fr;
+  if (n_row < R && ft < n_tok) store_out(o, ft, n_row, acc);
+}
+
+template <int KIND>
+int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                     const GemvOut& o, hipStream_t s) {
+  using L = SkLayout<KIND, 1, 1>;
+  constexpr int kBytes = kKsWaves * L::BYTES + kKsWaves * kSkCB * 20 * 16 * 4;
+  static const bool attr_ok = [] {
+    return kBytes <= 65536 ||
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND>), kBytes);
+  }();
+  PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
+  PRANA_CHECK(n_tok <= 16, "gemm_skinny: one token tile");
+  hipLaunchKernelGGL(gemm_skinny_ks_kernel<KIND>, dim3((m.rows + 15) / 16), dim3(64 * kKsWaves), kBytes, s, m, q,
+                     sa, sums, (int)n_tok, o);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
 template <int KIND, int RW, int TT>
 int launch_skinny_t(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                     const GemvOut& o, hipStream_t s) {
@@ -1774,6 +1925,7 @@ int launch_skinny_tt(const DevMat& m, const int8_t* q, const float* sa, const in
   // tiles share each staged activation chunk among more rows)
   int rw = 1;
   while (rw < 4 && (m.rows + 32 * rw - 1) / (32 * rw) >= 256) rw *= 2;
+  if (rw == 1 && TT == 1) return launch_skinny_ks<KIND>(m, q, sa, sums, n_tok, o, s);
   if (rw == 1) return launch_skinny_t<KIND, 1, TT>(m, q, sa, sums, n_tok, o, s);
   if (rw == 2) return launch_skinny_t<KIND, 2, TT>(m, q, sa, sums, n_tok, o, s);
   return launch_skinny_t<KIND, 4, TT>(m, q, sa, sums, n_tok, o, s);

@@ -24,7 +24,7 @@ def same_bits(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols", [(14336, 4096), (32000, 4096)])
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (32000, 4096), (4096, 14336), (4096, 4096)])
 @pytest.mark.parametrize("n", [16, 64])
 def test_c1_large_shapes_batched(rows, cols, n):
     raw = P.synth_tensor(P.Q8_0, rows, cols, rows + n, 0.02)

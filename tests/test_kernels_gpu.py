@@ -105,6 +105,18 @@ def test_matmul_batched(ty, rows, cols, n_tok):
 
 
 @pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
+@pytest.mark.parametrize("rows,cols,n_tok", [(300, 1312, 13), (16, 4128, 16), (4100, 256, 9)])
+def test_matmul_skinny_block_split_ragged(ty, rows, cols, n_tok):
+    # 9..16 tokens over fewer than 8192 rows: four waves take consecutive
+    # chunks of 8 blocks and one lane per output folds their terms; 41 and 129
+    # blocks leave a partial chunk and a partial group of four chunks, 8 blocks
+    # leave three waves with nothing live
+    raw, g, o = _mat_pair(ty, rows, cols, 7 + n_tok, real=True)
+    a = rng(n_tok).standard_normal((n_tok, cols)).astype(np.float32)
+    assert same_bits(g.apply(a), o.apply(a))
+
+
+@pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
 @pytest.mark.parametrize("rows,cols,n_tok", [(37, 2048, 10), (300, 4096, 12), (129, 7168, 8), (70, 14336, 3),
                                              (70, 14336, 6), (4097, 4096, 9), (515, 14336, 16)])
 def test_matmul_verify_batch_chunked(ty, rows, cols, n_tok):
