@@ -1781,8 +1781,10 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
   const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
   const int row0 = static_cast<int>(blockIdx.x) * 16;
   const int n_chunks = (G + kSkCB - 1) / kSkCB;
-  uint8_t* stage = lds + wave * L::BYTES;
-  float* terms = reinterpret_cast<float*>(lds + kKsWaves * L::BYTES);
+  // each wave's staging region ends before the layout's activation sums,
+  // which this kernel does not use
+  uint8_t* stage = lds + wave * L::SM_OFF;
+  float* terms = reinterpret_cast<float*>(lds + kKsWaves * L::SM_OFF);
 
   auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
     SkRegs<KIND, 1, 1> r;
@@ -1814,7 +1816,6 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
       const int p = min(lane + 64 * i, L::SP - 1);
       const size_t gi = (size_t)min(p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
       r.sa[i] = sa[gi];
-      r.sm[i] = sums[gi];
     }
     return r;
   };
@@ -1872,6 +1873,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
   const int fr = tid & 15, ft = tid >> 4;  // the output this lane folds: row fr, token ft
   const float* tf = terms + (ft + (ft >> 2)) * 16 + fr;
   float acc = 0.0f;
+  // a chunk at or past n_chunks holds clamped (repeated) blocks, never folded
   SkRegs<KIND, 1, 1> r = load(wave);
   for (int c0 = 0; c0 < n_chunks; c0 += kKsWaves) {
     store(r);
@@ -1880,7 +1882,16 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
     products();
     __syncthreads();  // terms visible
     const int nb = min(kKsWaves * kSkCB, G - c0 * kSkCB);  // uniform: live blocks of this group
-    for (int b = 0; b < nb; b++) acc = acc + tf[b * kTermStride];
+    if (nb == kKsWaves * kSkCB) {
+      // whole group: every read issued before the adds
+      float t[kKsWaves * kSkCB];
+#pragma unroll
+      for (int b = 0; b < kKsWaves * kSkCB; b++) t[b] = tf[b * kTermStride];
+#pragma unroll
+      for (int b = 0; b < kKsWaves * kSkCB; b++) acc = acc + t[b];
+    } else {
+      for (int b = 0; b < nb; b++) acc = acc + tf[b * kTermStride];
+    }
   }
   const int n_row = row0 + fr;
   if (n_row < R && ft < n_tok) store_out(o, ft, n_row, acc);
@@ -1890,7 +1901,7 @@ template <int KIND>
 int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                      const GemvOut& o, hipStream_t s) {
   using L = SkLayout<KIND, 1, 1>;
-  constexpr int kBytes = kKsWaves * L::BYTES + kKsWaves * kSkCB * 20 * 16 * 4;
+  constexpr int kBytes = kKsWaves * L::SM_OFF + kKsWaves * kSkCB * 20 * 16 * 4;
   static const bool attr_ok = [] {
     return kBytes <= 65536 ||
            set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND>), kBytes);
