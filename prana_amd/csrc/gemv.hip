@@ -1753,9 +1753,11 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
 }
 
 // ---- one 16-row x 16-token tile per workgroup, blocks split over 4 waves
-// Below 512 tiles (fewer than 8192 rows, at most 16 tokens) a one-wave
-// workgroup per tile leaves three SIMDs of each CU idle, and each wave walks
-// its row tile's blocks alone. Here the 4 waves of a workgroup take
+// Below 8192 rows, 16-row workgroups of one wave per token tile leave most
+// SIMDs idle, and each wave walks its row tile's blocks alone. Here a
+// workgroup takes one 16-row x 16-token tile (grid: row tiles x token tiles;
+// a row tile's weights are read once per token tile, mostly from the caches
+// for matrices this small), and its 4 waves take
 // consecutive chunks of kSkCB blocks (wave w: chunk 4i + w), each staged in
 // the wave's own LDS region and multiplied on the matrix cores as in
 // gemm_skinny_kernel; each block's term (d*sa)*float(isum) goes to LDS, and
@@ -1780,6 +1782,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
   const int j = lane & 15, kg = lane >> 4;
   const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
   const int row0 = static_cast<int>(blockIdx.x) * 16;
+  const int tok0 = static_cast<int>(blockIdx.y) * 16;  // this workgroup's token tile
   const int n_chunks = (G + kSkCB - 1) / kSkCB;
   // each wave's staging region ends before the layout's activation sums,
   // which this kernel does not use
@@ -1800,7 +1803,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
 #pragma unroll
     for (int i = 0; i < L::APL; i++) {
       const int p = min(lane + 64 * i, L::AP - 1);
-      const int t = min(p / (2 * kSkCB), n_tok - 1), pr = p % (2 * kSkCB);
+      const int t = min(tok0 + p / (2 * kSkCB), n_tok - 1), pr = p % (2 * kSkCB);
       const int blk = min(cb0 + pr / 2, G - 1);
       r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
     }
@@ -1814,7 +1817,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
       const int p = min(lane + 64 * i, L::SP - 1);
-      const size_t gi = (size_t)min(p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
+      const size_t gi = (size_t)min(tok0 + p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
       r.sa[i] = sa[gi];
     }
     return r;
@@ -1894,7 +1897,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
     }
   }
   const int n_row = row0 + fr;
-  if (n_row < R && ft < n_tok) store_out(o, ft, n_row, acc);
+  if (n_row < R && tok0 + ft < n_tok) store_out(o, tok0 + ft, n_row, acc);
 }
 
 template <int KIND>
@@ -1907,9 +1910,8 @@ int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const in
            set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND>), kBytes);
   }();
   PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
-  PRANA_CHECK(n_tok <= 16, "gemm_skinny: one token tile");
-  hipLaunchKernelGGL(gemm_skinny_ks_kernel<KIND>, dim3((m.rows + 15) / 16), dim3(64 * kKsWaves), kBytes, s, m, q,
-                     sa, sums, (int)n_tok, o);
+  hipLaunchKernelGGL(gemm_skinny_ks_kernel<KIND>, dim3((m.rows + 15) / 16, (n_tok + 15) / 16), dim3(64 * kKsWaves),
+                     kBytes, s, m, q, sa, sums, (int)n_tok, o);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -1933,11 +1935,11 @@ template <int KIND, int TT>
 int launch_skinny_tt(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                      const GemvOut& o, hipStream_t s) {
   // rows per workgroup: grow while at least 256 workgroups remain (bigger
-  // tiles share each staged activation chunk among more rows)
+  // tiles share each staged activation chunk among more rows); below 8192
+  // rows the block-split kernel takes the matrix instead
   int rw = 1;
   while (rw < 4 && (m.rows + 32 * rw - 1) / (32 * rw) >= 256) rw *= 2;
-  if (rw == 1 && TT == 1) return launch_skinny_ks<KIND>(m, q, sa, sums, n_tok, o, s);
-  if (rw == 1) return launch_skinny_t<KIND, 1, TT>(m, q, sa, sums, n_tok, o, s);
+  if (rw == 1) return launch_skinny_ks<KIND>(m, q, sa, sums, n_tok, o, s);
   if (rw == 2) return launch_skinny_t<KIND, 2, TT>(m, q, sa, sums, n_tok, o, s);
   return launch_skinny_t<KIND, 4, TT>(m, q, sa, sums, n_tok, o, s);
 }
