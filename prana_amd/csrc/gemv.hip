@@ -1689,7 +1689,7 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
     }
   };
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto compute = [&](int buf, int c) __attribute__((always_inline)) {
+  auto compute_t = [&](int buf, int c, auto full) __attribute__((always_inline)) {
     const uint8_t* b = lds + buf * L::BYTES;
     const uint8_t* arow = b + L::A_OFF + (ttile * 16 + j) * L::ASTR + 8 * kg;
     const uint8_t* wrow = b + (rtile * 16 + j) * L::WSTR + (KIND == kKindQ4_0 ? 8 * (kg & 1) : 8 * kg);
@@ -1712,7 +1712,7 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
       const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
       const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * L::TOKS);
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-      const bool live = bb < nlive;
+      const bool live = decltype(full)::value || bb < nlive;
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int isum = cc[v];
@@ -1723,6 +1723,11 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
       // above this point (registers)
       if (bb % 4 == 3) asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]) : "memory");
     }
+  };
+  // a whole chunk needs no select of live blocks in its epilogue
+  auto compute = [&](int buf, int c) __attribute__((always_inline)) {
+    if (G - c * kSkCB >= kSkCB) compute_t(buf, c, std::true_type{});
+    else compute_t(buf, c, std::false_type{});
   };
 
   SkRegs<KIND, RW, TT> r0 = load(0), r1;
