@@ -483,9 +483,10 @@ int launch_expf_bits(uint32_t base, uint32_t n, float* out, hipStream_t s) {
 // ---------------------------------------------------------------- argmax
 // infer.rs:560-568: strict `>` scan, first max wins. A NaN at index 0 pins the
 // result to 0; later NaNs never win. Parallel form: per-lane strided scans
-// (increasing index, strict >, sixteen loads in flight per lane), then a
-// (value, lowest index) reduction across the workgroup.
+// (increasing index, strict >, 32 loads in flight per lane: one pass covers
+// 32768 values), then a (value, lowest index) reduction across the workgroup.
 constexpr int kArgNT = 1024;
+constexpr int kArgPer = 32;  // loads per lane per pass
 
 __device__ __forceinline__ void argmax_merge(float& av, int& aj, float bv, int bj, int n) {
   if (bj < n && (aj >= n || bv > av || (bv == av && bj < aj))) {
@@ -501,12 +502,14 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float best = -INFINITY;
   int bi = n;  // none
-  for (int base = 0; base < n; base += 16 * kArgNT) {
-    float x[16];
+  bool nan0 = false;  // row[0] is NaN (lane 0's first value)
+  for (int base = 0; base < n; base += kArgPer * kArgNT) {
+    float x[kArgPer];
 #pragma unroll
-    for (int u = 0; u < 16; u++) x[u] = row[min(base + u * kArgNT + tid, n - 1)];
+    for (int u = 0; u < kArgPer; u++) x[u] = row[min(base + u * kArgNT + tid, n - 1)];
+    if (base == 0 && tid == 0) nan0 = x[0] != x[0];
 #pragma unroll
-    for (int u = 0; u < 16; u++) {
+    for (int u = 0; u < kArgPer; u++) {
       const int i = base + u * kArgNT + tid;
       if (i < n && x[u] > best) {
         best = x[u];
@@ -521,10 +524,16 @@ __global__ __launch_bounds__(kArgNT) void argmax_kernel(const float* __restrict_
     s_i[wave] = bi;
   }
   __syncthreads();
-  if (tid == 0) {
-    for (int w = 1; w < kArgNT / 64; w++) argmax_merge(best, bi, s_v[w], s_i[w], n);
-    if (bi >= n || row[0] != row[0]) bi = 0;  // all -inf / NaN, or a NaN at index 0
-    out[blockIdx.x] = static_cast<uint32_t>(bi);
+  if (wave == 0) {
+    // the 16 waves' results in lanes 0..15, merged by the same rule
+    best = lane < kArgNT / 64 ? s_v[lane] : -INFINITY;
+    bi = lane < kArgNT / 64 ? s_i[lane] : n;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) argmax_merge(best, bi, __shfl_xor(best, o, 64), __shfl_xor(bi, o, 64), n);
+    if (tid == 0) {
+      if (bi >= n || nan0) bi = 0;  // all -inf / NaN, or a NaN at index 0
+      out[blockIdx.x] = static_cast<uint32_t>(bi);
+    }
   }
 }
 

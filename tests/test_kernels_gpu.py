@@ -543,5 +543,8 @@ def test_argmax_semantics():
     big = rng(2).standard_normal((5, 151936)).astype(np.float32)
     big[3, 1000] = big[3, 2000] = 100.0
     big[4, 10] = big[4, 10 + 1024] = 100.0                      # tie inside one lane's stride
+    big[2, 5 + 32768] = big[2, 5 + 2 * 32768] = 100.0           # tie across passes of one lane
+    big[1, 70000] = big[1, 3 + 64] = 100.0                      # tie across waves and passes
+    big[0, 900] = big[0, 1023] = 100.0                          # tie across the merged waves
     got = P.argmax(big)
     assert [int(v) for v in got] == [O.argmax(b) for b in big]
