@@ -232,6 +232,15 @@ int prana_forward_batch(prana_model_t m, prana_cache_t c, const uint32_t *tokens
  * sampled ids at the end. No stop ids. */
 int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, size_t n_steps, uint32_t *out);
 
+/* 1 when prana_decode / prana_generate replay a captured decode step (a HIP
+ * graph per attention regime), 0 when they launch the same kernels one by one:
+ * with PRANA_DECODE_GRAPH=0, or when a profiling tool (rocprofv3's
+ * librocprofiler-sdk-tool, ROCPROF_* settings, librocprofiler64,
+ * libroctracer64) is loaded into the process, under whose kernel tracing graph
+ * replays crashed the host. Host-only; needs no GPU. Decided once per process.
+ * No counterpart in the reference (its decode loop has no graphs). */
+int prana_decode_replay_enabled(void);
+
 /* GEMV launch profiling for roofline accounting: with on = P > 0, every P-th
  * model decode-GEMV dispatch records start/stop HIP events as part of the
  * dispatch itself (on its stream); on = 0 turns it off. read returns the timed

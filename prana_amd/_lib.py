@@ -104,6 +104,7 @@ _SIGS = {
     "prana_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
     "prana_forward_batch": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_void_p]),
     "prana_decode": (c_int, [c_void_p, c_void_p, C.c_uint32, c_size, c_size, c_void_p]),
+    "prana_decode_replay_enabled": (c_int, []),
     "prana_gemv_profile": (c_int, [c_int]),
     "prana_gemv_profile_read": (c_int, [C.POINTER(c_size), C.POINTER(C.c_double), C.POINTER(C.c_double), c_int]),
     "prana_gemv_profile_shapes": (c_int, [c_size, C.POINTER(c_size), C.POINTER(c_size), C.POINTER(C.c_double),

@@ -597,6 +597,8 @@ int prana_decode(prana_model_t m, prana_cache_t c, uint32_t token, size_t pos, s
   });
 }
 
+int prana_decode_replay_enabled(void) { return prana::decode_graphs_enabled() ? 1 : 0; }
+
 int prana_gemv_profile(int on) {
   return guard([&] {
     INIT_OR_RETURN();

@@ -12,6 +12,8 @@
 #include <cstring>
 #include <string>
 
+#include <unistd.h>
+
 namespace prana {
 
 namespace {
@@ -413,10 +415,35 @@ void StepGraph::reset() {
 
 constexpr size_t kStreamFloorIds = 4096;
 
-static bool decode_graphs_enabled() {
+// A profiling tool loaded into this process: rocprofv3 preloads
+// librocprofiler-sdk-tool and exports ROCPROF_* settings (older tools load
+// librocprofiler64 / libroctracer64 through ROCP_TOOL_LIBRARIES / HSA_TOOLS_LIB).
+// librocprofiler-register, which every HIP process maps, does not count.
+bool profiler_tool_present() {
+  for (char** e = environ; e && *e; ++e)
+    if (std::strncmp(*e, "ROCPROF_", 8) == 0 || std::strncmp(*e, "ROCP_TOOL_LIBRARIES=", 20) == 0 ||
+        std::strncmp(*e, "HSA_TOOLS_LIB=", 14) == 0)
+      return true;
+  std::FILE* f = std::fopen("/proc/self/maps", "r");
+  if (!f) return false;
+  char line[4096];
+  bool hit = false;
+  while (!hit && std::fgets(line, sizeof line, f))
+    hit = std::strstr(line, "librocprofiler-sdk") || std::strstr(line, "librocprofiler64") ||
+          std::strstr(line, "libroctracer64") || std::strstr(line, "librocprofv3");
+  std::fclose(f);
+  return hit;
+}
+
+// Replay of the captured decode step. Off with PRANA_DECODE_GRAPH=0, and off
+// whenever a profiling tool is present: under rocprofv3's kernel tracing a
+// process replaying the step crashed in host code inside hipGraphLaunch, so
+// the same kernels are then launched one by one (decided once per process).
+bool decode_graphs_enabled() {
   static const bool on = [] {
     const char* e = std::getenv("PRANA_DECODE_GRAPH");
-    return !(e && e[0] == '0');
+    if (e && e[0] == '0') return false;
+    return !profiler_tool_present();
   }();
   return on;
 }

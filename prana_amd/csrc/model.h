@@ -165,6 +165,11 @@ struct Model {
 
 int check_config(const prana_config& c);
 
+// Whether a profiling tool is loaded into the process, and whether decode
+// replays its captured step (not with PRANA_DECODE_GRAPH=0 or a tool present).
+bool profiler_tool_present();
+bool decode_graphs_enabled();
+
 int generate_speculative(Model& target, Model& draft, const uint32_t* prompt, size_t p, size_t steps, size_t k,
                          const uint32_t* stops, size_t n_stops, uint32_t* out, size_t* n_out, prana_gen_stats* st);
 
