@@ -366,6 +366,28 @@ __device__ __forceinline__ void quantize_quad8(const float* y, int* q, float* sc
   *sum_out = s;
 }
 
+// quantize_lane for a block held as eight consecutive values per lane of an
+// aligned 4-lane group (y[j] = element 8*(lane%4)+j of the block): one scale
+// per lane and two DPP steps per reduction. Same scale, values and sum.
+__device__ __forceinline__ void quantize_oct4(const float* y, int* q, float* scale_out, int* sum_out) {
+  float amax = fmaxf(fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3]))),
+                     fmaxf(fmaxf(fabsf(y[4]), fabsf(y[5])), fmaxf(fabsf(y[6]), fabsf(y[7]))));
+  amax = fmaxf(amax, __int_as_float(dpp_lane_mov<0xB1>(__float_as_int(amax))));  // quad_perm [1,0,3,2]
+  amax = fmaxf(amax, __int_as_float(dpp_lane_mov<0x4E>(__float_as_int(amax))));  // quad_perm [2,3,0,1]
+  const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+  const float inv = 1.0f / scale;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    q[j] = round_clamp127(y[j] * inv);
+    s += q[j];
+  }
+  s += dpp_lane_mov<0xB1>(s);
+  s += dpp_lane_mov<0x4E>(s);
+  *scale_out = scale;
+  *sum_out = s;
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
 }

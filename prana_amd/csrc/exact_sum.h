@@ -254,14 +254,17 @@ __host__ __device__ inline int pred_margin(int n) { return 8 * static_cast<int>(
 
 // The binade code of an approximate partial sum p >= 0: its binade, or
 // kPredAmb when p > 0 lies within r units of either boundary of its binade.
+// (Bitwise logic throughout: short-circuit forms compile to a branch per
+// call, and these run once per term.)
 __device__ __forceinline__ int binade_code(float p, int r) {
-  const uint32_t f = __float_as_uint(p) & 0x7fffffu;
-  const bool amb = p > 0.0f && (f < static_cast<uint32_t>(r) || f > 0x7fffffu - static_cast<uint32_t>(r));
+  const uint32_t u = __float_as_uint(p);
+  const uint32_t f = u & 0x7fffffu;
+  const bool amb = ((u & 0x7fffffffu) != 0) & ((f < static_cast<uint32_t>(r)) | (f > 0x7fffffu - static_cast<uint32_t>(r)));
   return amb ? kPredAmb : binade_fast(p);
 }
 
 // A step with binade code ec after a step with code ein starts a new segment.
-__device__ __forceinline__ bool seg_break(int ec, int ein) { return ec != ein || ec == kPredAmb; }
+__device__ __forceinline__ bool seg_break(int ec, int ein) { return (ec != ein) | (ec == kPredAmb); }
 
 // term_pair_bits(bits(t), e) for finite t >= 0, from exact float operations
 // (scaling by a power of two, floor and the difference are exact here; a
@@ -685,53 +688,75 @@ __device__ __forceinline__ float block_seq_sum_short(Term term, int n) {
   return group_seq_sum_short<NT, 1>(term, n);
 }
 
-// The predicted-binade fold for terms held in registers, four consecutive
-// terms per lane: lane t holds t4[k] = term(4t + k), zero past n, with
-// n <= 4 * NT (blockDim.x == NT, NT a multiple of 64, all lanes call it).
-// Lanes 0..7 hold the kPredHead = 32 head terms, which wave 0 folds serially
-// (read lane by lane); lane t >= 8 owns steps 4t .. 4t+3. Differences from
-// group_seq_sum_pred: no term is read from memory; the binade code of the
-// partial sum between two lanes is taken from one value both of them compute
-// with the same operations (the later lane's approximate entry sum), so the
-// lanes need not exchange their last codes (one barrier fewer); and the lane
-// that owns a crossing records the segment ending before it. The walk and
-// its verification are the same, and so is the fallback: non-finite terms,
-// more than kPredMaxCross crossings or a failed check fold term(0..n) on one
-// lane (term reads memory the whole workgroup sees). Every lane returns the
-// fold; four workgroup barriers (five on the fallback).
-template <int NT, class Term>
-__device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term term) {
-  static_assert(NT % 64 == 0 && NT / 64 <= 16, "whole waves, at most 16");
-  constexpr int W = NT / 64;
+// The predicted-binade fold for terms held in registers, TPL consecutive
+// terms per lane, evaluated by a group of NL lanes (NL a multiple of 64, at
+// most 16 waves): group lane r (0 <= r < NL, r = 0 on the group's first lane,
+// waves whole) holds t[k] = term(TPL*r + k), zero past n, with n <= TPL * NL.
+// The lanes holding the kPredHead = 32 head terms (r < 32 / TPL) are folded
+// serially by the group's wave 0 (read lane by lane); lane r beyond them owns
+// steps TPL*r .. TPL*r + TPL-1. Differences from group_seq_sum_pred: no term
+// is read from memory; the binade code of the partial sum between two lanes
+// is taken from one value both of them compute with the same operations (the
+// later lane's approximate entry sum), so the lanes need not exchange their
+// last codes (one barrier fewer); and the lane that owns a crossing records
+// the segment ending before it. The walk and its verification are the same,
+// and so is the fallback: non-finite terms, more than kPredMaxCross crossings
+// or a failed check fold term(0..n) on one lane (term reads memory the whole
+// group sees). Every lane of the group returns the fold.
+//
+// sync() is a barrier of the group's waves that also orders their LDS
+// accesses: __syncthreads() when the group is the workgroup, an LDS-counter
+// barrier for a group of waves inside a larger workgroup. Four group
+// barriers (six on the fallback).
+template <int NL, int TPL, class Sync, class Term>
+__device__ __forceinline__ float lanes_seq_sum(const float (&t)[TPL], int n, int r, Sync&& sync, Term term) {
+  static_assert(NL % 64 == 0 && NL / 64 <= 16, "whole waves, at most 16");
+  static_assert(TPL >= 1 && kPredHead % TPL == 0, "the head is whole lanes");
+  constexpr int W = NL / 64;
+  constexpr int kHeadLanes = kPredHead / TPL;
+  static_assert(kHeadLanes <= 64, "the head sits in wave 0");
   __shared__ float s_fw[W];
+  __shared__ int s_bad[W];
   __shared__ int s_sw[3 * W];
   __shared__ int s_tot[2 * (kPredMaxCross + 1)];
   __shared__ float s_ct[kPredMaxCross + 1];
   __shared__ int s_ce[kPredMaxCross + 1];
   __shared__ float s_head, s_res;
   __shared__ int s_ok;
-  const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int lane = r & 63, wave = r >> 6;
   bool bad = false;
 #pragma unroll
-  for (int k = 0; k < 4; k++) bad |= !(t4[k] <= 3.4028234663852886e38f);  // zero past n: finite
-  // the head: term(0 .. min(n, 32)) left to right, read from lanes 0..7
+  for (int k = 0; k < TPL; k++) bad |= !(t[k] <= 3.4028234663852886e38f);  // zero past n: finite
+  // the head: term(0 .. min(n, 32)) left to right, read from lanes 0..kHeadLanes-1
   if (wave == 0) {
     float h = -0.0f;
 #pragma unroll
-    for (int j = 0; j < kPredHead / 4; j++)
+    for (int j = 0; j < kHeadLanes; j++)
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t4[k]), j));
-        if (4 * j + k < n) h += v;
+      for (int k = 0; k < TPL; k++) {
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[k]), j));
+        if (TPL * j + k < n) h += v;
       }
     if (lane == 0) s_head = h;
   }
-  const int nv = tid < kPredHead / 4 ? 0 : max(0, min(4, n - 4 * tid));
+  const int nv = r < kHeadLanes ? 0 : max(0, min(TPL, n - TPL * r));
   // pass 1: approximate prefix sums (only the grids depend on them)
-  const float ls = nv > 0 ? (t4[0] + t4[1]) + (t4[2] + t4[3]) : 0.0f;
+  float ls = 0.0f;
+  if (nv > 0) {
+    if constexpr (TPL == 4) {
+      ls = (t[0] + t[1]) + (t[2] + t[3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < TPL; k++) ls += t[k];
+    }
+  }
   const float inc = scan_add_f32(ls);
   if (lane == 63) s_fw[wave] = inc;
-  const bool any_bad = group_or<1>(bad);  // barrier 1: also publishes s_fw and s_head
+  if (lane == 0) s_bad[wave] = __builtin_amdgcn_ballot_w64(bad) != 0;
+  sync();  // barrier 1: also publishes s_head
+  bool any_bad = false;
+#pragma unroll
+  for (int w = 0; w < W; w++) any_bad |= s_bad[w] != 0;
   const float sH = s_head;
   float result = sH;
   bool ok = !any_bad;
@@ -743,32 +768,53 @@ __device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term 
     // the next lane's entry, by the same operations as that lane computes it
     const float pre_n = wave + 1 < W ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), wave)) : 0.0f;
     const float P0n = lane < 63 ? sH + (pre + inc) : sH + (pre_n + 0.0f);
-    const bool next_steps = 4 * (tid + 1) < n;  // the next lane owns steps (tid + 1 >= 8 here when nv > 0)
-    // pass 2: codes, crossings and increment pairs of this lane's steps
-    int ec[4];
-    bool cross[4];
-    Pair pr[4];
-    SegAcc loc{Pair{0, 0}, 0};
+    const bool next_steps = TPL * (r + 1) < n;  // the next lane owns steps (it is past the head when nv > 0)
+    // pass 2: codes, crossings and increment pairs of this lane's steps. The
+    // approximate partial sums come first (one dependent add per step); the
+    // codes, flags and pairs of the steps are then independent of each
+    // other, and the lane's segment accumulator is a balanced tree of
+    // seg_combine over the steps (each step a crossing {identity, 1} or
+    // {pair, 0}; steps past nv the identity), no branches.
+    int ec[TPL];
+    bool cross[TPL];
+    Pair pr[TPL];
+    SegAcc el[TPL];
     {
+      float Pk[TPL];
       float P = P0;
-      int ein = binade_code(P0, R);
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        P += t4[k];
-        const bool last = k == nv - 1;
-        ec[k] = last && next_steps ? binade_code(P0n, R) : binade_code(P, R);
-        cross[k] = k < nv && seg_break(ec[k], ein);
-        pr[k] = k < nv && !cross[k] ? term_pair_fast(t4[k], ec[k]) : Pair{0, 0};
-        if (k < nv) {
-          if (cross[k]) {
-            loc.p = Pair{0, 0};
-            loc.c += 1;
-          } else {
-            loc.p = compose(loc.p, pr[k]);
-          }
-        }
-        ein = ec[k];
+      for (int k = 0; k < TPL; k++) {
+        P += t[k];
+        Pk[k] = P;
       }
+      const int e0 = binade_code(P0, R);
+      const int en = binade_code(P0n, R);
+#pragma unroll
+      for (int k = 0; k < TPL; k++) {
+        const bool last = (k == nv - 1) & next_steps;
+        const int ek = binade_code(Pk[k], R);
+        ec[k] = last ? en : ek;
+      }
+#pragma unroll
+      for (int k = 0; k < TPL; k++) {
+        const bool live = k < nv;
+        cross[k] = live & seg_break(ec[k], k == 0 ? e0 : ec[k - 1]);
+        const Pair q = term_pair_fast(t[k], ec[k]);
+        const bool use = live & !cross[k];
+        pr[k] = Pair{use ? q.e : 0, use ? q.o : 0};
+        el[k] = SegAcc{pr[k], cross[k] ? 1 : 0};
+      }
+    }
+    SegAcc loc;
+    {
+      SegAcc tr[TPL];
+#pragma unroll
+      for (int k = 0; k < TPL; k++) tr[k] = el[k];
+#pragma unroll
+      for (int w = 1; w < TPL; w *= 2)
+#pragma unroll
+        for (int k = 0; k + w < TPL; k += 2 * w) tr[k] = seg_combine(tr[k], tr[k + w]);
+      loc = tr[0];
     }
     const SegAcc incs = scan_seg(loc);
     if (lane == 63) {
@@ -776,7 +822,7 @@ __device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term 
       s_sw[3 * wave + 1] = incs.p.o;
       s_sw[3 * wave + 2] = incs.c;
     }
-    __syncthreads();  // barrier 2
+    sync();  // barrier 2
     SegAcc run{Pair{0, 0}, 0}, all;
     {
       const SegAcc tws = row_scan_seg(lane < W ? SegAcc{Pair{s_sw[3 * lane], s_sw[3 * lane + 1]}, s_sw[3 * lane + 2]}
@@ -792,28 +838,23 @@ __device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term 
     // records: a crossing closes the segment before it; the lane of the last
     // step closes the last segment
     if (all.c <= kPredMaxCross && nv > 0) {
-      SegAcc r = run;
+      SegAcc rr = run;
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        if (k < nv) {
-          if (cross[k]) {
-            s_tot[2 * r.c] = r.p.e;
-            s_tot[2 * r.c + 1] = r.p.o;
-            r.c += 1;
-            s_ct[r.c] = t4[k];
-            s_ce[r.c] = ec[k];
-            r.p = Pair{0, 0};
-          } else {
-            r.p = compose(r.p, pr[k]);
-          }
+      for (int k = 0; k < TPL; k++) {
+        if (cross[k]) {  // rare: the segment before this step closes here
+          s_tot[2 * rr.c] = rr.p.e;
+          s_tot[2 * rr.c + 1] = rr.p.o;
+          s_ct[rr.c + 1] = t[k];
+          s_ce[rr.c + 1] = ec[k];
         }
+        rr = seg_combine(rr, el[k]);
       }
-      if (4 * tid + nv == n) {
-        s_tot[2 * r.c] = r.p.e;
-        s_tot[2 * r.c + 1] = r.p.o;
+      if (TPL * r + nv == n) {
+        s_tot[2 * rr.c] = rr.p.e;
+        s_tot[2 * rr.c + 1] = rr.p.o;
       }
     }
-    __syncthreads();  // barrier 3
+    sync();  // barrier 3
     // the walk (group_seq_sum_pred's): wave 0 holds segment j in lane j
     if (wave == 0) {
       const int K = all.c;
@@ -842,22 +883,54 @@ __device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term 
         s_ok = good;
       }
     }
-    __syncthreads();  // barrier 4
+    sync();  // barrier 4
     ok = s_ok != 0;
     result = s_res;
   }
   if (!ok) {  // non-finite terms or a failed prediction: one lane's chain
-    __syncthreads();  // every read of s_res above is done
-    if (tid == 0) {
+    sync();  // every read of s_res above is done
+    if (r == 0) {
       float s = -0.0f;
       for (int i = 0; i < n; i++) s += term(i);
       s_res = s;
     }
-    __syncthreads();
+    sync();
     result = s_res;
   }
   return result;
 }
+
+// lanes_seq_sum over the whole workgroup (blockDim.x == NT), four terms per
+// lane: lane t holds t4[k] = term(4t + k).
+template <int NT, class Term>
+__device__ __forceinline__ float quad_seq_sum(const float (&t4)[4], int n, Term term) {
+  return lanes_seq_sum<NT, 4>(t4, n, static_cast<int>(threadIdx.x), [] { __syncthreads(); }, term);
+}
+
+// A barrier among `waves` consecutive waves of a workgroup whose other waves
+// do not take part: each wave adds one to an LDS counter once its earlier LDS
+// accesses are done, then waits until the counter reaches waves times the
+// number of barriers passed so far. The counter must be zero before the
+// group's first barrier (and it is never reset in between). The waiting waves
+// issue no global memory operations, so the wait ends once every wave of the
+// group has arrived; a bound on the polls keeps a wave from waiting forever
+// should one never arrive (the caller's result is then wrong, not hung).
+struct LdsGroupBarrier {
+  int* ctr;
+  int waves;
+  int passed;
+  __device__ void operator()() {
+    passed += 1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int target = waves * passed;
+    for (int polls = 0; polls < (1 << 22); polls++) {
+      if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
 
 constexpr int kPadSerialMax = 896;
 template <int NT, bool PADDED, int CMAX = 16>

@@ -12,6 +12,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -318,6 +319,29 @@ struct RegUnit<kKindQ4_0> {
     s -= 8 * a.sm[b];
     t[0] = f16_to_f32(static_cast<uint16_t>(d)) * a.sa[b] * static_cast<float>(s);
   }
+  // The block's integer dot s = sum_j (nibble_j - 8) * qa_j (|s| <= 32*8*127,
+  // so 16 bits) packed above the block's f16 scale bits; term() of the word
+  // and the activation scale gives terms()' value.
+  __device__ int slot(const Acts& a, int b) const {
+    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
+    const int4 a0 = aw[0], a1 = aw[1];
+    int s = 0;
+    s = sdot4(q.x & kMask, a0.x, s);
+    s = sdot4(q.y & kMask, a0.y, s);
+    s = sdot4(q.z & kMask, a0.z, s);
+    s = sdot4(q.w & kMask, a0.w, s);
+    s = sdot4((q.x >> 4) & kMask, a1.x, s);
+    s = sdot4((q.y >> 4) & kMask, a1.y, s);
+    s = sdot4((q.z >> 4) & kMask, a1.z, s);
+    s = sdot4((q.w >> 4) & kMask, a1.w, s);
+    s -= 8 * a.sm[b];
+    return static_cast<int>((d & 0xffffu) | (static_cast<uint32_t>(s) << 16));
+  }
+  // (the scale only feeds this product, so f16_operand's conversion gives
+  // f16_to_f32's result; see common.h)
+  __device__ static float term(int w, float sa) {
+    return f16_operand(static_cast<uint16_t>(w & 0xffff)) * sa * static_cast<float>(w >> 16);
+  }
 };
 
 template <int KIND>
@@ -436,6 +460,16 @@ constexpr int kActRows = 32;    // act-mode rows per matrix of a staged tile: on
 constexpr int kNormNT = 1024;    // lanes of a NORM workgroup for rows of 1025..4096 values (one per CU)
 constexpr int kNormNTSmall = 256;  // ... for rows of 513..1024 values
 constexpr int kNormMaxK = 4096;  // NORM rows: four values per lane
+constexpr int kSplitUAct = 4;    // units per unit lane per stage of a split gate|up launch (two stages in registers)
+constexpr int kSplitMaxStages = 16;
+
+// Orders this wave's LDS accesses before the ones that follow (a wait for
+// its outstanding LDS operations plus a compiler barrier) without waiting for
+// its global loads, which a workgroup-scope fence would also do.
+__device__ __forceinline__ void lds_order() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left at their maximum
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // LDS: acts [n_tok][astride bytes] | terms [nbuf][n_tok][ROWS][SB*TPU + 1].
 // STAGED: more than one stage (double-buffered registers and terms);
@@ -452,16 +486,26 @@ __device__ __forceinline__ void job_tile(const DecodeJob& job, int* mi, int* til
 // quantized, as launch_rmsnorm would produce them, computed in the prologue
 // while this workgroup's first weight loads are in flight; the row and the
 // sum's terms use the term region of LDS, which the fold reuses afterwards.
-template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false>
+// SPLIT (NORM at kNormNT lanes): waves 0..7 compute the norm, eight values
+// per lane, and later fold the terms; waves 8..15 hold the weight units and
+// keep up to two stages of them in flight from the start (see the prologue).
+template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false, bool SPLIT = false>
 __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_t* __restrict__ q,
                                                const float* __restrict__ sa, const int* __restrict__ sums,
                                                int n_tok, int mi, int tile) {
   static_assert(!NORM || NT == kNormNT || NT == kNormNTSmall, "NORM workgroups of 256 or 1024 lanes");
+  static_assert(!SPLIT || (NORM && NT == kNormNT), "split norm launches are 1024-lane NORM launches");
   if constexpr (NORM) n_tok = 1;  // a constant the token loops fold away
   extern __shared__ int4 smem4[];
   using R = RegUnit<KIND>;
   constexpr int TPU = R::kTpu;
   const int tid = threadIdx.x;
+  constexpr int NTL = SPLIT ? NT / 2 : NT;          // lanes holding weight units
+  // SPLIT: norm-wave barrier, flag, marked blocks, then one completion
+  // count per stage (unit waves that have stored the stage's dots)
+  __shared__ int s_dfr[SPLIT ? 3 + kSplitMaxStages : 1];
+  const int lt = SPLIT ? tid - NT / 2 : tid;        // this lane's index among them
+  const bool loader = !SPLIT || tid >= NT / 2;      // (uniform per wave)
   const int rt = job.rt, SB = job.sb;
   const int ROWS = ACT ? 2 * rt : rt;
   const int K = static_cast<int>(job.m[0].cols);
@@ -483,25 +527,27 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   // recomputed where needed (cheaper in registers than keeping U pairs),
   // except in NORM launches, which work out the pairs before the norm so
   // that the divisions stay off the path from the norm to the terms.
-  int urow[NORM ? U : 1], uoff[NORM ? U : 1];
-  if constexpr (NORM) {
+  constexpr bool kPairs = NORM;
+  int urow[kPairs ? U : 1], uoff[kPairs ? U : 1];
+  if constexpr (kPairs) {
 #pragma unroll
     for (int i = 0; i < U; i++) {
-      urow[i] = (tid + NT * i) / SB;
-      uoff[i] = (tid + NT * i) % SB;
+      urow[i] = (lt + NTL * i) / SB;
+      uoff[i] = (lt + NTL * i) % SB;
     }
   }
   auto unit_row = [&](int i) {
-    if constexpr (NORM) return urow[i];
-    else return (tid + NT * i) / SB;
+    if constexpr (kPairs) return urow[i];
+    else return (lt + NTL * i) / SB;
   };
   auto unit_off = [&](int i) {
-    if constexpr (NORM) return uoff[i];
-    else return (tid + NT * i) % SB;
+    if constexpr (kPairs) return uoff[i];
+    else return (lt + NTL * i) % SB;
   };
   auto unit_up = [&](int i) { return ACT && unit_row(i) >= rt; };
   auto unit_lr = [&](int i) { return unit_up(i) ? unit_row(i) - rt : unit_row(i); };
   auto load_stage = [&](R* buf, int s) {
+    if (!loader) return;
 #pragma unroll
     for (int i = 0; i < U; i++) {
       int row = unit_row(i), off = unit_off(i);
@@ -557,7 +603,167 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     load_stage(buf0, 0);
     if (STAGED && n_stages > 1) load_stage(buf1, 1);
   }
-  if constexpr (NORM) {
+  if constexpr (NORM && SPLIT) {
+    // Deferred block scales (one token, Q4_0, K <= 4096). A block's term is
+    // (d*sa)*float(s) with s an exact integer dot of the weights and the
+    // quantized activations q; sa depends on the norm's exact sum of squares
+    // (norms.rs:15), which takes microseconds, but q hardly does: q_i =
+    // round(y_i * 127/amax) is a ratio of values that all scale with the
+    // norm's factor. So:
+    //   waves 0..7  load the row, quantize y = x*w (the norm's factor left
+    //               out: q is a ratio within each block, so it hardly
+    //               depends on it), publish that q through LDS, each wave
+    //               counting itself in a flag; then evaluate the exact sum
+    //               (eight values per lane, synchronising through an LDS
+    //               counter), the exact y, scales and q, and mark every
+    //               32-block whose q differs from the published one;
+    //   waves 8..15 stream the weight units (two stages in flight from the
+    //               start) and, once the flag is up, store each (row, block)
+    //               dot with its f16 scale in LDS as the bytes arrive.
+    // After one workgroup barrier the marked blocks' dots are recomputed
+    // from the exact q (their units re-read), and one lane per row folds
+    // (d*sa)*float(s) in block order with the exact scales: the reference's
+    // terms in the reference's order, whatever the approximation gave.
+    static_assert(KIND == kKindQ4_0, "deferred block scales: Q4_0 units");
+    const int SR = nb + 1;                                     // padded slot row
+    int* slots = reinterpret_cast<int*>(sm8 + astride);        // [ROWS][SR]
+    float* xs = reinterpret_cast<float*>(sm8 + astride + (size_t)ROWS * SR * 4);  // row (one-lane fallback)
+    int8_t* qx = reinterpret_cast<int8_t*>(xs + exact::run_pad(K - 1) + 1);       // exact q
+    float* sx = reinterpret_cast<float*>(qx + K);              // exact block scales
+    int* smx = reinterpret_cast<int*>(sx + G);                 // exact block sums
+    int* mism = smx + G;                                       // 1: the block's q changed
+    int& s_nbar = s_dfr[0];
+    int& s_flag = s_dfr[1];
+    int& s_nmis = s_dfr[2];
+    const bool nl = !loader && 8 * tid < K;
+    float nx[8], nw[8];
+    if (nl) {
+      const float4* x4 = reinterpret_cast<const float4*>(job.nin.x) + 2 * tid;
+      const float4* w4 = reinterpret_cast<const float4*>(job.nin.w) + 2 * tid;
+      const float4 a = x4[0], b = x4[1], c = w4[0], d = w4[1];
+      nx[0] = a.x, nx[1] = a.y, nx[2] = a.z, nx[3] = a.w, nx[4] = b.x, nx[5] = b.y, nx[6] = b.z, nx[7] = b.w;
+      nw[0] = c.x, nw[1] = c.y, nw[2] = c.z, nw[3] = c.w, nw[4] = d.x, nw[5] = d.y, nw[6] = d.z, nw[7] = d.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) nx[j] = nw[j] = 0.0f;
+    }
+    if (tid < 3 + kSplitMaxStages) s_dfr[tid] = 0;
+    // the row loads are issued before this barrier, the weight loads after it
+    __syncthreads();
+    float* as_a = reinterpret_cast<float*>(sm8 + K);
+    int* am_a = reinterpret_cast<int*>(as_a + G);
+    if (loader) {
+      load_stage(buf0, 0);
+      if (STAGED && n_stages > 1) load_stage(buf1, 1);
+      for (int polls = 0; polls < (1 << 22); polls++) {  // bounded: the norm waves count in early
+        if (__hip_atomic_load(&s_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= NT / 2 / 64) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      lds_order();  // (not a workgroup fence: that would also wait for this wave's weight loads)
+      const Acts a{reinterpret_cast<const int*>(sm8), as_a, am_a};
+      auto stage_done = [&](int st) {  // this wave's dots of stage st are in LDS
+        lds_order();
+        if ((tid & 63) == 0) __hip_atomic_fetch_add(&s_dfr[3 + st], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      };
+      auto slot_stage = [&](const R* buf, int st) {
+#pragma unroll
+        for (int i = 0; i < U; i++) {
+          const int row = unit_row(i), off = unit_off(i);
+          const int lr = ACT && row >= rt ? row - rt : row;
+          const int blk = st * SB + off;
+          if (blk < nb && lr < rows_here) slots[row * SR + blk] = buf[i].slot(a, blk);
+        }
+      };
+      if (!STAGED) {
+        slot_stage(buf0, 0);
+        stage_done(0);
+      } else {
+        for (int st = 0; st < n_stages; st += 2) {
+          slot_stage(buf0, st);
+          stage_done(st);
+          if (st + 2 < n_stages) load_stage(buf0, st + 2);
+          if (st + 1 >= n_stages) break;
+          slot_stage(buf1, st + 1);
+          stage_done(st + 1);
+          if (st + 3 < n_stages) load_stage(buf1, st + 3);
+        }
+      }
+    } else {
+      exact::LdsGroupBarrier bar{&s_nbar, NT / 2 / 64, 0};
+      // the staged row serves the exact sum's one-lane fallback only
+      if (nl) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) xs[exact::run_pad(8 * tid + j)] = nx[j];
+      }
+      float t8[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) t8[j] = nx[j] * nx[j];  // zero on lanes past K
+      float y[8], sc;
+      int qa[8], qe[8], sm;
+#pragma unroll
+      for (int j = 0; j < 8; j++) y[j] = nx[j] * nw[j];
+      quantize_oct4(y, qa, &sc, &sm);  // K % 32 == 0: 4-lane groups are all live or all past K
+      auto pack4 = [](const int* v) {
+        return (v[0] & 0xff) | ((v[1] & 0xff) << 8) | ((v[2] & 0xff) << 16) | (static_cast<int>(v[3]) << 24);
+      };
+      if (nl) {
+        int* qw = reinterpret_cast<int*>(sm8) + 2 * tid;
+        qw[0] = pack4(qa);
+        qw[1] = pack4(qa + 4);
+        if ((tid & 3) == 0) am_a[tid >> 2] = sm;
+      }
+      lds_order();  // this wave's q is in LDS
+      if ((tid & 63) == 0) __hip_atomic_fetch_add(&s_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      // exact: norms.rs:9-23 in the reference's order, then quantize_acts
+      const float ss = exact::lanes_seq_sum<NT / 2, 8>(t8, K, tid, bar, [xs](int i) {
+        const float v = xs[exact::run_pad(i)];
+        return v * v;
+      });
+      const float mean_sq = ss / static_cast<float>(K);
+      const float inv = 1.0f / sqrtf(mean_sq + job.nin.eps);
+#pragma unroll
+      for (int j = 0; j < 8; j++) y[j] = nl ? nx[j] * inv * nw[j] : 0.0f;
+      quantize_oct4(y, qe, &sc, &sm);
+      int diff = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) diff |= qe[j] != qa[j];
+      diff |= dpp_lane_mov<0xB1>(diff);  // the block's four lanes
+      diff |= dpp_lane_mov<0x4E>(diff);
+      if (nl) {
+        int* qw = reinterpret_cast<int*>(qx) + 2 * tid;
+        qw[0] = pack4(qe);
+        qw[1] = pack4(qe + 4);
+        if ((tid & 3) == 0) {
+          sx[tid >> 2] = sc;
+          smx[tid >> 2] = sm;
+          mism[tid >> 2] = diff;
+          if (diff) __hip_atomic_fetch_add(&s_nmis, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
+      bar();  // every block's exact scale is in LDS
+      // the norm waves turn each stage's (row, block) words into f32 terms
+      // (d*sa)*float(s) as soon as the unit waves have stored the stage, so
+      // that only the fold remains after the workgroup barrier; lane l takes
+      // block column l % SB of the stage and every (NT/2)/SB-th row
+      const int unit_waves = NT / 2 / 64;
+      float* tf = reinterpret_cast<float*>(slots);
+      for (int st = 0; st < n_stages; st++) {
+        for (int polls = 0; polls < (1 << 22); polls++) {
+          if (__hip_atomic_load(&s_dfr[3 + st], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= unit_waves) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        lds_order();
+        const int b = st * SB + tid % SB;
+        if (b < nb) {
+          const float scale = sx[b];
+          for (int row = tid / SB; row < ROWS; row += NT / 2 / SB) {
+            const int i = row * SR + b;
+            tf[i] = R::term(slots[i], scale);
+          }
+        }
+      }
+    }
+  } else if constexpr (NORM) {
     // norms.rs:9-23 on this workgroup: the sum of squares in the reference's
     // left-to-right order (evaluated exactly), ms = ss/dim, inv =
     // 1/sqrt(ms+eps), y = (x*inv)*w, then quantize_acts' 32-blocks. The
@@ -651,7 +857,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
       if constexpr (NORM) asm volatile("" : "+v"(row), "+v"(off));  // as in load_stage
       const int lr = ACT && row >= rt ? row - rt : row;
       const int blk = s * SB + off;
-      if (blk < nb && lr < rows_here) {
+      if (loader && blk < nb && lr < rows_here) {
         for (int t = 0; t < n_tok; t++) {
           const uint8_t* ab = sm8 + t * astride;
           Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
@@ -681,7 +887,53 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     }
   };
 
-  if (!STAGED) {
+  if constexpr (SPLIT) {
+    // the deferred terms: every (row, block) dot is in LDS (see the prologue)
+    const int SR = nb + 1;
+    int* slots = reinterpret_cast<int*>(sm8 + astride);
+    const float* xs = reinterpret_cast<const float*>(sm8 + astride + (size_t)ROWS * SR * 4);
+    const int8_t* qx = reinterpret_cast<const int8_t*>(xs + exact::run_pad(K - 1) + 1);
+    const float* sx = reinterpret_cast<const float*>(qx + K);
+    const int* smx = reinterpret_cast<const int*>(sx + G);
+    const int* mism = smx + G;
+    if (s_dfr[2] > 0) {  // blocks the norm waves marked before the barrier above
+      // a block whose exact q differs from the published one: its dots are
+      // recomputed from the exact activations (units re-read from memory)
+      const Acts ax{reinterpret_cast<const int*>(qx), sx, smx};
+      for (int idx = tid; idx < ROWS * nb; idx += NT) {
+        const int row = idx / nb, b = idx - row * nb;
+        if (!mism[b]) continue;
+        const bool up = ACT && row >= rt;
+        const int lr = up ? row - rt : row;
+        if (lr >= rows_here) continue;
+        const size_t ui = (r0 + lr) * nb + b;
+        const int j = up ? 1 : 0;
+        R u;
+        u.load(qbase[ACT ? j : 0] + ui * R::kQB, sbase[ACT ? j : 0] + ui * R::kSB);
+        reinterpret_cast<float*>(slots)[row * SR + b] = R::term(u.slot(ax, b), sx[b]);
+      }
+      __syncthreads();
+    }
+    // one lane per row folds the terms (formed by the norm waves) in block order
+    const float* tf = reinterpret_cast<const float*>(slots);
+    if (folder) {
+      const float* tr = tf + fl_row * SR;
+      int i = 0;
+      for (; i + 8 <= nb; i += 8) {
+        float x0 = tr[i], x1 = tr[i + 1], x2 = tr[i + 2], x3 = tr[i + 3];
+        float x4 = tr[i + 4], x5 = tr[i + 5], x6 = tr[i + 6], x7 = tr[i + 7];
+        acc += x0;
+        acc += x1;
+        acc += x2;
+        acc += x3;
+        acc += x4;
+        acc += x5;
+        acc += x6;
+        acc += x7;
+      }
+      for (; i < nb; i++) acc += tr[i];
+    }
+  } else if (!STAGED) {
     process(buf0, 0);
   } else {
     for (int s = 0; s < n_stages; s += 2) {
@@ -781,7 +1033,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   }
 }
 
-template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false>
+template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false, bool SPLIT = false>
 __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
                                                         const float* __restrict__ sa,
                                                         const int* __restrict__ sums, int n_tok) {
@@ -789,8 +1041,8 @@ __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8
   if (!ACT) job_tile(job, &mi, &tile);
   // decode's one-token launches get a copy of the body in which the token
   // loops fold away (the branch is uniform)
-  if (n_tok == 1) gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, 1, mi, tile);
-  else gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM>(job, q, sa, sums, n_tok, mi, tile);
+  if (n_tok == 1) gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM, SPLIT>(job, q, sa, sums, 1, mi, tile);
+  else gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM, SPLIT>(job, q, sa, sums, n_tok, mi, tile);
 }
 
 // Matrices of two formats with the same unit width and tile geometry in one
@@ -1041,17 +1293,42 @@ TileGeom norm_act_geom(size_t K) {
   return nb == 28 || nb == 32 ? TileGeom{nb / 2, 64, nb, kNormNTSmall} : TileGeom{0, 0, 0, 0};
 }
 
+// Geometry of a split gate|up NORM launch (deferred block scales: Q4_0 rows
+// of 2049..4096 values; kNormNT lanes, the second half holding kSplitUAct
+// units per lane per stage): tiles of 64 rows of each matrix in stages of
+// 4 * kSplitUAct blocks, or u == 0 when off. (The Q|K|V launch keeps the
+// plain NORM form, which measured faster: there the exact sum, not the
+// weight stream, sets the launch's length.) On unless PRANA_NORM_SPLIT=0
+// (decided once per process).
+template <int KIND>
+TileGeom norm_split_act_geom(size_t K) {
+  static const bool on = [] {
+    const char* e = std::getenv("PRANA_NORM_SPLIT");
+    return !(e && e[0] == '0');
+  }();
+  const int nb = static_cast<int>(K / RegUnit<KIND>::kElems);
+  if (!on || KIND != kKindQ4_0 || K <= 2048 || K > static_cast<size_t>(kNormMaxK) || K % 32 != 0)
+    return TileGeom{0, 0, 0, 0};
+  // (the norm waves convert a stage as columns of (kNormNT/2) % sb == 0
+  // lanes, and the stage counters cover every stage)
+  constexpr int sb = kNormNT / 2 * kSplitUAct / 128;
+  static_assert((kNormNT / 2) % sb == 0, "stage columns tile the norm lanes");
+  return (nb + sb - 1) / sb <= kSplitMaxStages ? TileGeom{kSplitUAct, 64, sb, kNormNT} : TileGeom{0, 0, 0, 0};
+}
+
 // KB >= 0: the matrices come in two formats, KIND and KB, with the same tile
 // geometry (gemv_tile_mixed_kernel; not in act mode).
-template <int KIND, int U, bool ACT, bool STAGED, int NT, int KB = -1, bool NORM = false>
+template <int KIND, int U, bool ACT, bool STAGED, int NT, int KB = -1, bool NORM = false, bool SPLIT = false>
 int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, const float* sa, const int* sums,
                   size_t n_tok, hipStream_t s) {
   using R = RegUnit<KIND>;
   static_assert(KB < 0 || !ACT, "two formats only outside act mode");
+  static_assert(KB < 0 || !SPLIT, "split norm launches take one format");
   constexpr int kTpuMax = KB < 0 ? R::kTpu : std::max(R::kTpu, RegUnit<(KB < 0 ? KIND : KB)>::kTpu);
-  const void* const fn = KB < 0 ? reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>)
-                                : reinterpret_cast<const void*>(
-                                      gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT, NORM>);
+  const void* const fn = [] {
+    if constexpr (KB < 0) return reinterpret_cast<const void*>(gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM, SPLIT>);
+    else return reinterpret_cast<const void*>(gemv_tile_mixed_kernel<KIND, KB, U, STAGED, NT, NORM>);
+  }();
   DecodeJob job = job0;
   job.rt = g.rt;
   job.sb = g.sb;
@@ -1069,7 +1346,10 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   }
   // NORM: the row staged for the sum of squares shares the term region
   const size_t norm_bytes = NORM ? (static_cast<size_t>(exact::run_pad(static_cast<int>(K) - 1)) + 1) * 4 : 0;
-  const size_t per_tok = astride + std::max(term_bytes, norm_bytes);
+  // SPLIT (deferred block scales): the (row, block) dots of the whole tile,
+  // the staged row, the exact q, block scales, sums and change marks
+  const size_t split_bytes = static_cast<size_t>(rows_wg) * (nb + 1) * 4 + norm_bytes + K + 3 * (K / 32) * 4;
+  const size_t per_tok = astride + (SPLIT ? split_bytes : std::max(term_bytes, norm_bytes));
   PRANA_CHECK(!NORM || (n_tok == 1 && K <= static_cast<size_t>(4 * NT) && K % 32 == 0 && job.nin.x &&
                         job.nin.w && reinterpret_cast<uintptr_t>(job.nin.x) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(job.nin.w) % 16 == 0),
@@ -1088,7 +1368,7 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   size_t group = std::min<size_t>(kDecMaxTok, lds_cap / per_tok);
   group = std::min<size_t>(group, NT / rows_wg);  // one folder lane per (token, row)
   PRANA_CHECK(K <= 16384, "gemv: decode kernel supports cols <= 16384");
-  PRANA_CHECK(rows_wg * g.sb == NT * U, "gemv: tile geometry mismatch");
+  PRANA_CHECK(rows_wg * g.sb == (SPLIT ? NT / 2 : NT) * U, "gemv: tile geometry mismatch");
   PRANA_CHECK(group >= 1, "gemv: decode tile exceeds LDS");
   for (size_t t0 = 0; t0 < n_tok; t0 += group) {
     const size_t nt = std::min<size_t>(group, n_tok - t0);
@@ -1105,15 +1385,16 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     const size_t G = K / 32;
     LaunchEvents& le = launch_events();
     if constexpr (KB >= 0) {
-      hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, (KB < 0 ? KIND : KB), U, STAGED, NT, NORM>), dim3(total),
+      hipLaunchKernelGGL((gemv_tile_mixed_kernel<KIND, KB, U, STAGED, NT, NORM>), dim3(total),
                          dim3(NT), nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     } else if (le.start && t0 + nt >= n_tok && t0 == 0) {  // one launch: timestamp it
-      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>), dim3(total), dim3(NT), nt * per_tok,
-                            s, le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      hipExtLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM, SPLIT>), dim3(total), dim3(NT),
+                            nt * per_tok, s, le.start, le.stop, 0, j, q + t0 * K, sa + t0 * G, sums + t0 * G,
+                            (int)nt);
       le = LaunchEvents{};
     } else {
-      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM>), dim3(total), dim3(NT), nt * per_tok, s,
-                         j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
+      hipLaunchKernelGGL((gemv_tile_kernel<KIND, U, ACT, STAGED, NT, NORM, SPLIT>), dim3(total), dim3(NT),
+                         nt * per_tok, s, j, q + t0 * K, sa + t0 * G, sums + t0 * G, (int)nt);
     }
     PRANA_LAUNCH_CHECK();
   }
@@ -2437,6 +2718,10 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
     return dispatch_kind(gate.kind, [&](auto k) {
       constexpr int KIND = decltype(k)::value;
       if constexpr (RegUnit<KIND>::kElems == 32) {
+        const TileGeom gs = norm_split_act_geom<KIND>(gate.cols);
+        if constexpr (KIND == kKindQ4_0)
+          if (gs.u == kSplitUAct)
+            return launch_tile_u<KIND, kSplitUAct, true, true, kNormNT, -1, true, true>(job, gs, q, sa, sums, 1, s);
         const TileGeom g = norm_act_geom<KIND>(gate.cols);
         if (g.nt == kNormNT) return launch_tile_u<KIND, 4, true, true, kNormNT, -1, true>(job, g, q, sa, sums, 1, s);
         if (g.u == 14) return launch_tile_u<KIND, 14, true, false, kNormNTSmall, -1, true>(job, g, q, sa, sums, 1, s);
