@@ -45,6 +45,7 @@ MALL = 256 << 20
 C1_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]
 C1_TOKENS = [1, 4, 16, 64]
 C3_CTX = [1024, 4096, 16384, 32768]
+ATTN_ROWS = [545, 640, 1024]  # decode attention at the 7B bench's cache lengths (512-token prefill + steps)
 WARMUP, TIMED = 3, 20
 Q4_0, Q4_K, Q6_K = 2, 12, 14
 GEMM_CASES = [  # (tag, ggml type, rows, cols, N)
@@ -133,6 +134,22 @@ def run(manifest_path, only=None):
     nh, nkv, hd = 32, 8, 128
     kv = nkv * hd
     lib = P.load()
+    for rows in (ATTN_ROWS if only == "ATTN" else []):
+        # the 7B decode's attention (32/8 heads, hd 128, f16 cache) on the
+        # exact one-launch kernel, one query row at position rows - 1
+        print(f"ATTN rows={rows}", file=sys.stderr, flush=True)
+        qa = P.DeviceArray.from_host(rng.standard_normal(nh * hd).astype(np.float32))
+        ka = P.DeviceArray.from_host(rng.standard_normal((rows, kv)).astype(np.float16).view(np.uint16))
+        va = P.DeviceArray.from_host(rng.standard_normal((rows, kv)).astype(np.float16).view(np.uint16))
+        oa = P.DeviceArray((nh * hd,), np.float32)
+        for phase, calls in (("warmup", WARMUP), ("timed", TIMED)):
+            _marker(P, marker)
+            for i in range(calls):
+                P.check(lib.prana_attention_decode(qa.ptr, ka.ptr, va.ptr, rows - 1, nh, nkv, hd, oa.ptr, None))
+        _marker(P, marker)
+        P.check(lib.prana_synchronize())
+        cases.append({"config": "C4 attention", "case": f"decode over {rows} cache rows, exact", "calls": TIMED,
+                      "bytes": 2 * rows * kv * 2 + nh * hd * 8})
     for ctx in (C3_CTX if only in (None, "C3") else []):
         print(f"C3 ctx={ctx}", file=sys.stderr, flush=True)
         rows = ctx + 1
@@ -343,6 +360,43 @@ def summarize_counters(db, cus=256):
     print("\n".join(out))
 
 
+def attention_counters(dbs, cus=256):
+    """Per attention kernel (grid) from rocprofv3 --pmc runs of --only ATTN:
+    texture-address (TA) busy cycles per active compute unit (one workgroup
+    per CU) next to the kernel's GRBM active cycles per XCD, VALU and LDS
+    instructions per wave, and LDS bank-conflict and active cycles per CU."""
+    import collections
+    import re
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    names = {}
+    for db in dbs:
+        c = sqlite3.connect(db)
+        for did, kn, gs, wg, cn, v in c.execute(
+                "select dispatch_id, kernel_name, grid_size, workgroup_size, counter_name, value from counters_collection"):
+            key = (db, did)
+            per[key][cn] = max(per[key][cn], v) if cn == "GRBM_GUI_ACTIVE" else per[key][cn] + v
+            kk = kn.replace("(anonymous namespace)::", "").replace("prana::", "")
+            names[key] = (re.sub(r"^void ", "", kk.split("(")[0]), int(gs), int(wg))
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for key, d in per.items():
+        for cn, v in d.items():
+            agg[names[key]][cn].append(v)
+    med = lambda v: sorted(v)[len(v) // 2] if v else float("nan")
+    out = ["| kernel | grid | workgroups | GRBM active cycles | TA busy cycles / CU | VALU insts / wave | LDS insts / wave "
+           "| LDS bank-conflict cycles / CU | LDS active cycles / CU |", "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for (k, gs, wg), d in sorted(agg.items()):
+        if "attn" not in k:
+            continue
+        wgs = gs // wg
+        waves = med(d.get("SQ_WAVES", [])) or 1
+        act = min(wgs, cus)
+        out.append(f"| `{k}` | {gs} | {wgs} | {med(d.get('GRBM_GUI_ACTIVE', [])):.0f} | "
+                   f"{med(d.get('TA_TA_BUSY_sum', [])) / act:.0f} | {med(d.get('SQ_INSTS_VALU', [])) / waves:.0f} | "
+                   f"{med(d.get('SQ_INSTS_LDS', [])) / waves:.0f} | {med(d.get('SQ_LDS_BANK_CONFLICT', [])) / act:.0f} | "
+                   f"{med(d.get('SQ_LDS_IDX_ACTIVE', [])) / act:.0f} |")
+    print("\n".join(out))
+
+
 def decode_trace_summary(db, bench_json, command):
     """Markdown summary of a kernel trace of bench.py (7B-shape Q4_0 decode):
     per-kernel time over the run, the decode GEMVs by shape (grid size), and
@@ -444,7 +498,8 @@ def main():
     ap.add_argument("--summarize", metavar="DB")
     ap.add_argument("--counters", metavar="DB", help="MFMA / VALU utilisation table of a --pmc run")
     ap.add_argument("--models", action="store_true", help="end-to-end C0 / C2 / C4 passes instead of the kernel sweep")
-    ap.add_argument("--only", choices=["C1", "GEMM", "C3", "VERIFY"], help="run one configuration's sweep")
+    ap.add_argument("--only", choices=["C1", "GEMM", "C3", "VERIFY", "ATTN"], help="run one configuration's sweep")
+    ap.add_argument("--attn-counters", nargs="+", metavar="DB", help="attention counter table of --pmc runs of --only ATTN")
     ap.add_argument("--spec", type=int, metavar="K", help="C4 speculative decode alone, K drafts per round")
     ap.add_argument("--tokens", type=int, default=48, help="tokens of the --spec call")
     ap.add_argument("--round-trace", metavar="DB", help="per-kernel table of a kernel trace of --spec")
@@ -462,6 +517,8 @@ def main():
         decode_trace_summary(*args.decode_trace)
     elif args.counters:
         summarize_counters(args.counters)
+    elif args.attn_counters:
+        attention_counters(args.attn_counters)
     elif args.summarize:
         summarize(args.summarize, args.manifest)
     else:
