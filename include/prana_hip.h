@@ -147,13 +147,16 @@ int prana_attention_verify(const float *q, const uint16_t *k_cache, const uint16
 /* Split-K flash decoding: attention_decode (attention.rs:129-160) for n_seq
  * (1..16) independent sequences, each over its own f16 cache, in tiles of
  * cache rows whose partial softmax states (max, sum, P.V) are merged by a
- * second launch. Results are within 1e-4 relative of the reference's
- * sequential order, not bit-identical (the exact path is
+ * second launch. Each output element is within 1e-4 relative of the
+ * reference's sequential order plus 1e-6 of sum_t p_t |v_t[d]| (the error scale
+ * of the reassociated weighted sum), not bit-identical (the exact path is
  * prana_attention_decode). q, out: device [n_seq][n_heads*head_dim] f32, RoPE
  * already applied to q; k_caches / v_caches: host arrays of n_seq device
- * pointers to [rows][n_kv_heads*head_dim] f16; pos: host array, sequence i
- * attends to rows 0..=pos[i]. head_dim 64 or 128; n_heads / n_kv_heads 1, 2, 4
- * or 8. Synchronous; scratch comes from the library. */
+ * pointers to [rows][n_kv_heads*head_dim] f16, 16-byte aligned; pos: host
+ * array, sequence i attends to rows 0..=pos[i]. Any n_heads / n_kv_heads; a
+ * head_dim that is a multiple of 8 up to 256 (MAX_HEAD_DIM, attention.rs:42;
+ * others return PRANA_ERR_INVALID). Synchronous; scratch comes from the
+ * library. */
 int prana_attention_decode_splitk(const float *q, const uint16_t *const *k_caches, const uint16_t *const *v_caches,
                                   const size_t *pos, size_t n_seq, size_t n_heads, size_t n_kv_heads,
                                   size_t head_dim, float *out, prana_stream_t stream);

@@ -6,13 +6,17 @@
 // softmax sum and the P.V fold are reassociated); the exact one-query kernels
 // in attention.hip remain the path of the model's decode.
 //
-//   split  : one workgroup per (tile of T cache rows, KV head, sequence). A K
-//            or V row of one KV head is read once, coalesced (hd/8 lanes x 16
-//            bytes), and serves the G query heads of its group: every lane
-//            holds 8 dims of q for each of them, the G partial dots of a row
-//            are reduced over its hd/8 lanes with DPP; each wave keeps its own
-//            max, sum of exp(s - max) and P.V per head in registers, and the
-//            four waves are merged once at the end of the tile.
+//   split  : one workgroup per (tile of T cache rows, KV head and block of
+//            up to GB of its query heads, sequence). A K or V row of one KV
+//            head is read once per head block, coalesced (HDP/8 lanes x 16
+//            bytes, HDP = the head width rounded up to 64, 128 or 256; lanes
+//            past the width load nothing), and serves the block's query
+//            heads: every lane holds 8 dims of q for each of them, the
+//            partial dots of a row are reduced over its lanes with DPP; each
+//            wave keeps its own max, sum of exp(s - max) and P.V per head in
+//            registers, and the four waves are merged once at the end of the
+//            tile. Any group size (heads per KV head) and any head width that
+//            is a multiple of 8, up to 256.
 //   combine: one workgroup per (query head, sequence, 32 dims):
 //            M = max m_s, L = sum l_s exp(m_s - M),
 //            out = sum acc_s exp(m_s - M) / L, in parallel over splits.
@@ -65,6 +69,7 @@ struct FlashArgs {
   const uint16_t* vc[kFdMaxSeq];
   int pos[kFdMaxSeq];  // attends to rows 0..=pos of sequence s
   int n_heads, n_kv_heads, max_splits, rows_per_split;
+  int hd, group, head_blocks;  // head width, query heads per KV head, blocks of GB of them
   float scale;  // 1 / sqrt(hd), as attention.rs:172 computes it
   float* part;  // [n_seq][n_heads][max_splits][hd + 2]: acc[hd], m, l
 };
@@ -82,13 +87,14 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// Sum over aligned groups of LPR lanes (8 or 16), every lane getting it.
+// Sum over aligned groups of LPR lanes (8, 16 or 32), every lane getting it.
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
   v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f<0x141>(v);  // row_half_mirror: the other quad of the 8-lane half
-  if constexpr (LPR == 16) v += dpp_f<0x140>(v);  // row_mirror: the other half of the row
+  if constexpr (LPR >= 16) v += dpp_f<0x140>(v);  // row_mirror: the other half of the row
+  if constexpr (LPR == 32) v += __shfl_xor(v, 16, 64);  // the other row of the 32-lane group
   return v;
 }
 
@@ -101,8 +107,11 @@ __device__ __forceinline__ void halves8(const uint4& w, float* x) {
   }
 }
 
-// HD: head width (64 or 128); G: query heads per KV head; ITER: rows each
-// lane group takes per tile (T = 4 waves * ITER * 512/HD rows).
+// HD: the padded head width (64, 128 or 256; a.hd <= HD is the real one, a
+// multiple of 8); G: query heads per workgroup (the block of a KV head's
+// group, a.group of them in all: block b takes heads b*G .. b*G+G-1 of the
+// group, those past a.group are computed on a valid head and not stored);
+// ITER: rows each lane group takes per tile (T = 4 waves * ITER * 512/HD rows).
 template <int HD, int G, int ITER>
 __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
   constexpr int LPR = HD / 8;      // lanes per cache row
@@ -112,35 +121,46 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
   __shared__ float s_acc[4][G][HD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = lane / LPR, sub = lane % LPR;
-  const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int split = blockIdx.x, seq = blockIdx.z;
+  const int kvh = blockIdx.y / a.head_blocks, hblk = blockIdx.y % a.head_blocks;
   const int n = a.pos[seq] + 1;
   const int r0 = split * T;
   if (r0 >= n) return;  // uniform: past this sequence's window
-  const int kv_stride = a.n_kv_heads * HD;
-  const uint16_t* kb = a.kc[seq] + (size_t)kvh * HD + sub * 8;
-  const uint16_t* vb = a.vc[seq] + (size_t)kvh * HD + sub * 8;
+  const int hd = a.hd;
+  const bool live = sub * 8 < hd;  // this lane's 8 dims lie inside the head
+  const int kv_stride = a.n_kv_heads * hd;
+  const uint16_t* kb = a.kc[seq] + (size_t)kvh * hd + sub * 8;
+  const uint16_t* vb = a.vc[seq] + (size_t)kvh * hd + sub * 8;
   const int wrow0 = r0 + wave * ITER * RPI + rg;  // this lane group's first row
   // every K and V load of the tile in flight at once (rows past the window
-  // read row n-1 and are masked below)
+  // read row n-1 and are masked below; lanes past the width read nothing)
   uint4 kr[ITER], vr[ITER];
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     const int row = min(wrow0 + it * RPI, n - 1);
-    kr[it] = ld_stream(kb + (size_t)row * kv_stride);
+    kr[it] = live ? ld_stream(kb + (size_t)row * kv_stride) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int it = 0; it < ITER; it++) {
     const int row = min(wrow0 + it * RPI, n - 1);
-    vr[it] = ld_stream(vb + (size_t)row * kv_stride);
+    vr[it] = live ? ld_stream(vb + (size_t)row * kv_stride) : make_uint4(0, 0, 0, 0);
   }
   float qv[G][8];
-  const int h0 = kvh * G;
+  const int gb0 = hblk * G;                       // first head of the block within the group
+  const int h0 = kvh * a.group + gb0;             // its query head index
+  const int nh_here = min(G, a.group - gb0);      // heads of the block inside the group
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0 + g) * HD + sub * 8);
-    const float4 x0 = qp[0], x1 = qp[1];
-    qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
-    qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+    const int h = h0 + min(g, nh_here - 1);
+    if (live) {
+      const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h) * hd + sub * 8);
+      const float4 x0 = qp[0], x1 = qp[1];
+      qv[g][0] = x0.x; qv[g][1] = x0.y; qv[g][2] = x0.z; qv[g][3] = x0.w;
+      qv[g][4] = x1.x; qv[g][5] = x1.y; qv[g][6] = x1.z; qv[g][7] = x1.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) qv[g][k] = 0.0f;
+    }
 #pragma unroll
     for (int k = 0; k < 8; k++) qv[g][k] *= a.scale;  // (q/sqrt(hd)).k
   }
@@ -207,7 +227,7 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-      for (int k = 0; k < 8; k++) s_acc[wave][g][sub * 8 + k] = acc[g][k];
+      for (int k = 0; k < 8; k++) s_acc[wave][g][sub * 8 + k] = acc[g][k];  // (zeros past the width)
   if (lane == 0)
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -217,10 +237,11 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
   __syncthreads();
   // merge the waves: M = max m_w, each state scaled by exp(m_w - M) (0 for a
   // wave past the window; wave 0 holds row r0 < n, so M is finite)
-  float* base = a.part + (((size_t)seq * a.n_heads + h0) * a.max_splits + split) * (HD + 2);
-  const size_t hstride = (size_t)a.max_splits * (HD + 2);
+  float* base = a.part + (((size_t)seq * a.n_heads + h0) * a.max_splits + split) * (hd + 2);
+  const size_t hstride = (size_t)a.max_splits * (hd + 2);
   for (int e = tid; e < G * HD; e += kFdNT) {
     const int g = e / HD, d = e % HD;
+    if (g >= nh_here || d >= hd) continue;
     const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
     float o = 0.0f;
 #pragma unroll
@@ -228,14 +249,14 @@ __global__ __launch_bounds__(kFdNT) void flash_split_kernel(FlashArgs a) {
       if (s_m[w][g] != -INFINITY) o = fmaf(s_acc[w][g][d], __expf(s_m[w][g] - M), o);
     base[g * hstride + d] = o;
   }
-  if (tid < G) {
+  if (tid < nh_here) {
     const float M = fmaxf(fmaxf(s_m[0][tid], s_m[1][tid]), fmaxf(s_m[2][tid], s_m[3][tid]));
     float l = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; w++)
       if (s_m[w][tid] != -INFINITY) l = fmaf(s_l[w][tid], __expf(s_m[w][tid] - M), l);
-    base[tid * hstride + HD] = M;
-    base[tid * hstride + HD + 1] = l;
+    base[tid * hstride + hd] = M;
+    base[tid * hstride + hd + 1] = l;
   }
 }
 
@@ -270,7 +291,7 @@ __global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c, int
 #pragma unroll
     for (int k = 0; k < kFcBatch; k++) {
       const int sp = min(sp0 + k * kFcPG, ns - 1);
-      av[k] = p[(size_t)sp * rec + d0 + dl];
+      av[k] = p[(size_t)sp * rec + min(d0 + dl, hd - 1)];
       mv[k] = p[(size_t)sp * rec + hd];
     }
   };
@@ -322,7 +343,7 @@ __global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c, int
   }
   s_o[pg][dl] = o;
   __syncthreads();
-  if (tid < kFcDims) {
+  if (tid < kFcDims && d0 + tid < hd) {
     float t = 0.0f;
 #pragma unroll
     for (int g = 0; g < kFcPG; g++) t += s_o[g][tid];
@@ -331,11 +352,13 @@ __global__ __launch_bounds__(kFcNT) void flash_combine_kernel(CombineArgs c, int
 }
 
 template <int HD, int G, int ITER>
-int launch_flash_t(const FlashArgs& a, const CombineArgs& c, int n_seq, hipStream_t s) {
-  hipLaunchKernelGGL((flash_split_kernel<HD, G, ITER>), dim3(a.max_splits, a.n_kv_heads, n_seq), dim3(kFdNT), 0, s,
-                     a);
+int launch_flash_t(FlashArgs a, const CombineArgs& c, int n_seq, hipStream_t s) {
+  a.head_blocks = (a.group + G - 1) / G;
+  hipLaunchKernelGGL((flash_split_kernel<HD, G, ITER>), dim3(a.max_splits, a.n_kv_heads * a.head_blocks, n_seq),
+                     dim3(kFdNT), 0, s, a);
   PRANA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(flash_combine_kernel, dim3(a.n_heads, n_seq, HD / kFcDims), dim3(kFcNT), 0, s, c, HD);
+  hipLaunchKernelGGL(flash_combine_kernel, dim3(a.n_heads, n_seq, (a.hd + kFcDims - 1) / kFcDims), dim3(kFcNT), 0, s,
+                     c, a.hd);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -346,18 +369,21 @@ int launch_flash_g(const FlashArgs& a, const CombineArgs& c, int iter, int n_seq
   return launch_flash_t<HD, G, 4>(a, c, n_seq, s);
 }
 
+// Heads per workgroup: the group itself when it is 1, 2 or 4, else blocks of
+// 8 (a group of 3 takes one block of 4; 5-7 one of 8, the spare heads
+// computed and not stored; larger groups several blocks of 8).
 template <int HD>
 int launch_flash_hd(const FlashArgs& a, const CombineArgs& c, int g, int iter, int n_seq, hipStream_t s) {
-  switch (g) {
-    case 1: return launch_flash_g<HD, 1>(a, c, iter, n_seq, s);
-    case 2: return launch_flash_g<HD, 2>(a, c, iter, n_seq, s);
-    case 4: return launch_flash_g<HD, 4>(a, c, iter, n_seq, s);
-    case 8: return launch_flash_g<HD, 8>(a, c, iter, n_seq, s);
-  }
-  return fail(kErrUnsupported, "flash decode: query heads per KV head must be 1, 2, 4 or 8");
+  if (g == 1) return launch_flash_g<HD, 1>(a, c, iter, n_seq, s);
+  if (g == 2) return launch_flash_g<HD, 2>(a, c, iter, n_seq, s);
+  if (g <= 4) return launch_flash_g<HD, 4>(a, c, iter, n_seq, s);
+  return launch_flash_g<HD, 8>(a, c, iter, n_seq, s);
 }
 
 }  // namespace
+
+// The head width the split kernel's lanes cover: 64, 128 or 256.
+static size_t flash_padded_hd(size_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
 
 // Tile size: long windows take T = 4 waves * 8 rows per lane group (small
 // enough in registers for several workgroups per CU, whose load and compute
@@ -365,8 +391,7 @@ int launch_flash_hd(const FlashArgs& a, const CombineArgs& c, int g, int iter, i
 // over the CUs.
 FlashPlan flash_decode_plan(const size_t* pos, size_t n_seq, size_t n_heads, size_t n_kv_heads, size_t hd) {
   FlashPlan p{};
-  const int g = static_cast<int>(n_heads / std::max<size_t>(n_kv_heads, 1));
-  const int rpi = static_cast<int>(512 / std::max<size_t>(hd, 1));
+  const int rpi = static_cast<int>(512 / flash_padded_hd(hd));
   size_t max_rows = 0;
   for (size_t i = 0; i < n_seq; i++) max_rows = std::max(max_rows, pos[i] + 1);
   const int big_iter = 8;
@@ -384,7 +409,7 @@ int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const u
                         float* part_buf, size_t part_floats, hipStream_t s) {
   PRANA_CHECK(n_seq >= 1 && n_seq <= static_cast<size_t>(kFdMaxSeq), "flash decode: 1..16 sequences per call");
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "flash decode: n_heads must be a multiple of n_kv_heads");
-  PRANA_CHECK(hd == 64 || hd == 128, "flash decode: head_dim must be 64 or 128");
+  PRANA_CHECK(hd > 0 && hd <= 256 && hd % 8 == 0, "flash decode: head_dim must be a multiple of 8 up to 256");
   PRANA_CHECK(q && out && k_caches && v_caches && pos && part_buf, "flash decode: null argument");
   const FlashPlan plan = flash_decode_plan(pos, n_seq, n_heads, n_kv_heads, hd);
   PRANA_CHECK(part_floats >= plan.scratch_floats, "flash decode: partial-state buffer below the plan's size");
@@ -393,6 +418,8 @@ int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const u
   a.q = q;
   for (size_t i = 0; i < n_seq; i++) {
     PRANA_CHECK(k_caches[i] && v_caches[i], "flash decode: null cache pointer");
+    PRANA_CHECK(reinterpret_cast<uintptr_t>(k_caches[i]) % 16 == 0 && reinterpret_cast<uintptr_t>(v_caches[i]) % 16 == 0,
+                "flash decode: caches must be 16-byte aligned");
     PRANA_CHECK(pos[i] < 0x7fffffffu, "flash decode: position out of range");
     a.kc[i] = k_caches[i];
     a.vc[i] = v_caches[i];
@@ -403,14 +430,18 @@ int launch_flash_decode(const float* q, const uint16_t* const* k_caches, const u
   a.n_kv_heads = static_cast<int>(n_kv_heads);
   a.max_splits = plan.max_splits;
   a.rows_per_split = plan.rows_per_split;
+  a.hd = static_cast<int>(hd);
+  a.group = static_cast<int>(n_heads / n_kv_heads);
   a.scale = 1.0f / sqrtf(static_cast<float>(hd));
   a.part = part_buf;
   c.part = part_buf;
   c.n_heads = a.n_heads;
   c.max_splits = a.max_splits;
   c.out = out;
-  const int g = static_cast<int>(n_heads / n_kv_heads);
-  if (hd == 128) return launch_flash_hd<128>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
+  const int g = a.group;
+  const size_t hdp = flash_padded_hd(hd);
+  if (hdp == 256) return launch_flash_hd<256>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
+  if (hdp == 128) return launch_flash_hd<128>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
   return launch_flash_hd<64>(a, c, g, plan.iter, static_cast<int>(n_seq), s);
 }
 
