@@ -755,13 +755,43 @@ static void one_head(const float *qv, const uint16_t *kc, const uint16_t *vc, co
   }
 }
 
+/* Heads are independent outputs; long windows deal them to threads. */
+typedef struct {
+  const float *q;
+  const uint16_t *kc, *vc;
+  size_t pos, n_heads, group, kv_stride, hd, first, step;
+  float *out;
+} head_job;
+
+static void *head_rows(void *p) {
+  head_job *j = p;
+  float *scores = malloc((j->pos + 1) * sizeof(float)), *probs = malloc((j->pos + 1) * sizeof(float));
+  for (size_t h = j->first; h < j->n_heads; h += j->step)
+    one_head(j->q + h * j->hd, j->kc, j->vc, NULL, NULL, j->pos, h / j->group, j->kv_stride, j->hd,
+             j->out + h * j->hd, scores, probs);
+  free(scores); free(probs);
+  return NULL;
+}
+
 void po_attention_decode(const float *q, const uint16_t *kc, const uint16_t *vc, size_t pos,
                          size_t n_heads, size_t n_kv_heads, size_t hd, float *out) {
-  size_t kv_stride = n_kv_heads * hd, group = n_heads / n_kv_heads;
-  float *scores = malloc((pos + 1) * sizeof(float)), *probs = malloc((pos + 1) * sizeof(float));
-  for (size_t h = 0; h < n_heads; h++)
-    one_head(q + h * hd, kc, vc, NULL, NULL, pos, h / group, kv_stride, hd, out + h * hd, scores, probs);
-  free(scores); free(probs);
+  head_job base = {q, kc, vc, pos, n_heads, n_heads / n_kv_heads, n_kv_heads * hd, hd, 0, 1, out};
+  int nt = g_threads;
+  if (nt > 64) nt = 64;
+  if ((size_t)nt > n_heads) nt = (int)n_heads;
+  if (nt <= 1 || (pos + 1) * n_heads * hd < (1u << 18)) {
+    head_rows(&base);
+    return;
+  }
+  pthread_t th[64];
+  head_job jobs[64];
+  for (int t = 0; t < nt; t++) {
+    jobs[t] = base;
+    jobs[t].first = (size_t)t;
+    jobs[t].step = (size_t)nt;
+    pthread_create(&th[t], NULL, head_rows, &jobs[t]);
+  }
+  for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
 }
 
 void po_attention_verify(const float *q, const uint16_t *kc, const uint16_t *vc, size_t pos0, size_t seq,
@@ -771,15 +801,46 @@ void po_attention_verify(const float *q, const uint16_t *kc, const uint16_t *vc,
     po_attention_decode(q + i * q_stride, kc, vc, pos0 + i, n_heads, n_kv_heads, hd, out + i * q_stride);
 }
 
+/* Each (query row, head) output is computed by one_head alone, so the rows are
+ * dealt round-robin to threads (row i costs i + 1 dots); the bits do not depend
+ * on the split. */
+typedef struct {
+  const float *q, *k, *v;
+  size_t seq, n_heads, group, kv_stride, hd, first, step;
+  float *out;
+} attn_job;
+
+static void *attn_rows(void *p) {
+  attn_job *j = p;
+  size_t q_stride = j->n_heads * j->hd;
+  float *scores = malloc(j->seq * sizeof(float)), *probs = malloc(j->seq * sizeof(float));
+  for (size_t i = j->first; i < j->seq; i += j->step)
+    for (size_t h = 0; h < j->n_heads; h++)
+      one_head(j->q + i * q_stride + h * j->hd, NULL, NULL, j->k, j->v, i, h / j->group, j->kv_stride, j->hd,
+               j->out + i * q_stride + h * j->hd, scores, probs);
+  free(scores); free(probs);
+  return NULL;
+}
+
 void po_attention(const float *q, const float *k, const float *v, size_t seq, size_t n_heads,
                   size_t n_kv_heads, size_t hd, float *out) {
-  size_t kv_stride = n_kv_heads * hd, q_stride = n_heads * hd, group = n_heads / n_kv_heads;
-  float *scores = malloc(seq * sizeof(float)), *probs = malloc(seq * sizeof(float));
-  for (size_t i = 0; i < seq; i++)
-    for (size_t h = 0; h < n_heads; h++)
-      one_head(q + i * q_stride + h * hd, NULL, NULL, k, v, i, h / group, kv_stride, hd,
-               out + i * q_stride + h * hd, scores, probs);
-  free(scores); free(probs);
+  attn_job base = {q, k, v, seq, n_heads, n_heads / n_kv_heads, n_kv_heads * hd, hd, 0, 1, out};
+  int nt = g_threads;
+  if (nt > 64) nt = 64;
+  if ((size_t)nt > seq) nt = (int)seq;
+  if (nt <= 1 || seq < 64) {
+    attn_rows(&base);
+    return;
+  }
+  pthread_t th[64];
+  attn_job jobs[64];
+  for (int t = 0; t < nt; t++) {
+    jobs[t] = base;
+    jobs[t].first = (size_t)t;
+    jobs[t].step = (size_t)nt;
+    pthread_create(&th[t], NULL, attn_rows, &jobs[t]);
+  }
+  for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
 }
 
 /* ------------------------------------------------------------------ */

@@ -6,7 +6,8 @@ the oracle built from the same bytes:
     (matmul_q8_prefill / matmul_kquant_prefill, matmul.rs:185-232,
     kquant.rs:368-370);
   - C2: the full qwen2-0.5B-shape model, a 64-token prompt and 32 greedy steps
-    (stream, logits and KV cache rows);
+    (stream, logits and KV cache rows), and the stated 2048-token prefill with
+    512 greedy steps, 128 of them followed by the oracle;
   - C4: the 7B-shape layer (full width, two layers) after a 511-token prefill."""
 import numpy as np
 import pytest
@@ -100,22 +101,31 @@ def test_c4_width_prefill_511_then_decode():
 
 
 def test_c2_stated_2048_prefill_then_greedy():
-    # C2 as stated: 2048-token random prefill, then greedy decode (the first
-    # 16 of the 512 steps are compared; every step runs the same kernels)
+    # C2 as stated: 2048-token random prefill, then 512 greedy steps on the
+    # device; the oracle follows the first 128 of them token for token, and
+    # the cache rows those steps wrote and the logits after them are compared
+    # bit for bit
     cfg = dict(M.C2)
-    cfg["seq_len"] = 2100
+    cfg["seq_len"] = 2600
     t = M.c2_tensors(seed=2)
     g, o = P.Model(cfg, t), O.Model(cfg, t)
     prompt = np.random.default_rng(2048).integers(0, cfg["vocab_size"], 2048).astype(np.uint32)
-    gc, oc = g.cache(2100), o.cache(2100)
+    gc, oc = g.cache(2600), o.cache(2600)
     gc.prefill(prompt[:-1])
     oc.prefill(prompt[:-1])
     for layer in (0, 23):
         for which in (0, 1):
             assert np.array_equal(gc.read(layer, which, 2047), oc.read(layer, which, 2047)), (layer, which)
-    got = gc.decode(int(prompt[-1]), 2047, 16)
+    got = gc.decode(int(prompt[-1]), 2047, 512)
+    assert len(got) == 512
     tok, want = int(prompt[-1]), []
-    for i in range(16):
+    for i in range(128):
         tok = int(O.argmax(oc.forward(tok, 2047 + i)))
         want.append(tok)
-    assert list(got) == want
+    assert list(got[:128]) == want
+    for layer in (0, 11, 23):
+        for which in (0, 1):
+            assert np.array_equal(gc.read(layer, which, 2175), oc.read(layer, which, 2175)), (layer, which)
+    # step 129 again on both sides (the device rewrites row 2175 with the same
+    # token it decoded there): its logits, bit for bit
+    assert same_bits(gc.forward(want[-1], 2175), oc.forward(want[-1], 2175))

@@ -356,7 +356,9 @@ def test_c4_speculative_equals_plain_greedy(c4, k):
     cfg, t = c4
     g = P.Model(cfg, t)
     draft = P.Model(M.c4_draft_config(), M.synth_tensors(M.c4_draft_config(), M.types_c0, 1))
-    prompt = np.random.default_rng(44).integers(0, cfg["vocab_size"], 32).astype(np.uint32)
+    # the stated workload: a 512-token prompt, i.e. a 511-token prefill
+    # before the first speculative round
+    prompt = np.random.default_rng(44).integers(0, cfg["vocab_size"], 512).astype(np.uint32)
     plain, _ = g.generate(prompt, 24)
     spec, st = P.generate_speculative(g, draft, prompt, 24, k)
     assert list(spec) == list(plain)
