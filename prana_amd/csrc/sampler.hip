@@ -15,7 +15,8 @@
 // differently) is evaluated as the plain f32 subtraction from the exact value
 // before it; it either ends the walk (r <= 0) or starts the next scan. In the
 // lowest binade (e = -126, grid 2^-149 down to 0) only r <= 0 ends a segment.
-// Non-finite probabilities (and an initial r of 0) walk on one lane.
+// Spans holding a negative or non-finite probability, and an r that is not a
+// positive finite number, walk on one lane.
 #include <climits>
 
 #include "common.h"
@@ -61,9 +62,11 @@ __global__ __launch_bounds__(kPickNT) void sample_pick_kernel(const float* __res
 #pragma unroll
     for (int i = 0; i < kPickCT; i++) {
       v[i] = j0 + i < n ? p[j0 + i] : 0.0f;
-      bad |= !(v[i] <= 3.4028234663852886e38f);  // NaN or +inf
+      // the scan's pairs are decrements: negative, NaN and infinite terms
+      // (-0.0 included in neither) take the one-lane walk
+      bad |= !(v[i] >= 0.0f && v[i] <= 3.4028234663852886e38f);
     }
-    if (__syncthreads_or(bad) || !(r > 0.0f)) {
+    if (__syncthreads_or(bad) || !(r > 0.0f && r <= 3.4028234663852886e38f)) {
       if (tid == 0) {  // this span, one term at a time
         const int end = min(n, b + kPickSpan);
         float rr = r;

@@ -66,6 +66,30 @@ def test_pick_non_finite():
     assert P.sample_pick(p, np.float32(0.5)) == O.sample_pick(p, np.float32(0.5))
 
 
+def test_pick_negative_and_infinite_terms_and_r():
+    f = np.float32
+    # a negative term raises r: 0.75 -> 0.76 -> 0.51 -> 0.01, never <= 0
+    p = f([-0.01, 0.25, 0.5])
+    assert O.sample_pick(p, f(0.75)) == 2  # the last index, reached by running off the end
+    assert P.sample_pick(p, f(0.75)) == O.sample_pick(p, f(0.75))
+    q = f([-0.01, 0.25, 0.5, 0.5])
+    assert O.sample_pick(q, f(0.75)) == 3
+    assert P.sample_pick(q, f(0.75)) == 3
+    rng = np.random.default_rng(7)
+    for n in (50, 9000, 20000):
+        base = (rng.random(n) * 2.0 / n).astype(np.float32)
+        for where, val in ((n // 3, -0.25), (n // 2, -np.inf), (n - 1, -1e-3), (0, -0.0)):
+            p = base.copy()
+            p[where] = val
+            for r in (f(0.3), f(0.999), f(np.inf), f(0.0), f(-1.0)):
+                assert P.sample_pick(p, r) == O.sample_pick(p, r), (n, where, val, float(r))
+    # r = +inf never reaches <= 0 (inf - p stays inf), unless a term is +inf
+    p = np.full(20000, 1e-5, np.float32)
+    assert P.sample_pick(p, f(np.inf)) == 19999
+    p[123] = np.inf
+    assert P.sample_pick(p, f(np.inf)) == O.sample_pick(p, f(np.inf))
+
+
 @pytest.mark.parametrize("vocab,temp", [(32000, 0.8), (151936, 1.0), (48, 0.5), (32000, 0.0)])
 def test_sample_stream(vocab, temp):
     logits = (np.random.default_rng(vocab).standard_normal((30, vocab)) * 4).astype(np.float32)
