@@ -297,8 +297,10 @@ int prana_gguf_counts(prana_gguf_t g, uint32_t *version, size_t *n_tensors, size
 /* Name of the index-th tensor of the directory (file order). */
 int prana_gguf_tensor_name(prana_gguf_t g, size_t index, char *buf, size_t cap, size_t *len);
 /* TensorInfo (gguf.rs:133-138): ggml type, dims in ggml order (dims[0] =
- * contiguous; dims holds up to 8), and the byte size of its data, checked
- * against the data section (Gguf::raw, gguf.rs:202-205). */
+ * contiguous), and the byte size of its data, checked against the data
+ * section (Gguf::raw, gguf.rs:202-205). dims holds up to 8: a tensor with more
+ * gives PRANA_ERR_SHORT_BUFFER unless dims is NULL (then *n_dims says how many
+ * it has; its data and f32 readers take any count). */
 int prana_gguf_tensor_info(prana_gguf_t g, const char *name, int *ggml_type, uint64_t *dims, int *n_dims,
                            size_t *nbytes);
 /* The tensor's bytes in place (valid until prana_gguf_close). */

@@ -729,6 +729,9 @@ int prana_gguf_tensor_info(prana_gguf_t g, const char* name, int* ggml_type, uin
     const uint8_t* b;
     size_t nb;
     if (int rc = g->g->raw(name, &t, &b, &nb)) return rc;
+    if (dims && t->dims.size() > 8)
+      return fail(kErrShortBuffer, "tensor '" + std::string(name) + "' has " + std::to_string(t->dims.size()) +
+                                       " dimensions; dims holds 8");
     if (ggml_type) *ggml_type = static_cast<int>(t->type);
     if (n_dims) *n_dims = static_cast<int>(t->dims.size());
     if (dims)

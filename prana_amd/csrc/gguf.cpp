@@ -22,7 +22,9 @@ namespace prana {
 namespace {
 
 constexpr uint32_t kGgufMagic = 0x46554747u;  // "GGUF" little-endian
-constexpr uint32_t kMaxDims = 8;
+// Arrays of arrays are read to this depth; a deeper file is refused rather
+// than recursed into without bound.
+constexpr int kMaxNesting = 16;
 
 struct Cursor {
   const uint8_t* p;
@@ -49,9 +51,11 @@ struct Cursor {
   }
 };
 
-// Reader::value (gguf.rs:102-130): value types 0..12. Returns 0, or 1 for a
-// truncated file, or 2 for an unknown value type.
-int read_value(Cursor& c, uint32_t ty, GValue* v) {
+// Reader::value (gguf.rs:102-130): value types 0..12, arrays of any element
+// type including arrays. Returns 0, or 1 for a truncated file, 2 for an
+// unknown value type (stored in *bad), 3 for arrays nested deeper than
+// kMaxNesting.
+int read_value(Cursor& c, uint32_t ty, GValue* v, uint32_t* bad, int depth = 0) {
   v->type = ty;
   switch (ty) {
     case 0: { uint8_t x; if (!c.pod(&x)) return 1; v->u = x; return 0; }
@@ -66,20 +70,20 @@ int read_value(Cursor& c, uint32_t ty, GValue* v) {
     case 9: {
       uint64_t count;
       if (!c.pod(&v->elem_type) || !c.pod(&count)) return 1;
-      // Nested arrays appear in no llama / qwen2 / gemma key; refusing them
-      // keeps every element at one byte or more, so count is bounded by the
-      // bytes left.
-      if (v->elem_type == 9) return 2;
+      if (v->elem_type == 9 && count > 0 && depth + 1 >= kMaxNesting) return 3;
+      // every element takes at least one byte (a nested array's header 12),
+      // so a count beyond the bytes left is a truncated file
       if (count > c.n - c.off) return 1;
       v->arr.resize(static_cast<size_t>(count));
       for (auto& e : v->arr)
-        if (int rc = read_value(c, v->elem_type, &e)) return rc;
+        if (int rc = read_value(c, v->elem_type, &e, bad, depth + 1)) return rc;
       return 0;
     }
     case 10: { uint64_t x; if (!c.pod(&x)) return 1; v->u = x; return 0; }
     case 11: { int64_t x; if (!c.pod(&x)) return 1; v->i = x; return 0; }
     case 12: { double x; if (!c.pod(&x)) return 1; v->f = x; return 0; }
   }
+  *bad = ty;
   return 2;
 }
 
@@ -205,10 +209,15 @@ int Gguf::parse() {  // Gguf::from_bytes (gguf.rs:162-196)
     uint32_t ty;
     GValue v;
     if (!c.str(&key) || !c.pod(&ty)) return fail(kErrInvalid, "gguf truncated");
-    if (int rc = read_value(c, ty, &v))
-      return rc == 1 ? fail(kErrInvalid, "gguf truncated")
-                     : fail(kErrUnsupported, "unsupported gguf value type " +
-                                                 std::to_string(ty == 9 ? v.elem_type : ty) + " ('" + key + "')");
+    uint32_t bad = 0;
+    if (int rc = read_value(c, ty, &v, &bad)) {
+      if (rc == 1) return fail(kErrInvalid, "gguf truncated");
+      if (rc == 3)
+        return fail(kErrUnsupported, "gguf arrays nested deeper than " + std::to_string(kMaxNesting) + " ('" + key +
+                                         "')");
+      return fail(kErrUnsupported, "unsupported gguf value type " + std::to_string(bad) + " ('" +
+                                       key + "')");
+    }
     meta[key] = std::move(v);
   }
   for (uint64_t i = 0; i < n_tensors; i++) {
@@ -216,7 +225,7 @@ int Gguf::parse() {  // Gguf::from_bytes (gguf.rs:162-196)
     uint32_t nd;
     GTensor t;
     if (!c.str(&name) || !c.pod(&nd)) return fail(kErrInvalid, "gguf truncated");
-    if (nd > kMaxDims) return fail(kErrInvalid, "tensor '" + name + "': " + std::to_string(nd) + " dimensions");
+    if (nd > (c.n - c.off) / 8) return fail(kErrInvalid, "gguf truncated");  // 8 bytes per dim
     t.dims.resize(nd);
     for (auto& d : t.dims)
       if (!c.pod(&d)) return fail(kErrInvalid, "gguf truncated");

@@ -221,6 +221,65 @@ def test_unknown_value_type_and_huge_array():
         P.Gguf(data=w.to_bytes())
 
 
+def nested(depth, leaf=b""):
+    """An array value nested `depth` levels deep: each level one array of one
+    array, the innermost an empty array of u8 (or `leaf` after its header)."""
+    raw = struct.pack("<IQ", W.U8, 0) + leaf
+    for _ in range(depth - 1):
+        raw = struct.pack("<IQ", W.ARR, 1) + raw
+    return raw
+
+
+def test_nested_arrays_parse_like_the_reference():
+    # Reader::value (gguf.rs:118-125) reads arrays of arrays; the entries after
+    # them still parse, and the array reports its element type
+    inner = struct.pack("<IQ", W.U32, 2) + struct.pack("<II", 7, 8)
+    empty = struct.pack("<IQ", W.ARR, 0)
+    w = W.Writer().kv_raw(W.gstr("arrs") + struct.pack("<IIQ", W.ARR, W.ARR, 2) + inner + inner)
+    w.kv_raw(W.gstr("none") + struct.pack("<I", W.ARR) + empty)
+    w.kv_raw(W.gstr("deep") + struct.pack("<I", W.ARR) + nested(16))
+    w.kv("after", W.U32, 5)
+    g = P.Gguf(data=w.to_bytes())
+    assert g.meta_type("arrs") == (W.ARR, W.ARR)
+    assert g.meta_type("none") == (W.ARR, W.ARR)
+    assert g.meta_usize("after") == 5
+    # an unknown element type inside a nested array is named
+    bad = struct.pack("<IQ", W.ARR, 1) + struct.pack("<IQ", 13, 1) + b"\0" * 8
+    with pytest.raises(P.PranaError, match="unsupported gguf value type 13"):
+        P.Gguf(data=W.Writer().kv_raw(W.gstr("x") + struct.pack("<I", W.ARR) + bad).to_bytes())
+    # deeper than 16 levels is refused (the reference would recurse), and a
+    # nested count beyond the file's bytes is a truncation
+    with pytest.raises(P.PranaError, match="nested deeper than 16"):
+        P.Gguf(data=W.Writer().kv_raw(W.gstr("x") + struct.pack("<I", W.ARR) + nested(17)).to_bytes())
+    huge = struct.pack("<IQ", W.ARR, 1) + struct.pack("<IQ", W.ARR, 1 << 40)
+    with pytest.raises(P.PranaError, match="truncated"):
+        P.Gguf(data=W.Writer().kv_raw(W.gstr("x") + struct.pack("<I", W.ARR) + huge).to_bytes())
+
+
+def test_tensor_with_many_dimensions():
+    # TensorInfo keeps any number of dims (gguf.rs:179-186); the library opens
+    # the file and reads the data; only the fixed 8-entry dims buffer of
+    # prana_gguf_tensor_info refuses more
+    dims = [1, 2, 1, 1, 3, 1, 1, 1, 1, 2]
+    vals = np.arange(12, dtype=np.float32)
+    w = W.Writer().tensor("t10", dims, 0, vals.tobytes()).tensor("t2", [3, 2], 0, vals[:6].tobytes())
+    g = P.Gguf(data=w.to_bytes())
+    assert g.tensor_f32("t10").tolist() == vals.tolist()
+    assert g.tensor_bytes("t10") == vals.tobytes()
+    assert g.tensor_info("t2")[1] == [3, 2]
+    with pytest.raises(P.PranaError, match="has 10 dimensions"):
+        g.tensor_info("t10")
+    import ctypes as C
+    nd = C.c_int()
+    assert P.load().prana_gguf_tensor_info(g.h, b"t10", None, None, C.byref(nd), None) == 0 and nd.value == 10
+    # a dims count beyond the file's bytes is a truncation, not an allocation
+    raw = bytearray(w.to_bytes())
+    at = raw.index(b"t10") + 3
+    raw[at:at + 4] = struct.pack("<I", 1 << 30)
+    with pytest.raises(P.PranaError, match="truncated"):
+        P.Gguf(data=bytes(raw))
+
+
 def test_tensor_type_and_alignment_errors():
     w = W.Writer().tensor("q41", [32], 3, b"\0" * 20).tensor("odd", [48], P.Q4_0, b"\0" * 27)
     w.tensor("kq", [128], P.Q4_K, b"\0" * 144)
