@@ -56,6 +56,19 @@ struct Acts {
   const int* sm;
 };
 
+// One 32-element block of the activations out of LDS (its 32 int8 values, scale
+// and sum), read once and shared by every unit of a lane that sits on the
+// same block.
+struct ActBlk {
+  int4 a0, a1;
+  float sa;
+  int sm;
+  __device__ static ActBlk at(const Acts& a, int b) {
+    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
+    return ActBlk{aw[0], aw[1], a.sa[b], a.sm[b]};
+  }
+};
+
 template <int KIND>
 struct Fmt;
 
@@ -304,9 +317,9 @@ struct RegUnit<kKindQ4_0> {
     q = *reinterpret_cast<const int4*>(qp);
     d = *reinterpret_cast<const uint16_t*>(sp);
   }
-  __device__ void terms(const Acts& a, int b, float* t) const {
-    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
-    const int4 a0 = aw[0], a1 = aw[1];
+  // sum_j (nibble_j - 8) * qa_j over the block, from the stored nibbles
+  // (unsigned, one dot per half) and the activations' sum
+  __device__ int isum(const int4& a0, const int4& a1, int sm) const {
     int s = 0;
     s = sdot4(q.x & kMask, a0.x, s);
     s = sdot4(q.y & kMask, a0.y, s);
@@ -316,27 +329,19 @@ struct RegUnit<kKindQ4_0> {
     s = sdot4((q.y >> 4) & kMask, a1.y, s);
     s = sdot4((q.z >> 4) & kMask, a1.z, s);
     s = sdot4((q.w >> 4) & kMask, a1.w, s);
-    s -= 8 * a.sm[b];
-    t[0] = f16_to_f32(static_cast<uint16_t>(d)) * a.sa[b] * static_cast<float>(s);
+    return s - 8 * sm;
   }
+  __device__ void terms_blk(const ActBlk& ab, float* t) const {
+    t[0] = f16_to_f32(static_cast<uint16_t>(d)) * ab.sa * static_cast<float>(isum(ab.a0, ab.a1, ab.sm));
+  }
+  __device__ void terms(const Acts& a, int b, float* t) const { terms_blk(ActBlk::at(a, b), t); }
   // The block's integer dot s = sum_j (nibble_j - 8) * qa_j (|s| <= 32*8*127,
   // so 16 bits) packed above the block's f16 scale bits; term() of the word
   // and the activation scale gives terms()' value.
-  __device__ int slot(const Acts& a, int b) const {
-    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
-    const int4 a0 = aw[0], a1 = aw[1];
-    int s = 0;
-    s = sdot4(q.x & kMask, a0.x, s);
-    s = sdot4(q.y & kMask, a0.y, s);
-    s = sdot4(q.z & kMask, a0.z, s);
-    s = sdot4(q.w & kMask, a0.w, s);
-    s = sdot4((q.x >> 4) & kMask, a1.x, s);
-    s = sdot4((q.y >> 4) & kMask, a1.y, s);
-    s = sdot4((q.z >> 4) & kMask, a1.z, s);
-    s = sdot4((q.w >> 4) & kMask, a1.w, s);
-    s -= 8 * a.sm[b];
-    return static_cast<int>((d & 0xffffu) | (static_cast<uint32_t>(s) << 16));
+  __device__ int slot_blk(const ActBlk& ab) const {
+    return static_cast<int>((d & 0xffffu) | (static_cast<uint32_t>(isum(ab.a0, ab.a1, ab.sm)) << 16));
   }
+  __device__ int slot(const Acts& a, int b) const { return slot_blk(ActBlk::at(a, b)); }
   // (the scale only feeds this product, so f16_operand's conversion gives
   // f16_to_f32's result; see common.h)
   __device__ static float term(int w, float sa) {
@@ -355,21 +360,20 @@ struct RegUnitQ8 {
     q1 = p[1];
     d = KIND == kKindQ8F ? *reinterpret_cast<const uint32_t*>(sp) : *reinterpret_cast<const uint16_t*>(sp);
   }
-  __device__ void terms(const Acts& a, int b, float* t) const {
-    const int4* aw = reinterpret_cast<const int4*>(a.w) + b * 2;
-    const int4 a0 = aw[0], a1 = aw[1];
+  __device__ void terms_blk(const ActBlk& ab, float* t) const {
     int s = 0;
-    s = sdot4(q0.x, a0.x, s);
-    s = sdot4(q0.y, a0.y, s);
-    s = sdot4(q0.z, a0.z, s);
-    s = sdot4(q0.w, a0.w, s);
-    s = sdot4(q1.x, a1.x, s);
-    s = sdot4(q1.y, a1.y, s);
-    s = sdot4(q1.z, a1.z, s);
-    s = sdot4(q1.w, a1.w, s);
+    s = sdot4(q0.x, ab.a0.x, s);
+    s = sdot4(q0.y, ab.a0.y, s);
+    s = sdot4(q0.z, ab.a0.z, s);
+    s = sdot4(q0.w, ab.a0.w, s);
+    s = sdot4(q1.x, ab.a1.x, s);
+    s = sdot4(q1.y, ab.a1.y, s);
+    s = sdot4(q1.z, ab.a1.z, s);
+    s = sdot4(q1.w, ab.a1.w, s);
     float dv = KIND == kKindQ8F ? __uint_as_float(d) : f16_to_f32(static_cast<uint16_t>(d));
-    t[0] = dv * a.sa[b] * static_cast<float>(s);
+    t[0] = dv * ab.sa * static_cast<float>(s);
   }
+  __device__ void terms(const Acts& a, int b, float* t) const { terms_blk(ActBlk::at(a, b), t); }
 };
 template <>
 struct RegUnit<kKindQ8_0> : RegUnitQ8<kKindQ8_0> {};
@@ -462,6 +466,28 @@ constexpr int kNormNTSmall = 256;  // ... for rows of 513..1024 values
 constexpr int kNormMaxK = 4096;  // NORM rows: four values per lane
 constexpr int kSplitUAct = 4;    // units per unit lane per stage of a split gate|up launch (two stages in registers)
 constexpr int kSplitMaxStages = 16;
+constexpr int kSplitStage0 = 5;    // first stage counter in the split launch's LDS words
+constexpr int kSplitSB = kNormNT / 2 * kSplitUAct / 128;  // blocks per row per stage of a split launch
+constexpr int kXchPolls = 1 << 16; // bound on a split launch's wait for workgroup 0's norm
+
+// A tile's bound on its wait for the norm workgroup: kXchPolls unless
+// PRANA_SPLIT_WAIT_POLLS sets it (0 sends every tile to its own evaluation of
+// the sum, the path a wait that runs out takes; the tests use it).
+int split_wait_polls() {
+  const char* e = std::getenv("PRANA_SPLIT_WAIT_POLLS");  // (read per launch; a replayed graph keeps its value)
+  return e ? std::max(0, std::atoi(e)) : kXchPolls;
+}
+
+// Handoff words of a split launch, xch = {64-bit word, count}: the norm
+// workgroup publishes the word, each tile workgroup counts itself once it is
+// done with it (an atomic add whose result nobody waits for), and the norm
+// workgroup, once all have counted (or its wait runs out), sets both back to
+// zero for the next launch in the stream. A tile that finds the word zero
+// for longer than its own wait evaluates the sum itself, so a late reader
+// costs time, never bits.
+__device__ __forceinline__ void split_count_in(unsigned* xch) {
+  __hip_atomic_fetch_add(xch + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Orders this wave's LDS accesses before the ones that follow (a wait for
 // its outstanding LDS operations plus a compiler barrier) without waiting for
@@ -501,9 +527,10 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   constexpr int TPU = R::kTpu;
   const int tid = threadIdx.x;
   constexpr int NTL = SPLIT ? NT / 2 : NT;          // lanes holding weight units
-  // SPLIT: norm-wave barrier, flag, marked blocks, then one completion
-  // count per stage (unit waves that have stored the stage's dots)
-  __shared__ int s_dfr[SPLIT ? 3 + kSplitMaxStages : 1];
+  // SPLIT: norm-wave barrier, flag, marked blocks, the handoff's inv bits and
+  // outcome, then one completion count per stage (unit waves that have stored
+  // the stage's dots)
+  __shared__ int s_dfr[SPLIT ? kSplitStage0 + kSplitMaxStages : 1];
   const int lt = SPLIT ? tid - NT / 2 : tid;        // this lane's index among them
   const bool loader = !SPLIT || tid >= NT / 2;      // (uniform per wave)
   const int rt = job.rt, SB = job.sb;
@@ -603,6 +630,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     load_stage(buf0, 0);
     if (STAGED && n_stages > 1) load_stage(buf1, 1);
   }
+  float pacc = 0.0f;  // SPLIT: a row lane's fold, when the norm waves fold during the stream
   if constexpr (NORM && SPLIT) {
     // Deferred block scales (one token, Q4_0, K <= 4096). A block's term is
     // (d*sa)*float(s) with s an exact integer dot of the weights and the
@@ -647,7 +675,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
 #pragma unroll
       for (int j = 0; j < 8; j++) nx[j] = nw[j] = 0.0f;
     }
-    if (tid < 3 + kSplitMaxStages) s_dfr[tid] = 0;
+    if (tid < kSplitStage0 + kSplitMaxStages) s_dfr[tid] = 0;
     // the row loads are issued before this barrier, the weight loads after it
     __syncthreads();
     float* as_a = reinterpret_cast<float*>(sm8 + K);
@@ -663,15 +691,21 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
       const Acts a{reinterpret_cast<const int*>(sm8), as_a, am_a};
       auto stage_done = [&](int st) {  // this wave's dots of stage st are in LDS
         lds_order();
-        if ((tid & 63) == 0) __hip_atomic_fetch_add(&s_dfr[3 + st], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if ((tid & 63) == 0) __hip_atomic_fetch_add(&s_dfr[kSplitStage0 + st], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       };
+      // (the split geometry has NTL % SB == 0: all of a lane's units sit on
+      // block offset lt % SB and share one read of its activations)
       auto slot_stage = [&](const R* buf, int st) {
+        const int off = unit_off(0);
+        const int blk = st * SB + off;
+        if (blk < nb) {
+          const ActBlk av = ActBlk::at(a, blk);
 #pragma unroll
-        for (int i = 0; i < U; i++) {
-          const int row = unit_row(i), off = unit_off(i);
-          const int lr = ACT && row >= rt ? row - rt : row;
-          const int blk = st * SB + off;
-          if (blk < nb && lr < rows_here) slots[row * SR + blk] = buf[i].slot(a, blk);
+          for (int i = 0; i < U; i++) {
+            const int row = unit_row(i);
+            const int lr = ACT && row >= rt ? row - rt : row;
+            if (lr < rows_here) slots[row * SR + blk] = buf[i].slot_blk(av);
+          }
         }
       };
       if (!STAGED) {
@@ -714,13 +748,41 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
       }
       lds_order();  // this wave's q is in LDS
       if ((tid & 63) == 0) __hip_atomic_fetch_add(&s_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      // exact: norms.rs:9-23 in the reference's order, then quantize_acts
-      const float ss = exact::lanes_seq_sum<NT / 2, 8>(t8, K, tid, bar, [xs](int i) {
-        const float v = xs[exact::run_pad(i)];
-        return v * v;
-      });
-      const float mean_sq = ss / static_cast<float>(K);
-      const float inv = 1.0f / sqrtf(mean_sq + job.nin.eps);
+      // exact: norms.rs:9-23 in the reference's order, then quantize_acts.
+      // Every workgroup normalises the same row, so with a handoff buffer
+      // the launch's extra workgroup 0 (dispatched first) evaluates the sum
+      // and the tiles wait for its inv = 1/sqrt(ss/K + eps), their norm
+      // waves idle instead of competing with the unit waves for issue slots.
+      // A wait that runs out evaluates the sum here instead (same bits).
+      auto exact_inv = [&]() {
+        const float ss = exact::lanes_seq_sum<NT / 2, 8>(t8, K, tid, bar, [xs](int i) {
+          const float v = xs[exact::run_pad(i)];
+          return v * v;
+        });
+        const float mean_sq = ss / static_cast<float>(K);
+        return 1.0f / sqrtf(mean_sq + job.nin.eps);
+      };
+      // The handoff word holds (1 << 32) | bits(inv) once published, so one
+      // single-copy-atomic 64-bit load gives the flag and the value together;
+      // relaxed device-scope accesses throughout (an acquire would invalidate
+      // the caches that the weight stream runs through on every poll).
+      unsigned long long* const xch = reinterpret_cast<unsigned long long*>(job.nin.xch);
+      float inv;
+      {
+        if (tid == 0) {
+          unsigned long long w = 0;
+          for (int polls = 0; polls < job.nin.xch_polls; polls++) {
+            w = __hip_atomic_load(&xch[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (w >> 32) break;
+            __builtin_amdgcn_s_sleep(2);
+          }
+          s_dfr[3] = static_cast<int>(w & 0xffffffffu);
+          s_dfr[4] = static_cast<int>(w >> 32);
+        }
+        bar();  // the handoff's outcome is in LDS
+        inv = s_dfr[4] ? __int_as_float(s_dfr[3]) : exact_inv();  // (uniform)
+      }
+      if (tid == 0) split_count_in(job.nin.xch);
 #pragma unroll
       for (int j = 0; j < 8; j++) y[j] = nl ? nx[j] * inv * nw[j] : 0.0f;
       quantize_oct4(y, qe, &sc, &sm);
@@ -740,25 +802,58 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
           if (diff) __hip_atomic_fetch_add(&s_nmis, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       }
-      bar();  // every block's exact scale is in LDS
-      // the norm waves turn each stage's (row, block) words into f32 terms
-      // (d*sa)*float(s) as soon as the unit waves have stored the stage, so
-      // that only the fold remains after the workgroup barrier; lane l takes
-      // block column l % SB of the stage and every (NT/2)/SB-th row
+      bar();  // every block's exact scale and mark is in LDS
       const int unit_waves = NT / 2 / 64;
-      float* tf = reinterpret_cast<float*>(slots);
-      for (int st = 0; st < n_stages; st++) {
+      auto stage_wait = [&](int st) {  // until the unit waves have stored stage st
         for (int polls = 0; polls < (1 << 22); polls++) {
-          if (__hip_atomic_load(&s_dfr[3 + st], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= unit_waves) break;
+          if (__hip_atomic_load(&s_dfr[kSplitStage0 + st], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= unit_waves)
+            break;
           __builtin_amdgcn_s_sleep(1);
         }
         lds_order();
-        const int b = st * SB + tid % SB;
-        if (b < nb) {
-          const float scale = sx[b];
-          for (int row = tid / SB; row < ROWS; row += NT / 2 / SB) {
-            const int i = row * SR + b;
-            tf[i] = R::term(slots[i], scale);
+      };
+      if (s_nmis == 0) {
+        // no block changed q: the row lanes fold each stage's terms
+        // (d*sa)*float(s) in block order as soon as it is stored, so that
+        // only the last stage's adds remain once the weights are in
+        if (tid < ROWS) {
+          const int lr = ACT && tid >= rt ? tid - rt : tid;
+          const int* sr = slots + tid * SR;
+          for (int st = 0; st < n_stages; st++) {
+            stage_wait(st);
+            const int b0 = st * SB;
+            if (lr >= rows_here) continue;
+            if (b0 + kSplitSB <= nb && SB == kSplitSB) {
+              int w[kSplitSB];
+              float sc16[kSplitSB];
+#pragma unroll
+              for (int j = 0; j < kSplitSB; j++) {
+                w[j] = sr[b0 + j];
+                sc16[j] = sx[b0 + j];
+              }
+#pragma unroll
+              for (int j = 0; j < kSplitSB; j++) pacc += R::term(w[j], sc16[j]);
+            } else {
+              for (int b = b0; b < min(b0 + SB, nb); b++) pacc += R::term(sr[b], sx[b]);
+            }
+          }
+        }
+      } else {
+        // the norm waves turn each stage's (row, block) words into f32 terms
+        // as soon as the unit waves have stored the stage; the marked blocks
+        // are recomputed after the workgroup barrier, then folded with the
+        // rest. Lane l takes block column l % SB of the stage and every
+        // (NT/2)/SB-th row.
+        float* tf = reinterpret_cast<float*>(slots);
+        for (int st = 0; st < n_stages; st++) {
+          stage_wait(st);
+          const int b = st * SB + tid % SB;
+          if (b < nb) {
+            const float scale = sx[b];
+            for (int row = tid / SB; row < ROWS; row += NT / 2 / SB) {
+              const int i = row * SR + b;
+              tf[i] = R::term(slots[i], scale);
+            }
           }
         }
       }
@@ -851,18 +946,44 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
 
   auto process = [&](const R* buf, int s) {
     float* tb = terms + (s & 1) * buf_floats;
-#pragma unroll
-    for (int i = 0; i < U; i++) {
-      int row = unit_row(i), off = unit_off(i);
-      if constexpr (NORM) asm volatile("" : "+v"(row), "+v"(off));  // as in load_stage
-      const int lr = ACT && row >= rt ? row - rt : row;
+    bool shared = false;
+    if constexpr (R::kElems == 32) shared = NTL % SB == 0;
+    if (shared) {
+      // every unit of this lane sits on block offset lt % SB: one read of
+      // that activation block per token serves all U of them
+      int off = unit_off(0);
+      if constexpr (NORM) asm volatile("" : "+v"(off));  // as in load_stage
       const int blk = s * SB + off;
-      if (loader && blk < nb && lr < rows_here) {
+      if (loader && blk < nb) {
         for (int t = 0; t < n_tok; t++) {
           const uint8_t* ab = sm8 + t * astride;
-          Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
-                 reinterpret_cast<const int*>(ab + K) + G};
-          buf[i].terms(a, blk, tb + (t * ROWS + row) * TS + off * TPU);
+          const ActBlk av = ActBlk::at(Acts{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
+                                            reinterpret_cast<const int*>(ab + K) + G},
+                                       blk);
+#pragma unroll
+          for (int i = 0; i < U; i++) {
+            int row = unit_row(i);
+            if constexpr (NORM) asm volatile("" : "+v"(row));
+            const int lr = ACT && row >= rt ? row - rt : row;
+            if constexpr (R::kElems == 32)
+              if (lr < rows_here) buf[i].terms_blk(av, tb + (t * ROWS + row) * TS + off * TPU);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < U; i++) {
+        int row = unit_row(i), off = unit_off(i);
+        if constexpr (NORM) asm volatile("" : "+v"(row), "+v"(off));  // as in load_stage
+        const int lr = ACT && row >= rt ? row - rt : row;
+        const int blk = s * SB + off;
+        if (loader && blk < nb && lr < rows_here) {
+          for (int t = 0; t < n_tok; t++) {
+            const uint8_t* ab = sm8 + t * astride;
+            Acts a{reinterpret_cast<const int*>(ab), reinterpret_cast<const float*>(ab + K),
+                   reinterpret_cast<const int*>(ab + K) + G};
+            buf[i].terms(a, blk, tb + (t * ROWS + row) * TS + off * TPU);
+          }
         }
       }
     }
@@ -896,7 +1017,9 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     const float* sx = reinterpret_cast<const float*>(qx + K);
     const int* smx = reinterpret_cast<const int*>(sx + G);
     const int* mism = smx + G;
-    if (s_dfr[2] > 0) {  // blocks the norm waves marked before the barrier above
+    if (s_dfr[2] == 0) {  // (uniform) the row lanes folded every stage already
+      if (folder) acc = pacc;
+    } else {  // blocks the norm waves marked before the barrier above
       // a block whose exact q differs from the published one: its dots are
       // recomputed from the exact activations (units re-read from memory)
       const Acts ax{reinterpret_cast<const int*>(qx), sx, smx};
@@ -913,25 +1036,25 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
         reinterpret_cast<float*>(slots)[row * SR + b] = R::term(u.slot(ax, b), sx[b]);
       }
       __syncthreads();
-    }
-    // one lane per row folds the terms (formed by the norm waves) in block order
-    const float* tf = reinterpret_cast<const float*>(slots);
-    if (folder) {
-      const float* tr = tf + fl_row * SR;
-      int i = 0;
-      for (; i + 8 <= nb; i += 8) {
-        float x0 = tr[i], x1 = tr[i + 1], x2 = tr[i + 2], x3 = tr[i + 3];
-        float x4 = tr[i + 4], x5 = tr[i + 5], x6 = tr[i + 6], x7 = tr[i + 7];
-        acc += x0;
-        acc += x1;
-        acc += x2;
-        acc += x3;
-        acc += x4;
-        acc += x5;
-        acc += x6;
-        acc += x7;
+      // one lane per row folds the terms (formed by the norm waves) in block order
+      const float* tf = reinterpret_cast<const float*>(slots);
+      if (folder) {
+        const float* tr = tf + fl_row * SR;
+        int i = 0;
+        for (; i + 8 <= nb; i += 8) {
+          float x0 = tr[i], x1 = tr[i + 1], x2 = tr[i + 2], x3 = tr[i + 3];
+          float x4 = tr[i + 4], x5 = tr[i + 5], x6 = tr[i + 6], x7 = tr[i + 7];
+          acc += x0;
+          acc += x1;
+          acc += x2;
+          acc += x3;
+          acc += x4;
+          acc += x5;
+          acc += x6;
+          acc += x7;
+        }
+        for (; i < nb; i++) acc += tr[i];
       }
-      for (; i < nb; i++) acc += tr[i];
     }
   } else if (!STAGED) {
     process(buf0, 0);
@@ -1033,12 +1156,63 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
   }
 }
 
+// The norm workgroup of a split gate|up launch with a handoff buffer: the
+// exact left-to-right sum of squares of the row (norms.rs:15) over all NT
+// lanes, four values each, then inv = 1/sqrt(ss/K + eps) (norms.rs:16-17)
+// published as (1 << 32) | bits(inv) in the buffer's 64-bit word, where the
+// tile workgroups wait for it. It streams no weights, so nothing competes
+// with the sum for issue slots; it re-arms the words once the tiles have read
+// them (split_count_in).
+template <int NT>
+__device__ __forceinline__ void split_norm_producer(const NormIn& nin, int K) {
+  extern __shared__ int4 smem4[];
+  float* xs = reinterpret_cast<float*>(smem4);  // the row (the sum's one-lane fallback)
+  const int tid = threadIdx.x;
+  const bool live = 4 * tid < K;
+  float4 x4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (live) x4 = reinterpret_cast<const float4*>(nin.x)[tid];
+  const float nx[4] = {x4.x, x4.y, x4.z, x4.w};
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) xs[exact::run_pad(4 * tid + j)] = nx[j];
+  }
+  float t4[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) t4[j] = nx[j] * nx[j];  // zero past K
+  const float ss = exact::quad_seq_sum<NT>(t4, K, [xs](int i) {
+    const float v = xs[exact::run_pad(i)];
+    return v * v;
+  });
+  if (tid == 0) {
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(K) + nin.eps);
+    unsigned long long* const word = reinterpret_cast<unsigned long long*>(nin.xch);
+    __hip_atomic_store(word, (1ull << 32) | __float_as_uint(inv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int polls = 0; polls < kXchPolls; polls++) {
+      if (__hip_atomic_load(nin.xch + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= gridDim.x - 1) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    __hip_atomic_store(nin.xch + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <int KIND, int U, bool ACT, bool STAGED, int NT, bool NORM = false, bool SPLIT = false>
 __global__ __launch_bounds__(NT) void gemv_tile_kernel(DecodeJob job, const int8_t* __restrict__ q,
                                                         const float* __restrict__ sa,
                                                         const int* __restrict__ sums, int n_tok) {
   int mi = 0, tile = blockIdx.x;
   if (!ACT) job_tile(job, &mi, &tile);
+  if constexpr (SPLIT) {  // workgroup 0 evaluates the norm for the tiles, which start at 1
+    if (blockIdx.x == 0) {
+      split_norm_producer<NT>(job.nin, static_cast<int>(job.m[0].cols));
+      return;
+    }
+    // Consecutive workgroups land on different XCDs (round robin); tile
+    // numbers are dealt so that each XCD streams one contiguous run of rows
+    // (every XCD then reads every memory channel alike).
+    const int b = blockIdx.x - 1, nt = gridDim.x - 1;
+    tile = nt % 8 == 0 ? (b % 8) * (nt / 8) + b / 8 : b;
+  }
   // decode's one-token launches get a copy of the body in which the token
   // loops fold away (the branch is uniform)
   if (n_tok == 1) gemv_tile_body<KIND, U, ACT, STAGED, NT, NORM, SPLIT>(job, q, sa, sums, 1, mi, tile);
@@ -1311,8 +1485,8 @@ TileGeom norm_split_act_geom(size_t K) {
     return TileGeom{0, 0, 0, 0};
   // (the norm waves convert a stage as columns of (kNormNT/2) % sb == 0
   // lanes, and the stage counters cover every stage)
-  constexpr int sb = kNormNT / 2 * kSplitUAct / 128;
-  static_assert((kNormNT / 2) % sb == 0, "stage columns tile the norm lanes");
+  constexpr int sb = kSplitSB;
+  static_assert((kNormNT / 2) % sb == 0, "stage columns tile the norm lanes; a unit lane's units share a block");
   return (nb + sb - 1) / sb <= kSplitMaxStages ? TileGeom{kSplitUAct, 64, sb, kNormNT} : TileGeom{0, 0, 0, 0};
 }
 
@@ -1370,6 +1544,15 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
   PRANA_CHECK(K <= 16384, "gemv: decode kernel supports cols <= 16384");
   PRANA_CHECK(rows_wg * g.sb == (SPLIT ? NT / 2 : NT) * U, "gemv: tile geometry mismatch");
   PRANA_CHECK(group >= 1, "gemv: decode tile exceeds LDS");
+  // a split launch leads with its norm workgroup, which hands inv over
+  if (SPLIT) {
+    PRANA_CHECK(job.nin.xch && reinterpret_cast<uintptr_t>(job.nin.xch) % 8 == 0,
+                "gemv: a split norm launch needs 8-byte-aligned handoff words");
+    job.nin.xch_polls = split_wait_polls();
+    PRANA_CHECK((static_cast<size_t>(exact::run_pad(static_cast<int>(K) - 1)) + 1) * 4 <= per_tok,
+                "gemv: split norm row exceeds the launch's LDS");
+    total += 1;
+  }
   for (size_t t0 = 0; t0 < n_tok; t0 += group) {
     const size_t nt = std::min<size_t>(group, n_tok - t0);
     DecodeJob j = job;
@@ -2718,7 +2901,8 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
     return dispatch_kind(gate.kind, [&](auto k) {
       constexpr int KIND = decltype(k)::value;
       if constexpr (RegUnit<KIND>::kElems == 32) {
-        const TileGeom gs = norm_split_act_geom<KIND>(gate.cols);
+        // (the split launch needs the handoff words for its norm workgroup)
+        const TileGeom gs = norm->xch ? norm_split_act_geom<KIND>(gate.cols) : TileGeom{0, 0, 0, 0};
         if constexpr (KIND == kKindQ4_0)
           if (gs.u == kSplitUAct)
             return launch_tile_u<KIND, kSplitUAct, true, true, kNormNT, -1, true, true>(job, gs, q, sa, sums, 1, s);

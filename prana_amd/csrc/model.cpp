@@ -246,6 +246,11 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
       return rc;
     ws.cap_tok = n;
   }
+  if (!ws.xch.p) {  // zeroed once; each launch that uses it leaves it zeroed
+    if ((rc = ws.xch.alloc(64))) return rc;
+    PRANA_HIP(hipMemset(ws.xch.p, 0, ws.xch.bytes));
+    ws.gen++;
+  }
   size_t need = (prefill_attn ? attention_scratch_floats(n_tok, c.n_heads, n_tok, false)
                               : attention_scratch_floats(n_tok, c.n_heads, ctx_cap)) * 4;
   const void* before = ws.scratch.p;
@@ -609,7 +614,7 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     if ((rc = apply(*L.w[kWo], n, ws.attn.as<float>(), ores, s))) return rc;
     // --- gated MLP block (infer.rs:191-203)
     // decode: the gate|up launch normalises x itself when its matrices allow it
-    const NormIn nin_ffn{x, L.vec[kRmsFfn].as<float>(), c.norm_eps};
+    const NormIn nin_ffn{x, L.vec[kRmsFfn].as<float>(), c.norm_eps, ws.xch.as<unsigned>()};
     const bool ffn_fused = mode == 0 && n == 1 && gemv_norm_act_fusable(L.w[kW1]->d, L.w[kW3]->d);
     if (!ffn_fused && (rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
     if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s, ffn_fused ? &nin_ffn : nullptr))) return rc;

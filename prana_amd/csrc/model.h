@@ -43,6 +43,7 @@ struct Workspace {
   DevBuf stream_out;  // device-side token stream of decode()
   DevBuf step_state;  // {position, step} of a replayed decode step
   DevBuf sampling;    // scaled logits, probabilities and uniform draws of sampled steps
+  DevBuf xch;         // norm handoff words of the split gate|up launch (NormIn::xch)
   size_t gen = 0;     // bumped whenever a buffer above moves
 };
 

@@ -285,6 +285,21 @@ def run_spec(k, tokens):
                       "decode_tok_s": round(st.generated_tokens / st.decode_seconds, 1)}), flush=True)
 
 
+def run_c2_decode(tokens):
+    """C2 decode alone (for a kernel trace of its steps): the qwen2-0.5B-shape
+    model of run_models, a warm-up call, then one timed generate call with a
+    2048-token prompt (2047-token prefill) and `tokens` greedy tokens."""
+    import prana_amd as P
+    from prana_amd import models as M
+
+    g = P.Model(M.C2, M.c2_tensors(seed=2))
+    prompt = np.random.default_rng(20261202).integers(0, M.C2["vocab_size"], 2048).astype(np.uint32)
+    g.generate(prompt[:64], 8)
+    _, st = g.generate(prompt, tokens)
+    print(json.dumps({"config": "C2", "generated_tokens": st.generated_tokens,
+                      "decode_tok_s": round(st.generated_tokens / st.decode_seconds, 1)}), flush=True)
+
+
 def models_table(rows):
     out = ["| config | case | prefill tok/s | decode tok/s | note |", "|---|---|---:|---:|---|"]
     for r in rows:
@@ -501,8 +516,9 @@ def main():
     ap.add_argument("--only", choices=["C1", "GEMM", "C3", "VERIFY", "ATTN"], help="run one configuration's sweep")
     ap.add_argument("--attn-counters", nargs="+", metavar="DB", help="attention counter table of --pmc runs of --only ATTN")
     ap.add_argument("--spec", type=int, metavar="K", help="C4 speculative decode alone, K drafts per round")
-    ap.add_argument("--tokens", type=int, default=48, help="tokens of the --spec call")
-    ap.add_argument("--round-trace", metavar="DB", help="per-kernel table of a kernel trace of --spec")
+    ap.add_argument("--tokens", type=int, default=48, help="tokens of the --spec or --c2-decode call")
+    ap.add_argument("--c2-decode", action="store_true", help="C2 decode alone (2048-token prompt, --tokens steps)")
+    ap.add_argument("--round-trace", metavar="DB", help="per-kernel table of a kernel trace of --spec or --c2-decode")
     ap.add_argument("--decode-trace", nargs=3, metavar=("DB", "BENCH_JSON", "COMMAND"),
                     help="summary of a kernel trace of bench.py (with the bench's JSON line and the trace command)")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
@@ -511,6 +527,8 @@ def main():
         print(models_table(run_models()))
     elif args.spec:
         run_spec(args.spec, args.tokens)
+    elif args.c2_decode:
+        run_c2_decode(args.tokens)
     elif args.round_trace:
         round_trace_summary(args.round_trace)
     elif args.decode_trace:

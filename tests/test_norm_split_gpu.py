@@ -1,7 +1,9 @@
 """GPU parity of the decode launches that normalise their own input at
 4096-wide rows (rmsnorm, norms.rs:9-23, fused into the Q|K|V and gate|up
-GEMVs): half of each workgroup's waves evaluate the exact left-to-right sum of
-squares while the other half streams the weights. The inputs are embedding
+GEMVs): in the Q|K|V launch every workgroup evaluates the exact left-to-right
+sum of squares; in the gate|up launch one workgroup evaluates it and hands
+the factor to the tiles, whose unit waves stream the weights meanwhile (or,
+with the wait switched off, each tile evaluates it itself). The inputs are embedding
 rows chosen to stress that sum (ties against the running sum, powers of two,
 subnormal squares, a wide dynamic range, zeros, a sum that overflows to inf
 and falls back to the one-lane fold), each decoded as a token of a one-layer
@@ -42,8 +44,12 @@ def stress_rows(dim, seed):
     return np.stack(rows).astype(np.float32)
 
 
-@pytest.mark.parametrize("ty", ["Q4_0", "Q8_0"])
-def test_split_norm_stress_rows_bitexact(ty):
+@pytest.mark.parametrize("ty,wait", [("Q4_0", None), ("Q8_0", None), ("Q4_0", "0")])
+def test_split_norm_stress_rows_bitexact(ty, wait, monkeypatch):
+    # wait "0": the gate|up tiles do not wait for the launch's norm workgroup
+    # and evaluate the sum themselves (the path of a wait that runs out)
+    if wait is not None:
+        monkeypatch.setenv("PRANA_SPLIT_WAIT_POLLS", wait)
     kind = {"Q4_0": M.Q4_0, "Q8_0": M.Q8_0}[ty]
     dim = 4096
     emb = stress_rows(dim, 4096 + kind)
