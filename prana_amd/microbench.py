@@ -436,13 +436,13 @@ def decode_trace_summary(db, bench_json, command):
         out.append(f"| `{short(n)}` | {cnt} | {avg / 1000:.2f} | {mn / 1000:.2f} | {mx / 1000:.2f} | {sm / 1e6:.2f} "
                    f"| {100 * sm / tot:.1f}% |")
     out.append(f"| (all kernels) | {sum(r[1] for r in rows)} | | | | {tot / 1e6:.2f} | 100% |")
-    shapes = {("gemv_tile_kernel<3, 4, false, false, 1024, true>", 192 * 1024):
+    shapes = {("gemv_tile_kernel<3, 4, false, false, 1024, true, false>", 192 * 1024):
               ("rmsnorm + Q\\|K\\|V 6144x4096 + RoPE", 14.16),
-              ("gemv_tile_kernel<3, 4, false, false, 256, false>", 512 * 256): ("wo 4096x4096", 9.44),
-              ("gemv_tile_kernel<3, 4, true, true, 1024, true>", 224 * 1024):
+              ("gemv_tile_kernel<3, 4, false, false, 256, false, false>", 512 * 256): ("wo 4096x4096", 9.44),
+              ("gemv_tile_kernel<3, 4, true, true, 1024, true, true>", 225 * 1024):
               ("rmsnorm + gate\\|up 2x14336x4096 + SiLU + quantize", 66.06),
-              ("gemv_tile_kernel<3, 7, false, false, 256, false>", 1024 * 256): ("down 4096x14336", 33.03),
-              ("gemv_tile_kernel<3, 4, false, false, 256, false>", 4000 * 256): ("LM head 32000x4096", 73.73)}
+              ("gemv_tile_kernel<3, 7, false, false, 256, false, false>", 1024 * 256): ("down 4096x14336", 33.03),
+              ("gemv_tile_kernel<3, 4, false, false, 256, false, false>", 4000 * 256): ("LM head 32000x4096", 73.73)}
     d = defaultdict(list)
     for name, dur, gx in c.execute("select name, duration, grid_x from kernels where name like '%gemv_tile_kernel%'"):
         d[(short(name), gx)].append(dur / 1000)
