@@ -478,15 +478,32 @@ int split_wait_polls() {
   return e ? std::max(0, std::atoi(e)) : kXchPolls;
 }
 
-// Handoff words of a split launch, xch = {64-bit word, count}: the norm
-// workgroup publishes the word, each tile workgroup counts itself once it is
-// done with it (an atomic add whose result nobody waits for), and the norm
-// workgroup, once all have counted (or its wait runs out), sets both back to
-// zero for the next launch in the stream. A tile that finds the word zero
-// for longer than its own wait evaluates the sum itself, so a late reader
-// costs time, never bits.
-__device__ __forceinline__ void split_count_in(unsigned* xch) {
-  __hip_atomic_fetch_add(xch + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Handoff words of a split launch, xch = {64-bit word, ..., one flag word per
+// tile}: the norm workgroup publishes the word, each tile sets its flag once
+// it is done with the word, and the norm workgroup, once every flag is set (or
+// its wait runs out), sets the word and the flags back to zero for the next
+// launch in the stream. A tile that finds the word zero for longer than its
+// own wait evaluates the sum itself, so a late reader costs time, never bits.
+constexpr int kXchIn = 64;  // words: the tiles' count-in flags
+constexpr int kXchMaxTiles = 512;
+static_assert((kXchIn + kXchMaxTiles) * 4 <= static_cast<int>(kNormXchBytes), "handoff words fit the buffer");
+
+// Each tile sets its own flag word with a device-scope store (many workgroups
+// adding to one counter serialise at its address); one wave of the norm
+// workgroup waits for all of them, lanes reading 64 apart. Bounded.
+__device__ __forceinline__ void split_count_in(unsigned* xch, int tile) {
+  __hip_atomic_store(xch + kXchIn + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void split_wait_counted(const unsigned* xch, int n) {
+  const int lane = threadIdx.x & 63;
+  for (int polls = 0; polls < kXchPolls; polls++) {
+    bool all = true;
+    for (int i = lane; i < n; i += 64)
+      all &= __hip_atomic_load(const_cast<unsigned*>(xch) + kXchIn + i, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    if (__builtin_amdgcn_ballot_w64(!all) == 0) return;
+    __builtin_amdgcn_s_sleep(8);
+  }
 }
 
 // Orders this wave's LDS accesses before the ones that follow (a wait for
@@ -782,7 +799,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
         bar();  // the handoff's outcome is in LDS
         inv = s_dfr[4] ? __int_as_float(s_dfr[3]) : exact_inv();  // (uniform)
       }
-      if (tid == 0) split_count_in(job.nin.xch);
+      if (tid == 0) split_count_in(job.nin.xch, static_cast<int>(blockIdx.x) - 1);
 #pragma unroll
       for (int j = 0; j < 8; j++) y[j] = nl ? nx[j] * inv * nw[j] : 0.0f;
       quantize_oct4(y, qe, &sc, &sm);
@@ -1183,16 +1200,17 @@ __device__ __forceinline__ void split_norm_producer(const NormIn& nin, int K) {
     const float v = xs[exact::run_pad(i)];
     return v * v;
   });
-  if (tid == 0) {
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(K) + nin.eps);
+  if (tid < 64) {  // publish inv; once every tile has read it, re-arm the words for the next launch
     unsigned long long* const word = reinterpret_cast<unsigned long long*>(nin.xch);
-    __hip_atomic_store(word, (1ull << 32) | __float_as_uint(inv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int polls = 0; polls < kXchPolls; polls++) {
-      if (__hip_atomic_load(nin.xch + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= gridDim.x - 1) break;
-      __builtin_amdgcn_s_sleep(8);
+    if (tid == 0) {
+      const float inv = 1.0f / sqrtf(ss / static_cast<float>(K) + nin.eps);
+      __hip_atomic_store(word, (1ull << 32) | __float_as_uint(inv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __hip_atomic_store(nin.xch + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int n = static_cast<int>(gridDim.x) - 1;
+    split_wait_counted(nin.xch, n);
+    for (int i = tid; i < n; i += 64)
+      __hip_atomic_store(nin.xch + kXchIn + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1549,6 +1567,7 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     PRANA_CHECK(job.nin.xch && reinterpret_cast<uintptr_t>(job.nin.xch) % 8 == 0,
                 "gemv: a split norm launch needs 8-byte-aligned handoff words");
     job.nin.xch_polls = split_wait_polls();
+    PRANA_CHECK(total <= kXchMaxTiles, "gemv: more split tiles than handoff flags");
     PRANA_CHECK((static_cast<size_t>(exact::run_pad(static_cast<int>(K) - 1)) + 1) * 4 <= per_tok,
                 "gemv: split norm row exceeds the launch's LDS");
     total += 1;

@@ -146,13 +146,14 @@ struct NormIn {
   const float* x;
   const float* w;
   float eps;
-  // optional: four zeroed, 8-byte-aligned words in device memory through which
-  // the split gate|up launch hands workgroup 0's norm factor to the other
-  // workgroups (a 64-bit flag|value word and a count; left zeroed again at the
-  // end of each launch; one launch at a time)
+  // optional: kNormXchBytes of zeroed, 8-byte-aligned device memory through
+  // which the split gate|up launch hands its norm workgroup's factor to the
+  // tiles (a 64-bit flag|value word, then one flag word per tile; left zeroed
+  // again at the end of each launch; one launch at a time)
   unsigned* xch = nullptr;
   int xch_polls = 0;  // (set by the launch)
 };
+constexpr size_t kNormXchBytes = 4096;
 // Whether launch_gemv_multi can take these matrices with a NormIn (one token):
 // block-32 formats, 512 < cols <= 4096, every tile's workgroup resident at once.
 bool gemv_norm_fusable(const DevMat* ms, int n);

@@ -247,7 +247,7 @@ int Model::ensure_ws(size_t n_tok, size_t ctx_cap, bool prefill_attn) {
     ws.cap_tok = n;
   }
   if (!ws.xch.p) {  // zeroed once; each launch that uses it leaves it zeroed
-    if ((rc = ws.xch.alloc(64))) return rc;
+    if ((rc = ws.xch.alloc(kNormXchBytes))) return rc;
     PRANA_HIP(hipMemset(ws.xch.p, 0, ws.xch.bytes));
     ws.gen++;
   }
