@@ -343,6 +343,38 @@ __device__ __forceinline__ void seg_push(SegAcc& acc, bool cross, Pair pr) {
   acc.c += cross ? 1 : 0;
 }
 
+// The walk of the predicted-binade scan (one wave): segment j's composed map
+// (te, to), the crossing term ct that starts it and the binade code ce of
+// that step sit in lane j. From the head's exact value sH it adds each
+// crossing as an f32 add and applies each segment's map to the exact value at
+// its start, checking that the start lies in the binade the map assumed and
+// that the end stays inside it. A value lies in binade E (e >= -126) exactly
+// when its count of E's ulps, val * 2^(23-E) (an exact scaling here), is in
+// [2^23, 2^24) ([0, 2^24) for E = -126), and that count is the m of
+// decompose(); the loop carries no early exit, only the check result (when a
+// check fails, the caller folds serially and drops this value).
+__device__ __forceinline__ float walk_segments(float sH, int K, int te, int to, float ct, int ce, bool* good_out) {
+  bool good = K <= kPredMaxCross;
+  const int Kc = min(K, kPredMaxCross);
+  float val = sH;
+  int E = binade_fast(sH);
+  for (int j = 0; j <= Kc; j++) {
+    if (j > 0) {
+      val = val + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct), j));
+      E = __builtin_amdgcn_readlane(ce, j);
+    }
+    if (E == kPredAmb) continue;  // an ambiguous crossing: its segment is empty
+    const float mf = ldexpf(val, 23 - E);
+    good &= (mf < 16777216.0f) & ((E == -126) | (mf >= 8388608.0f));  // false for inf and NaN too
+    const int32_t m = static_cast<int32_t>(fminf(mf, 16777216.0f));
+    const int32_t me = apply(Pair{__builtin_amdgcn_readlane(te, j), __builtin_amdgcn_readlane(to, j)}, m);
+    good &= me < (1 << 24);
+    val = ldexpf(static_cast<float>(me), E - 23);
+  }
+  *good_out = good;
+  return val;
+}
+
 // Barrier and OR-vote of a lane group (see group_seq_sum_pred): the
 // workgroup for NG == 1, else the calling wave.
 template <int NG>
@@ -613,26 +645,9 @@ __device__ inline float group_seq_sum_pred(Term a, int n, bool* ok) {
   // from segment to segment
   if (wave == 0) {
     const int K = all.c;
-    bool good = K <= kPredMaxCross;
     const int jl = min(lane, kPredMaxCross);
-    const int te = s_tot[2 * jl], to = s_tot[2 * jl + 1], ce = s_ce[jl];
-    const float ct = s_ct[jl];
-    float val = sH;
-    int E = binade_fast(sH);
-    for (int j = 0; good && j <= K; j++) {
-      if (j > 0) {
-        val = val + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct), j));
-        E = __builtin_amdgcn_readlane(ce, j);
-        good = val <= 3.4028234663852886e38f;
-      }
-      if (E == kPredAmb) continue;  // an ambiguous crossing: its segment is empty
-      int e;
-      int32_t m;
-      decompose(val, &e, &m);
-      const int32_t me = apply(Pair{__builtin_amdgcn_readlane(te, j), __builtin_amdgcn_readlane(to, j)}, m);
-      good = good && e == E && me < (1 << 24);
-      val = static_cast<float>(me) * ldexpf(1.0f, E - 23);
-    }
+    bool good;
+    const float val = walk_segments(sH, K, s_tot[2 * jl], s_tot[2 * jl + 1], s_ct[jl], s_ce[jl], &good);
     if (lane == 0) {
       s_res = val;
       s_ok = good;
@@ -730,13 +745,20 @@ __device__ __forceinline__ float lanes_seq_sum(const float (&t)[TPL], int n, int
   // the head: term(0 .. min(n, 32)) left to right, read from lanes 0..kHeadLanes-1
   if (wave == 0) {
     float h = -0.0f;
+    if (n >= kPredHead) {  // (uniform) every head term is live: no select between the adds
 #pragma unroll
-    for (int j = 0; j < kHeadLanes; j++)
+      for (int j = 0; j < kHeadLanes; j++)
 #pragma unroll
-      for (int k = 0; k < TPL; k++) {
-        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[k]), j));
-        if (TPL * j + k < n) h += v;
-      }
+        for (int k = 0; k < TPL; k++) h += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[k]), j));
+    } else {
+#pragma unroll
+      for (int j = 0; j < kHeadLanes; j++)
+#pragma unroll
+        for (int k = 0; k < TPL; k++) {
+          const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[k]), j));
+          if (TPL * j + k < n) h += v;
+        }
+    }
     if (lane == 0) s_head = h;
   }
   const int nv = r < kHeadLanes ? 0 : max(0, min(TPL, n - TPL * r));
@@ -858,26 +880,9 @@ __device__ __forceinline__ float lanes_seq_sum(const float (&t)[TPL], int n, int
     // the walk (group_seq_sum_pred's): wave 0 holds segment j in lane j
     if (wave == 0) {
       const int K = all.c;
-      bool good = K <= kPredMaxCross;
       const int jl = min(lane, kPredMaxCross);
-      const int te = s_tot[2 * jl], to = s_tot[2 * jl + 1], ce = s_ce[jl];
-      const float ct = s_ct[jl];
-      float val = sH;
-      int E = binade_fast(sH);
-      for (int j = 0; good && j <= K; j++) {
-        if (j > 0) {
-          val = val + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ct), j));
-          E = __builtin_amdgcn_readlane(ce, j);
-          good = val <= 3.4028234663852886e38f;
-        }
-        if (E == kPredAmb) continue;  // an ambiguous crossing: its segment is empty
-        int e;
-        int32_t m;
-        decompose(val, &e, &m);
-        const int32_t me = apply(Pair{__builtin_amdgcn_readlane(te, j), __builtin_amdgcn_readlane(to, j)}, m);
-        good = good && e == E && me < (1 << 24);
-        val = static_cast<float>(me) * ldexpf(1.0f, E - 23);
-      }
+      bool good;
+      const float val = walk_segments(sH, K, s_tot[2 * jl], s_tot[2 * jl + 1], s_ct[jl], s_ce[jl], &good);
       if (lane == 0) {
         s_res = val;
         s_ok = good;
