@@ -481,6 +481,67 @@ def decode_trace_summary(db, bench_json, command):
     print("\n".join(out))
 
 
+def traffic_summary(fetch_db, write_db, commands):
+    """HBM bytes per decode-GEMV launch of the 7B-shape bench, by projection,
+    from two rocprofv3 --pmc runs of `bench.py --copy-calibration` (FETCH_SIZE,
+    then WRITE_SIZE; KiB per dispatch), each scaled by what the same counter
+    reads for the bench's 512 MiB device-to-device calibration copy. Prints the
+    JSON that bench.py reads for its roofline's `traffic`."""
+    from collections import defaultdict
+
+    def load(f):
+        return sqlite3.connect(f).execute(
+            "select dispatch_id, kernel_name, grid_size, value from counters_collection").fetchall()
+
+    F, Wr = load(fetch_db), load(write_db)
+    nb = 512 << 20
+    ffac = max(v for _, n, _, v in F if "copyBuffer" in n) * 1024 / nb
+    wfac = max(v for _, n, _, v in Wr if "copyBuffer" in n) * 1024 / nb
+    q4 = lambda r, c: r * c // 32 * 18
+    fam = {("false, false, 1024, true, false>", 192 * 1024): ("Q|K|V + attention rmsnorm", q4(6144, 4096)),
+           ("4, false, false, 256, false, false>", 512 * 256): ("wo", q4(4096, 4096)),
+           ("true, true, 1024, true, true>", 225 * 1024): ("gate|up + SiLU + FFN rmsnorm", 2 * q4(14336, 4096)),
+           ("7, false, false, 256, false, false>", 1024 * 256): ("down", q4(4096, 14336)),
+           ("4, false, false, 256, false, false>", 4000 * 256): ("LM head", q4(32000, 4096))}
+
+    def classify(name, gs):
+        if "gemv_tile_kernel<3" not in name:
+            return None
+        for (sig, g), v in fam.items():
+            if sig in name and gs == g:
+                return v
+        return None
+
+    agg = defaultdict(lambda: [0, 0.0, 0.0])
+    for rows, idx, fac in ((F, 1, ffac), (Wr, 2, wfac)):
+        for _, name, gs, v in rows:
+            c = classify(name, gs)
+            if c is None:
+                continue
+            a = agg[c[0]]
+            if idx == 1:
+                a[0] += 1
+            a[idx] += v * 1024 / fac
+    out = {"workload": "7B-shape Q4_0 decode (bench.py): the decode weight GEMV launches (gemv_tile_kernel "
+                       "instances), split by projection; the Q|K|V and gate|up launches also compute their input's "
+                       "rmsnorm (the gate|up launch in its leading norm workgroup)",
+           "hbm_bytes_per_launch": {}, "per_projection": {}}
+    for _, (label, alg) in fam.items():
+        a = agg.get(label)
+        if not a or a[0] == 0:
+            continue
+        fetch, write = a[1] / a[0], a[2] / a[0]
+        out["hbm_bytes_per_launch"][label] = round(fetch + write)
+        out["per_projection"][label] = {"dispatches": a[0], "algorithmic_bytes": alg, "fetch_bytes": round(fetch),
+                                        "write_bytes": round(write), "fetch_vs_algorithmic": round(fetch / alg, 4)}
+    out["scaling"] = {"method": "FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by what the same counters read "
+                                "for a 512 MiB device-to-device copy (bench.py --copy-calibration, kernel "
+                                "__amd_rocclr_copyBuffer)",
+                      "fetch_counter_per_true_byte": round(ffac, 4), "write_counter_per_true_byte": round(wfac, 4)}
+    out["commands"] = commands
+    print(json.dumps(out, indent=1))
+
+
 def round_trace_summary(db):
     """Per-kernel table of the last timed call in a kernel trace of --spec:
     every kernel after the call's prefill (the last prefill-GEMM or prefill
@@ -521,6 +582,9 @@ def main():
     ap.add_argument("--round-trace", metavar="DB", help="per-kernel table of a kernel trace of --spec or --c2-decode")
     ap.add_argument("--decode-trace", nargs=3, metavar=("DB", "BENCH_JSON", "COMMAND"),
                     help="summary of a kernel trace of bench.py (with the bench's JSON line and the trace command)")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="HBM traffic JSON of two --pmc runs (FETCH_SIZE, WRITE_SIZE) of bench.py --copy-calibration")
+    ap.add_argument("--traffic-commands", nargs="*", default=[], help="the commands recorded in the --traffic JSON")
     ap.add_argument("--manifest", default=os.path.join(os.getcwd(), "microbench_cases.json"))
     args = ap.parse_args()
     if args.models:
@@ -533,6 +597,8 @@ def main():
         round_trace_summary(args.round_trace)
     elif args.decode_trace:
         decode_trace_summary(*args.decode_trace)
+    elif args.traffic:
+        traffic_summary(*args.traffic, args.traffic_commands)
     elif args.counters:
         summarize_counters(args.counters)
     elif args.attn_counters:
