@@ -23,6 +23,10 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
+# Matrix-core results in ordinary VGPRs: the batched GEMMs read every result
+# lane in their f32 epilogue, and with accumulation registers each of those
+# reads costs a v_accvgpr_read (16 of ~93 VALU instructions per block).
+PER_SOURCE = {"gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def hipcc():
@@ -35,7 +39,7 @@ def hipcc():
 def _compile(src):
     obj = os.path.join(OUT, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [hipcc()] + COMMON + lang + ["-c", src, "-o", obj]
+    cmd = [hipcc()] + COMMON + PER_SOURCE.get(os.path.basename(src), []) + lang + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -1824,19 +1824,23 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(DevMat m, const float* __
 
 // ===================================================================
 // Batched matmul on the int8 matrix cores (prefill / verify, N > 16 tokens).
+// Q4_0 needs no activation sums here: its nibbles enter the matrix cores as
+// the signed values n - 8.
 //
-// One v_mfma_i32_32x32x16_i8 pair gives the exact i32 block dots of one
+// One v_mfma_i32_32x32x32_i8 gives the exact i32 block dots of one
 // 32-element block for a 32-token x 32-row tile; the f32 term of each
 // (token, row) is then formed with the decode kernels' expression and added
 // to that output's accumulator, block after block, so every output is the
 // same left-to-right fold as in the decode path (bitwise equal per element,
 // as matmul_q8_prefill / matmul_kquant_prefill are to their decode forms).
-// Lane layout (checked on the device): A[i][k] i = lane%32, k = 8*(lane/32)
-// + byte; B[k][j] j = lane%32; D[i][j] j = lane%32, i = 8*(v/4) +
-// 4*(lane/32) + v%4 for the 16 values v of a lane.
+// Lane layout (checked on the device): A[i][k] i = lane%32, B[k][j]
+// j = lane%32, with the same k for byte b of an A lane and of a B lane in
+// the same lane half; D[i][j] j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4
+// for the 16 values v of a lane.
 // A = activations (i = token), B = weights (j = row): each lane owns one
 // weight row and sixteen tokens of its wave's tile.
 typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));  // also the skinny kernels' result type
 
 constexpr int kMmaRows = 128;  // weight rows per workgroup (32 per wave)
 constexpr int kMmaToks = 32;   // tokens per workgroup
@@ -1856,17 +1860,16 @@ struct MmaLayout {
   static constexpr int WSTR = CB * QB + 8;             // bytes per staged weight row
   static constexpr int ASTR = CB * 32 + 8;             // bytes per staged activation row
   static constexpr int DSTR = CB + 1;                  // words per staged weight-scale row
-  // one buffer: W [kMmaRows][WSTR] | A [kMmaToks][ASTR] | D [kMmaRows][DSTR] | SA, SM [CB][kMmaToks]
+  // one buffer: W [kMmaRows][WSTR] | A [kMmaToks][ASTR] | D [kMmaRows][DSTR] | SA [CB][kMmaToks]
   static constexpr int A_OFF = kMmaRows * WSTR;
   static constexpr int D_OFF = A_OFF + kMmaToks * ASTR;
   static constexpr int SA_OFF = D_OFF + kMmaRows * DSTR * 4;
-  static constexpr int SM_OFF = SA_OFF + CB * kMmaToks * 4;
-  static constexpr int BYTES = SM_OFF + CB * kMmaToks * 4;
+  static constexpr int BYTES = SA_OFF + CB * kMmaToks * 4;
   // 16-byte pieces per chunk and per lane (256 lanes)
   static constexpr int WPR = CB * QB / 16;  // pieces per weight row
   static constexpr int WP = kMmaRows * WPR, AP = kMmaToks * CB * 2;
   static constexpr int WPL = WP / 256, APL = AP / 256;
-  static constexpr int SP = kMmaToks * CB;  // activation scales (and sums) per chunk
+  static constexpr int SP = kMmaToks * CB;  // activation scales per chunk
   static constexpr int DPL = kMmaRows * CB / 256, SPL = (SP + 255) / 256;
   static_assert(WP % 256 == 0 && AP % 256 == 0 && DPL * 256 == kMmaRows * CB, "whole pieces per lane");
 };
@@ -1877,13 +1880,11 @@ struct MmaRegs {
   sk_i4 w[L::WPL], a[L::APL];
   uint32_t d[L::DPL];
   float sa[L::SPL];
-  int sm[L::SPL];
 };
 
 template <int KIND>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* __restrict__ q,
-                                                        const float* __restrict__ sa, const int* __restrict__ sums,
-                                                        int n_tok, GemvOut o) {
+                                                        const float* __restrict__ sa, int n_tok, GemvOut o) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
   using L = MmaLayout<KIND>;
   extern __shared__ int4 mma_smem[];
@@ -1925,7 +1926,6 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
       const int p = min(tid + 256 * i, L::SP - 1);  // consecutive lanes: consecutive blocks of one token
       const size_t gi = (size_t)min(m0 + p / L::CB, n_tok - 1) * G + min(cb0 + p % L::CB, G - 1);
       r.sa[i] = sa[gi];
-      r.sm[i] = sums[gi];
     }
     return r;
   };
@@ -1955,7 +1955,6 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
       const int p = tid + 256 * i;
       if (p < L::SP) {
         reinterpret_cast<float*>(b + L::SA_OFF)[(p % L::CB) * kMmaToks + p / L::CB] = r.sa[i];
-        reinterpret_cast<int*>(b + L::SM_OFF)[(p % L::CB) * kMmaToks + p / L::CB] = r.sm[i];
       }
     }
   };
@@ -1970,9 +1969,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
     const uint32_t* drow = reinterpret_cast<const uint32_t*>(b + L::D_OFF) + wr_row * L::DSTR;
     const float* sab = reinterpret_cast<const float*>(b + L::SA_OFF) + 4 * h;
     const int nlive = min(L::CB, G - c * L::CB);  // uniform
-#pragma unroll
-    for (int bb = 0; bb < L::CB; bb++) {
-      if (bb >= nlive) break;  // uniform
+    // block bb's integer dots (tokens 8g + 4h + e of the tile in values v = 4g + e)
+    auto dots = [&](int bb) __attribute__((always_inline)) {
       const long a1 = *reinterpret_cast<const long*>(arow + bb * 32);
       const long a2 = *reinterpret_cast<const long*>(arow + bb * 32 + 16);
       long b1, b2;
@@ -1989,20 +1987,41 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
         b1 = *reinterpret_cast<const long*>(wrow + bb * 32);
         b2 = *reinterpret_cast<const long*>(wrow + bb * 32 + 16);
       }
+      // one 32-deep product: byte j of either operand is element 8h + j
+      // (j < 8) or 16 + 8h + (j - 8), the same pairing for A and B, so the
+      // sum over the instruction's k is the block's dot whatever order the
+      // matrix core gives k
+      const v4i_t av = {static_cast<int>(a1), static_cast<int>(a1 >> 32), static_cast<int>(a2),
+                        static_cast<int>(a2 >> 32)};
+      const v4i_t bv = {static_cast<int>(b1), static_cast<int>(b1 >> 32), static_cast<int>(b2),
+                        static_cast<int>(b2 >> 32)};
+      const v16i_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+      return __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+    };
+    // block bb's f32 terms, added to each output's running total
+    auto terms = [&](const v16i_t& cc, int bb) __attribute__((always_inline)) {
       const float d = KIND == kKindQ8F ? __uint_as_float(drow[bb]) : f16_operand(static_cast<uint16_t>(drow[bb]));
-      v16i_t cc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-      cc = __builtin_amdgcn_mfma_i32_32x32x16_i8(a1, b1, cc, 0, 0, 0);
-      cc = __builtin_amdgcn_mfma_i32_32x32x16_i8(a2, b2, cc, 0, 0, 0);
 #pragma unroll
-      for (int g = 0; g < 4; g++) {  // tokens 8g + 4h + e of the tile hold values v = 4g + e
+      for (int g = 0; g < 4; g++) {
         const float4 s4 = *reinterpret_cast<const float4*>(sab + bb * kMmaToks + 8 * g);
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int isum = cc[4 * g + e];  // Q4_0: already less 8*sum_a (signed weights)
-          acc[4 * g + e] += d * sv[e] * static_cast<float>(isum);  // (d*sa)*float(isum), as the decode terms
-        }
+        for (int e = 0; e < 4; e++)  // (d*sa)*float(isum), as the decode terms
+          acc[4 * g + e] += d * sv[e] * static_cast<float>(cc[4 * g + e]);
       }
+    };
+    if (nlive == L::CB) {  // uniform: a whole chunk, each block's dots issued one block ahead of its terms
+      static_assert(L::CB % 2 == 0, "blocks in pairs");
+      v16i_t c0 = dots(0), c1;
+#pragma unroll
+      for (int bb = 0; bb < L::CB; bb += 2) {
+        c1 = dots(bb + 1);
+        terms(c0, bb);
+        if (bb + 2 < L::CB) c0 = dots(bb + 2);
+        terms(c1, bb + 1);
+      }
+    } else {
+      for (int bb = 0; bb < nlive; bb++) terms(dots(bb), bb);  // the row's last, partial chunk
     }
   };
 
@@ -2034,8 +2053,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
 }
 
 template <int KIND>
-int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
-                     const GemvOut& o, hipStream_t s) {
+int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, size_t n_tok, const GemvOut& o,
+                     hipStream_t s) {
   PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30), "gemm: shape out of range");
   using L = MmaLayout<KIND>;
   static const bool attr_ok = [] {
@@ -2044,7 +2063,7 @@ int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const in
   }();
   PRANA_CHECK(attr_ok, "gemm: LDS size not granted");
   dim3 grid((m.rows + kMmaRows - 1) / kMmaRows, (n_tok + kMmaToks - 1) / kMmaToks);
-  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, m, q, sa, sums, (int)n_tok, o);
+  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, m, q, sa, (int)n_tok, o);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -2060,7 +2079,6 @@ int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, const in
 // while chunk c is multiplied, so two chunks of loads are in flight behind
 // the one being used. Every output folds its block terms (d*sa)*float(isum)
 // in block order, as the decode kernels do.
-typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int kSkCB = 8;  // blocks per staged chunk
 
 template <int KIND, int RW, int TT>
@@ -2979,9 +2997,9 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
       PRANA_LAUNCH_CHECK();
       return kOk;
     }
-    case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
-    case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
+    case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(m, q, sa, n_tok, o, s);
+    case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(m, q, sa, n_tok, o, s);
+    case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(m, q, sa, n_tok, o, s);
     case kKindQ4_K: return launch_gemm_kq<kKindQ4_K>(m, q, sa, sums, n_tok, o, s);
     case kKindQ6_K: return launch_gemm_kq<kKindQ6_K>(m, q, sa, sums, n_tok, o, s);
   }
