@@ -1882,17 +1882,32 @@ struct MmaRegs {
   float sa[L::SPL];
 };
 
+// Up to three matrices of one kind and width over the same activations
+// (Q|K|V, gate|up) in one launch: x-blocks [t0[i], t0[i+1]) are matrix i's
+// row tiles, so a small matrix (a GQA K or V) does not leave most of the
+// chip idle in a launch of its own.
+struct MmaJob {
+  DevMat m[3];
+  GemvOut o[3];
+  int t0[3];  // first x-block of each matrix (t0[0] = 0)
+  int n_mats;
+};
+
 template <int KIND>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* __restrict__ q,
-                                                        const float* __restrict__ sa, int n_tok, GemvOut o) {
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ sa, int n_tok) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
   using L = MmaLayout<KIND>;
   extern __shared__ int4 mma_smem[];
   uint8_t* lds = reinterpret_cast<uint8_t*>(mma_smem);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+  const int bx = blockIdx.x;
+  const int mi = job.n_mats > 2 && bx >= job.t0[2] ? 2 : job.n_mats > 1 && bx >= job.t0[1] ? 1 : 0;  // uniform
+  const DevMat m = mi == 0 ? job.m[0] : mi == 1 ? job.m[1] : job.m[2];
+  const GemvOut o = mi == 0 ? job.o[0] : mi == 1 ? job.o[1] : job.o[2];
   const int K = static_cast<int>(m.cols), G = K / 32;
   const int R = static_cast<int>(m.rows);
-  const int row0 = blockIdx.x * kMmaRows;
+  const int row0 = (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * kMmaRows;
   const int m0 = blockIdx.y * kMmaToks;
   const int n_chunks = (G + L::CB - 1) / L::CB;
 
@@ -2053,17 +2068,30 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(DevMat m, const int8_t* 
 }
 
 template <int KIND>
-int launch_gemm_mfma(const DevMat& m, const int8_t* q, const float* sa, size_t n_tok, const GemvOut& o,
+int launch_gemm_mfma(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa, size_t n_tok,
                      hipStream_t s) {
-  PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30), "gemm: shape out of range");
+  PRANA_CHECK(n_mats >= 1 && n_mats <= 3, "gemm: 1..3 matrices");
   using L = MmaLayout<KIND>;
   static const bool attr_ok = [] {
     return L::BYTES * 2 <= 65536 ||
            set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_mfma_kernel<KIND>), L::BYTES * 2);
   }();
   PRANA_CHECK(attr_ok, "gemm: LDS size not granted");
-  dim3 grid((m.rows + kMmaRows - 1) / kMmaRows, (n_tok + kMmaToks - 1) / kMmaToks);
-  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, m, q, sa, (int)n_tok, o);
+  MmaJob job{};
+  size_t tiles = 0;
+  for (int i = 0; i < n_mats; i++) {
+    const DevMat& m = ms[i];
+    PRANA_CHECK(m.kind == KIND && m.cols == ms[0].cols, "gemm: matrices must share kind and cols");
+    PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30), "gemm: shape out of range");
+    job.m[i] = m;
+    job.o[i] = os[i];
+    job.t0[i] = static_cast<int>(tiles);
+    tiles += (m.rows + kMmaRows - 1) / kMmaRows;
+  }
+  job.n_mats = n_mats;
+  PRANA_CHECK(tiles >= 1 && tiles < (1u << 31), "gemm: row tiles out of range");
+  dim3 grid(static_cast<unsigned>(tiles), (n_tok + kMmaToks - 1) / kMmaToks);
+  hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, job, q, sa, (int)n_tok);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -2847,6 +2875,15 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
   for (int i = 1; i < n; i++) one_kind = one_kind && ms[i].kind == ms[0].kind;
   const std::pair<int, int> pair = one_kind ? std::make_pair(-1, -1) : mixed_pair(ms, n);
   PRANA_CHECK(one_kind || gemv_multi_fusable(ms, n), "gemv_multi: matrices must share a kind or form a fusable pair");
+  const int k0 = ms[0].kind;
+  if (one_kind && n > 1 && (k0 == kKindQ8F || k0 == kKindQ8_0 || k0 == kKindQ4_0) && n_tok > kDecodeMaxTokens &&
+      !gemv_skinny(k0, n_tok)) {  // one matrix-core launch over all the matrices' row tiles
+    switch (k0) {
+      case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(ms, os, n, q, sa, n_tok, s);
+      case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(ms, os, n, q, sa, n_tok, s);
+      default: return launch_gemm_mfma<kKindQ4_0>(ms, os, n, q, sa, n_tok, s);
+    }
+  }
   if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
@@ -2997,9 +3034,9 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
       PRANA_LAUNCH_CHECK();
       return kOk;
     }
-    case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(m, q, sa, n_tok, o, s);
-    case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(m, q, sa, n_tok, o, s);
-    case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(m, q, sa, n_tok, o, s);
+    case kKindQ8F: return launch_gemm_mfma<kKindQ8F>(&m, &o, 1, q, sa, n_tok, s);
+    case kKindQ8_0: return launch_gemm_mfma<kKindQ8_0>(&m, &o, 1, q, sa, n_tok, s);
+    case kKindQ4_0: return launch_gemm_mfma<kKindQ4_0>(&m, &o, 1, q, sa, n_tok, s);
     case kKindQ4_K: return launch_gemm_kq<kKindQ4_K>(m, q, sa, sums, n_tok, o, s);
     case kKindQ6_K: return launch_gemm_kq<kKindQ6_K>(m, q, sa, sums, n_tok, o, s);
   }
