@@ -44,14 +44,14 @@ struct Elem<false> {
 // the row is fetched with 16-byte loads before the chain; HD == 0: runtime
 // width, scalar loads.
 template <int HD, bool F16>
-__device__ __forceinline__ float row_dot(const float* s_q, const typename Elem<F16>::T* krow, int hd) {
+__device__ __forceinline__ float row_dot(const float* s_q, const typename Elem<F16>::T* krow, int hd, int ps = 1) {
   float dot = -0.0f;
   if constexpr (HD > 0 && F16) {
     static_assert(HD % 8 == 0, "f16 rows load 8 halves at a time");
     uint4 raw[HD / 8];
     const uint4* p = reinterpret_cast<const uint4*>(krow);
 #pragma unroll
-    for (int i = 0; i < HD / 8; i++) raw[i] = p[i];
+    for (int i = 0; i < HD / 8; i++) raw[i] = p[(size_t)i * ps];  // piece i: ps 16-byte words on
 #pragma unroll
     for (int i = 0; i < HD / 8; i++) {
       const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
@@ -86,10 +86,11 @@ __device__ __forceinline__ float row_dot(const float* s_q, const typename Elem<F
 
 struct HeadJob {
   const float* q_row;  // this query row (n_heads*hd)
-  const void* k;       // K rows (kv_stride elements apart)
+  const void* k;       // K rows (kv_stride elements apart), or pieces (kcache_index, kcap > 0)
   const void* v;
   int pos;  // absolute position: attends to rows 0..=pos
   int h, kvh, kv_stride, hd;
+  int kcap;
   int d0, dw;        // dims folded by this workgroup
   float* dst;        // output row (n_heads*hd)
   float* gscores;    // global scratch of >= pos+1 floats (used beyond kScoreLds)
@@ -166,15 +167,15 @@ __device__ __forceinline__ void make_products(const VPieces& v, const float* sc,
 // second chain fills the first's dependent-add latency.
 template <int HD>
 __device__ __forceinline__ void row_dot2_f16(const float* s_q, const uint16_t* ka, const uint16_t* kb, float* da,
-                                             float* db) {
+                                             float* db, int ps) {
   static_assert(HD % 8 == 0, "f16 rows load 8 halves at a time");
   uint4 ra[HD / 8], rb[HD / 8];
   const uint4* pa = reinterpret_cast<const uint4*>(ka);
   const uint4* pb = reinterpret_cast<const uint4*>(kb);
 #pragma unroll
-  for (int i = 0; i < HD / 8; i++) ra[i] = pa[i];
+  for (int i = 0; i < HD / 8; i++) ra[i] = pa[(size_t)i * ps];  // piece i: ps 16-byte words on
 #pragma unroll
-  for (int i = 0; i < HD / 8; i++) rb[i] = pb[i];
+  for (int i = 0; i < HD / 8; i++) rb[i] = pb[(size_t)i * ps];
   float a = -0.0f, b = -0.0f;
 #pragma unroll
   for (int i = 0; i < HD / 8; i++) {
@@ -202,13 +203,17 @@ __device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, flo
   const int n = J.pos + 1;
   const int hd = HD > 0 ? HD : J.hd;
   const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-  const T* kb = static_cast<const T*>(J.k) + (size_t)J.kvh * hd;
   float mx = -INFINITY;
   if constexpr (HD > 0 && F16) {
+    // row t at kb + t * rs, its 8-dim pieces ps 16-byte words apart
+    const bool pcs = J.kcap > 0;
+    const T* kb = static_cast<const T*>(J.k) + (size_t)J.kvh * hd * (pcs ? J.kcap : 1);
+    const size_t rs = pcs ? 8 : J.kv_stride;
+    const int ps = pcs ? J.kcap : 1;
     for (int t = tid; t < n; t += 2 * kNT) {
       const int t2 = t + kNT;
       float da, db;
-      row_dot2_f16<HD>(L.q, kb + (size_t)t * J.kv_stride, kb + (size_t)min(t2, n - 1) * J.kv_stride, &da, &db);
+      row_dot2_f16<HD>(L.q, kb + (size_t)t * rs, kb + (size_t)min(t2, n - 1) * rs, &da, &db, ps);
       const float s = da * scale;
       sc[t] = s;
       mx = fmaxf(mx, s);
@@ -220,6 +225,7 @@ __device__ __forceinline__ float head_scores(const HeadJob& J, const Lds& L, flo
     }
     return mx;
   }
+  const T* kb = static_cast<const T*>(J.k) + (size_t)J.kvh * hd;  // rows (kcap == 0 here)
   for (int t = tid; t < n; t += kNT) {
     float s = row_dot<HD, F16>(L.q, kb + (size_t)t * J.kv_stride, hd) * scale;
     sc[t] = s;
@@ -366,7 +372,7 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __r
                                                                 const uint16_t* __restrict__ k, int pos0,
                                                                 const int* __restrict__ pos_dev, int n_heads,
                                                                 int group, int n_kv, float* __restrict__ sc,
-                                                                int sc_stride) {
+                                                                int sc_stride, int kcap) {
   __shared__ __align__(16) float s_q[4 * HD];
   const int nhb = (group + 3) / 4;
   const int hb = blockIdx.y % nhb, ik = blockIdx.y / nhb;
@@ -382,10 +388,12 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores(const float* __r
   const int t = row0 + threadIdx.x;
   if (t >= n) return;
   const int kv_stride = n_kv * HD;
-  const uint4* kp = reinterpret_cast<const uint4*>(k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  const uint4* kp = reinterpret_cast<const uint4*>(
+      kcap ? k + (size_t)kvh * HD * kcap + (size_t)t * 8 : k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  const int ps = kcap ? kcap : 1;  // 16-byte words between a row's 8-dim pieces
   uint4 raw[HD / 8];
 #pragma unroll
-  for (int e = 0; e < HD / 8; e++) raw[e] = kp[e];
+  for (int e = 0; e < HD / 8; e++) raw[e] = kp[(size_t)e * ps];
   const float4* qv = reinterpret_cast<const float4*>(s_q);
   float dot[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
   // q of step e+1 is read while step e computes. The empty asm after each
@@ -440,7 +448,8 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores_rows(const float
                                                                      const uint16_t* __restrict__ k, int pos0,
                                                                      const int* __restrict__ pos_dev, int n_q,
                                                                      int n_heads, int group, int n_kv,
-                                                                     float* __restrict__ sc, int sc_stride) {
+                                                                     float* __restrict__ sc, int sc_stride,
+                                                                     int kcap) {
   constexpr int QR = 2;
   __shared__ __align__(16) float s_q[QR][4 * HD];
   const int nhb = (group + 3) / 4;
@@ -462,10 +471,12 @@ __global__ __launch_bounds__(kSplitRows) void attn_split_scores_rows(const float
   const int t = row0 + threadIdx.x;
   if (t >= n_max) return;
   const int kv_stride = n_kv * HD;
-  const uint4* kp = reinterpret_cast<const uint4*>(k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  const uint4* kp = reinterpret_cast<const uint4*>(
+      kcap ? k + (size_t)kvh * HD * kcap + (size_t)t * 8 : k + (size_t)t * kv_stride + (size_t)kvh * HD);
+  const int ps = kcap ? kcap : 1;  // 16-byte words between a row's 8-dim pieces
   uint4 raw[HD / 8];
 #pragma unroll
-  for (int e = 0; e < HD / 8; e++) raw[e] = kp[e];
+  for (int e = 0; e < HD / 8; e++) raw[e] = kp[(size_t)e * ps];
   float dot[QR][4];
 #pragma unroll
   for (int r = 0; r < QR; r++)
@@ -890,7 +901,7 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
                                                             const uint16_t* __restrict__ v, int pos0, int n_heads,
                                                             int group, float* __restrict__ out,
                                                             int8_t* __restrict__ qd, float* __restrict__ qsa,
-                                                            int* __restrict__ qsum) {
+                                                            int* __restrict__ qsum, int kcap) {
   using C = WideCfg<HD>;
   __shared__ __align__(16) float s_q[HD];
   __shared__ float s_red[kWideNT / 64];
@@ -904,16 +915,19 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   __syncthreads();
   // ---- scores (attention.rs:165-185): (fold_d q[d]*k_t[d] from -0.0) * (1/sqrt(hd))
   const float scale = 1.0f / sqrtf(static_cast<float>(HD));
-  const uint16_t* kb = k + (size_t)kvh * HD;
+  // row t at kb + t * rs, its 8-dim pieces ps 16-byte words apart
+  const uint16_t* kb = k + (size_t)kvh * HD * (kcap ? kcap : 1);
+  const size_t rs = kcap ? 8 : kv_stride;
+  const int ps = kcap ? kcap : 1;
   const int t1 = tid, t2 = tid + kWideNT;
   float mx = -INFINITY;
   if (t1 < n) {
-    const float s1 = row_dot<HD, true>(s_q, kb + (size_t)t1 * kv_stride, HD) * scale;
+    const float s1 = row_dot<HD, true>(s_q, kb + (size_t)t1 * rs, HD, ps) * scale;
     s_p[exact::run_pad(t1)] = s1;
     mx = s1;
   }
   if (t2 < n) {
-    const float s2 = row_dot<HD, true>(s_q, kb + (size_t)t2 * kv_stride, HD) * scale;
+    const float s2 = row_dot<HD, true>(s_q, kb + (size_t)t2 * rs, HD, ps) * scale;
     s_p[exact::run_pad(t2)] = s2;
     mx = fmaxf(mx, s2);
   }
@@ -1019,12 +1033,12 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
 
 template <int HD>
 int launch_wide(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, size_t n_q, size_t n_heads,
-                size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, hipStream_t s) {
+                size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, size_t kcap, hipStream_t s) {
   const bool fuse_q = aq && aq->q;  // whole heads are whole 32-blocks
   if (quantized) *quantized = fuse_q;
   hipLaunchKernelGGL(attn_wide_kernel<HD>, dim3(n_heads, n_q), dim3(kWideNT), 0, s, q, k, v, (int)pos0,
                      (int)n_heads, (int)(n_heads / n_kv_heads), out, fuse_q ? aq->q : nullptr,
-                     fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
+                     fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr, (int)kcap);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -1238,7 +1252,7 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
                                                    const int* __restrict__ pos_dev, int n_heads, int group, int hd,
                                                    int dsplit, float* __restrict__ out, float* __restrict__ scratch,
                                                    int scratch_stride, int mode, int8_t* __restrict__ qd,
-                                                   float* __restrict__ qsa, int* __restrict__ qsum) {
+                                                   float* __restrict__ qsa, int* __restrict__ qsum, int kcap) {
   __shared__ float s_q[256];
   __shared__ float s_red[kNT / 64];
   __shared__ __align__(16) float s_scores[exact::lane_pad(kScoreLds)];
@@ -1254,6 +1268,7 @@ __global__ __launch_bounds__(kNT) void attn_kernel(const float* __restrict__ q, 
   J.h = h;
   J.kvh = h / group;
   J.kv_stride = (n_heads / group) * hd;
+  J.kcap = kcap;
   J.hd = hd;
   J.dw = hd / dsplit;
   J.d0 = ds * J.dw;
@@ -1283,7 +1298,7 @@ size_t max_dyn_lds() {
 template <int HD>
 int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t pos0, const int* pos_dev, size_t n_q,
                  size_t n_heads, size_t n_kv_heads, float* out, float* scratch, size_t ctx_cap, const ActQuant* aq,
-                 bool* quantized, hipStream_t s) {
+                 bool* quantized, size_t kcap, hipStream_t s) {
   const int group = static_cast<int>(n_heads / n_kv_heads);
   const int stride = static_cast<int>(split_stride(ctx_cap));
   // a position read from device memory can be anything up to the capacity:
@@ -1294,12 +1309,12 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
     hipLaunchKernelGGL(attn_split_scores_rows<HD>,
                        dim3((rows + kSplitRows - 1) / kSplitRows, (n_q + 1) / 2 * n_kv_heads * ((group + 3) / 4)),
                        dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_q, (int)n_heads, group,
-                       (int)n_kv_heads, scratch, stride);
+                       (int)n_kv_heads, scratch, stride, (int)kcap);
   else
     hipLaunchKernelGGL(attn_split_scores<HD>,
                        dim3((rows + kSplitRows - 1) / kSplitRows, n_q * n_kv_heads * ((group + 3) / 4)),
                        dim3(kSplitRows), 0, s, q, k, (int)pos0, pos_dev, (int)n_heads, group,
-                       (int)n_kv_heads, scratch, stride);
+                       (int)n_kv_heads, scratch, stride, (int)kcap);
   PRANA_LAUNCH_CHECK();
   // the softmax stages the longest row's exponentials in LDS when they fit
   const size_t lds = (exact::run_pad(static_cast<int>(rows) - 1) + 1) * sizeof(float);
@@ -1346,25 +1361,29 @@ int launch_split(const float* q, const uint16_t* k, const uint16_t* v, size_t po
 template <bool F16>
 int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const int* pos_dev, size_t n_q,
                 size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
-                const ActQuant* aq, bool* quantized, hipStream_t s) {
+                const ActQuant* aq, bool* quantized, size_t kcap, hipStream_t s) {
   const size_t elem = F16 ? 2 : 4;
   const bool aligned = reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                        (hd * elem) % 16 == 0;
+  // a piecewise K cache: every path below reads it through a compiled head width
+  PRANA_CHECK(kcap == 0 || (F16 && aligned && (hd == 64 || hd == 128) && kcap >= pos0 + n_q &&
+                            kcap <= static_cast<size_t>(INT32_MAX / 8)),
+              "attention: a piecewise K cache needs aligned f16 rows of 64 or 128 dims");
   if (F16 && aligned && !pos_dev && n_q >= 2 && pos0 + n_q >= kWideMinRows && pos0 + n_q <= (size_t)kWideMax &&
       (hd == 64 || hd == 128)) {
     const uint16_t* kc = static_cast<const uint16_t*>(k);
     const uint16_t* vc = static_cast<const uint16_t*>(v);
-    return hd == 64 ? launch_wide<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s)
-                    : launch_wide<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, s);
+    return hd == 64 ? launch_wide<64>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, kcap, s)
+                    : launch_wide<128>(q, kc, vc, pos0, n_q, n_heads, n_kv_heads, out, aq, quantized, kcap, s);
   }
   // with pos_dev, pos0 still picks the path (the kernels read the position)
   if (F16 && aligned && scratch && pos0 + n_q >= kSplitMinRows && (hd == 64 || hd == 128)) {
     const uint16_t* kc = static_cast<const uint16_t*>(k);
     const uint16_t* vc = static_cast<const uint16_t*>(v);
     return hd == 64 ? launch_split<64>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap,
-                                       aq, quantized, s)
+                                       aq, quantized, kcap, s)
                     : launch_split<128>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, out, scratch, ctx_cap,
-                                        aq, quantized, s);
+                                        aq, quantized, kcap, s);
   }
   int mode = 0;
   if (aligned) {
@@ -1379,7 +1398,7 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
   if (quantized) *quantized = fuse_q;
   hipLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, q, k, v, (int)pos0, pos_dev,
                      (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode,
-                     fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr);
+                     fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr, (int)kcap);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -1411,14 +1430,14 @@ size_t attention_scratch_floats(size_t n_q, size_t n_heads, size_t ctx_cap, bool
 
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
-                           const int* pos_dev, hipStream_t s, const ActQuant* aq, bool* quantized) {
+                           const int* pos_dev, hipStream_t s, const ActQuant* aq, bool* quantized, size_t kcap) {
   if (n_q == 0) return kOk;
   PRANA_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0, "attention: n_heads must be a multiple of n_kv_heads");
   PRANA_CHECK(hd > 0 && hd <= 256, "attention: head_dim must be in 1..=256");
   if (ctx_cap == 0) ctx_cap = pos0 + n_q;
   PRANA_CHECK(pos_dev || pos0 + n_q <= ctx_cap, "attention: scratch capacity below pos0 + n_q");
   return launch_attn<true>(q, kc, vc, pos0, pos_dev, n_q, n_heads, n_kv_heads, hd, out, scratch, ctx_cap, aq, quantized,
-                           s);
+                           kcap, s);
 }
 
 int launch_attention_prefill(const float* q, const float* k, const float* v, size_t seq, size_t n_heads,
@@ -1432,7 +1451,7 @@ int launch_attention_prefill(const float* q, const float* k, const float* v, siz
     return hd == 64 ? launch_prefill_blk<64>(q, k, v, seq, n_heads, n_kv_heads, out, aq, quantized, s)
                     : launch_prefill_blk<128>(q, k, v, seq, n_heads, n_kv_heads, out, aq, quantized, s);
   }
-  return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, aq, quantized, s);
+  return launch_attn<false>(q, k, v, 0, nullptr, seq, n_heads, n_kv_heads, hd, out, scratch, seq, aq, quantized, 0, s);
 }
 
 }  // namespace prana

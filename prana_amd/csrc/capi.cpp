@@ -558,7 +558,13 @@ int prana_cache_read(prana_cache_t c, size_t layer, int which, size_t rows, uint
     PRANA_CHECK(layer < c->c.n_layers && rows <= c->c.len, "cache_read: out of range");
     PRANA_HIP(hipStreamSynchronize(ctx().stream));
     const uint16_t* src = which ? c->c.v(layer) : c->c.k(layer);
-    PRANA_HIP(hipMemcpy(host_out, src, rows * c->c.kv_dim * 2, hipMemcpyDeviceToHost));
+    const size_t kv_dim = c->c.kv_dim, kcap = c->c.kcap;
+    if (which || kcap == 0 || rows == 0) {
+      PRANA_HIP(hipMemcpy(host_out, src, rows * kv_dim * 2, hipMemcpyDeviceToHost));
+    } else {  // K in 8-dim pieces (kcache_index): back to rows, one column of pieces at a time
+      for (size_t g = 0; g < kv_dim / 8; g++)
+        PRANA_HIP(hipMemcpy2D(host_out + g * 8, kv_dim * 2, src + g * kcap * 8, 16, 16, rows, hipMemcpyDeviceToHost));
+    }
     return static_cast<int>(kOk);
   });
 }

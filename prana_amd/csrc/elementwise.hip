@@ -329,11 +329,12 @@ int launch_kv_write(uint16_t* cache, size_t first_row, size_t kv_stride, const f
 }
 
 // Decode glue after the Q/K/V projections (infer.rs:169-178): rope q and k
-// in place at `pos`, then write k and v to the f16 cache row `pos`.
+// in place at `pos`, then write k and v to the f16 cache row `pos` (K in the
+// kcache_index layout of kcap).
 __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
                                int q_dim, int kv_dim, int hd, const float2* __restrict__ table, int neox,
-                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, const int* __restrict__ pos_dev,
-                               int pos_host) {
+                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int kcap,
+                               const int* __restrict__ pos_dev, int pos_host) {
   int pos = pos_dev ? *pos_dev : pos_host;
   int half = hd / 2;
   const float2* tab = table + (size_t)pos * half;
@@ -358,8 +359,8 @@ __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k, con
     row[i0] = a;
     row[i1] = b;
     if (gid >= qp) {
-      kc[(size_t)pos * kv_dim + i0] = f32_to_f16(a);
-      kc[(size_t)pos * kv_dim + i1] = f32_to_f16(b);
+      kc[kcache_index(pos, i0, kv_dim, kcap)] = f32_to_f16(a);
+      kc[kcache_index(pos, i1, kv_dim, kcap)] = f32_to_f16(b);
     }
   } else if (gid < qp + kp + kv_dim) {
     int i = gid - qp - kp;
@@ -372,7 +373,7 @@ __global__ void rope_kv_kernel(float* __restrict__ q, float* __restrict__ k, con
 // f16 cache rows (infer.rs:247-262, 322-338) in one launch.
 __global__ void rope_kv_rows_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
                                     int n, int q_dim, int kv_dim, int hd, const float2* __restrict__ table, int neox,
-                                    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int pos0) {
+                                    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int kcap, int pos0) {
   const int half = hd / 2;
   const int qp = q_dim / 2, kp = kv_dim / 2, per = qp + kp + kv_dim;
   const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
@@ -398,8 +399,8 @@ __global__ void rope_kv_rows_kernel(float* __restrict__ q, float* __restrict__ k
     row[i0] = a;
     row[i1] = b;
     if (e >= qp) {
-      kc[(size_t)pos * kv_dim + i0] = f32_to_f16(a);
-      kc[(size_t)pos * kv_dim + i1] = f32_to_f16(b);
+      kc[kcache_index(pos, i0, kv_dim, kcap)] = f32_to_f16(a);
+      kc[kcache_index(pos, i1, kv_dim, kcap)] = f32_to_f16(b);
     }
   } else {
     const int i = e - qp - kp;
@@ -408,20 +409,24 @@ __global__ void rope_kv_rows_kernel(float* __restrict__ q, float* __restrict__ k
 }
 
 int launch_rope_kv_rows(float* q, float* k, const float* v, size_t n, size_t q_dim, size_t kv_dim, size_t hd,
-                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t pos0, hipStream_t s) {
+                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t kcap, size_t pos0,
+                        hipStream_t s) {
   const size_t total = n * (q_dim / 2 + kv_dim / 2 + kv_dim);
   if (total == 0) return kOk;
+  PRANA_CHECK(kcap == 0 || (kv_dim % 8 == 0 && pos0 + n <= kcap), "rope_kv_rows: rows beyond the K cache");
   hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((total + 255) / 256), dim3(256), 0, s, q, k, v, (int)n, (int)q_dim,
-                     (int)kv_dim, (int)hd, table, neox, kc, vc, (int)pos0);
+                     (int)kv_dim, (int)hd, table, neox, kc, vc, (int)kcap, (int)pos0);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
 
 int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
-                   int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s) {
+                   int neox, uint16_t* kc, uint16_t* vc, size_t kcap, const int* pos_dev, size_t pos_host,
+                   hipStream_t s) {
   size_t n = q_dim / 2 + kv_dim / 2 + kv_dim;
+  PRANA_CHECK(kcap == 0 || kv_dim % 8 == 0, "rope_kv: a piecewise K cache needs kv_dim % 8 == 0");
   hipLaunchKernelGGL(rope_kv_kernel, dim3((n + 255) / 256), dim3(256), 0, s, q, k, v, (int)q_dim, (int)kv_dim,
-                     (int)hd, table, neox, kc, vc, pos_dev, (int)pos_host);
+                     (int)hd, table, neox, kc, vc, (int)kcap, pos_dev, (int)pos_host);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }

@@ -1126,7 +1126,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
         rotate(a, b, rk.table[(size_t)pos * half + m]);
         const float y = first ? a : b;
         o.out[r] = y;
-        if (mi == 1) rk.kc[crow] = f32_to_f16(y);
+        if (mi == 1) rk.kc[kcache_index(pos, r, rows_m, rk.kcap)] = f32_to_f16(y);
       }
     }
     return;

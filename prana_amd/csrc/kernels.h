@@ -19,6 +19,16 @@ namespace prana {
 // byte count per block is the GGUF one, so roofline bytes are unchanged.
 enum Kind : int { kKindF32 = 0, kKindQ8F = 1, kKindQ8_0 = 2, kKindQ4_0 = 3, kKindQ4_K = 4, kKindQ6_K = 5 };
 
+// f16 K cache layouts. kcap == 0: rows [pos][kv_dim] (the reference's, and
+// the C entry points' caller-owned caches). kcap > 0 (a model's own cache,
+// 64- or 128-wide heads): pieces of 8 consecutive dims, position-major,
+// [kv_dim/8][kcap][8], so the attention kernels' lanes (one position each)
+// read a piece of a head with one coalesced wave load. Index of element
+// (position t, kv dim d):
+__host__ __device__ inline size_t kcache_index(size_t t, size_t d, size_t kv_dim, size_t kcap) {
+  return kcap ? ((d >> 3) * kcap + t) * 8 + (d & 7) : t * kv_dim + d;
+}
+
 struct DevMat {
   int kind;
   size_t rows, cols;
@@ -42,9 +52,11 @@ int launch_kv_write(uint16_t* cache, size_t first_row, size_t kv_stride, const f
 // n token rows at positions pos0..pos0+n-1: RoPE of q and k in place, and
 // the f16 cache rows of k and v.
 int launch_rope_kv_rows(float* q, float* k, const float* v, size_t n, size_t q_dim, size_t kv_dim, size_t hd,
-                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t pos0, hipStream_t s);
+                        const float2* table, int neox, uint16_t* kc, uint16_t* vc, size_t kcap, size_t pos0,
+                        hipStream_t s);
 int launch_rope_kv(float* q, float* k, const float* v, size_t q_dim, size_t kv_dim, size_t hd, const float2* table,
-                   int neox, uint16_t* kc, uint16_t* vc, const int* pos_dev, size_t pos_host, hipStream_t s);
+                   int neox, uint16_t* kc, uint16_t* vc, size_t kcap, const int* pos_dev, size_t pos_host,
+                   hipStream_t s);
 int launch_f32_to_f16(const float* in, size_t n, uint16_t* out, hipStream_t s);
 int launch_f16_to_f32(const uint16_t* in, size_t n, float* out, hipStream_t s);
 int launch_expf(const float* in, size_t n, float* out, hipStream_t s);
@@ -135,8 +147,9 @@ struct RopeKv {
   int hd, neox;
   int pos;              // used when pos_dev is null
   const int* pos_dev;
-  uint16_t* kc;
-  uint16_t* vc;
+  uint16_t* kc;         // layout kcache_index(.., kcap)
+  uint16_t* vc;         // rows
+  int kcap;
 };
 // rmsnorm (norms.rs:9-23) folded into a one-token GEMV launch: every
 // workgroup normalises the row x with the weights w itself (the exact
@@ -200,7 +213,7 @@ struct ActQuant {
 int launch_attention_cache(const float* q, const uint16_t* kc, const uint16_t* vc, size_t pos0, size_t n_q,
                            size_t n_heads, size_t n_kv_heads, size_t hd, float* out, float* scratch, size_t ctx_cap,
                            const int* pos_dev, hipStream_t s, const ActQuant* aq = nullptr,
-                           bool* quantized = nullptr);
+                           bool* quantized = nullptr, size_t kcap = 0);
 // attention (prefill, attention.rs:236-284) over f32 K/V of the window.
 // scratch >= attention_scratch_floats(seq, n_heads, seq, false) floats.
 // Score scratch a launch needs: cache windows (cache = true) keep the scores

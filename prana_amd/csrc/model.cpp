@@ -264,6 +264,7 @@ int Cache::create(const Model& m, size_t positions) {
   len = std::min(positions, m.c.seq_len);
   kv_dim = m.c.n_kv_heads * m.c.head_dim;
   n_layers = m.c.n_layers;
+  kcap = m.c.head_dim == 64 || m.c.head_dim == 128 ? len : 0;
   size_t per = len * kv_dim * 2;
   int rc = buf.alloc(std::max<size_t>(per * 2 * n_layers, 2));
   if (rc) return rc;
@@ -575,7 +576,8 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     bool roped = false;  // the decode Q|K|V launch also did RoPE and the cache rows
     {
       const GemvOut o[3] = {oq, ok, ov};
-      const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), pos_dev, kc, vc};
+      const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), pos_dev, kc, vc,
+                      static_cast<int>(cache.kcap)};
       if ((rc = apply_multi(wqkv, o, 3, n, ws.xb.as<float>(), s, mode == 0 ? &rk : nullptr, &roped,
                             norm_fused ? &nin : nullptr)))
         return rc;
@@ -584,15 +586,15 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     bool quantized = false;
     if (mode == 0) {
       if (!roped && (rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd,
-                                         tab, c.rope_neox, kc, vc, pos_dev, pos0, s)))
+                                         tab, c.rope_neox, kc, vc, cache.kcap, pos_dev, pos0, s)))
         return rc;
       if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
                                        ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, pos_dev, s, &aq,
-                                       &quantized)))
+                                       &quantized, cache.kcap)))
         return rc;
     } else {
       if ((rc = launch_rope_kv_rows(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, q_dim, kv_dim, hd, tab,
-                                    c.rope_neox, kc, vc, pos0, s)))
+                                    c.rope_neox, kc, vc, cache.kcap, pos0, s)))
         return rc;
       if (mode == 1)
         rc = launch_attention_prefill(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, c.n_heads,
@@ -601,7 +603,7 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
       else
         rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, n, c.n_heads, c.n_kv_heads, hd,
                                     ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, nullptr, s, &aq,
-                                    &quantized);
+                                    &quantized, cache.kcap);
       if (rc) return rc;
     }
     // A q_dim that is not a whole number of 32-blocks only occurs with a dense

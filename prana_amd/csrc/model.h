@@ -26,6 +26,7 @@ struct Layer {
 // KvCache::with_len: per layer K then V, each [len][kv_dim] f16, one allocation.
 struct Cache {
   size_t len = 0, kv_dim = 0, n_layers = 0;
+  size_t kcap = 0;  // K layout (kcache_index): len for 64- or 128-wide heads (8-dim pieces), else 0 (rows)
   DevBuf buf;
   int create(const Model& m, size_t positions);
   uint16_t* k(size_t l) const;
