@@ -272,6 +272,22 @@ def test_rmsnorm_register_runs_many_rows(dim):
         assert same_bits(got[i], want[i]), i
 
 
+@pytest.mark.parametrize("dim", [2080, 3072, 4096])
+def test_rmsnorm_batches_beyond_256_rows(dim):
+    # batches of more than 256 rows of 2049..4096 values take 256-lane
+    # workgroups (sixteen squares per lane in the exact sum): typical rows and
+    # the adversarial ones (ties, powers of two, subnormal squares, overflow,
+    # NaN, inf) spread through the batch, all bit-exact
+    r = rng(dim + 11)
+    adv = _adversarial_rows(dim, dim + 3)
+    x = (r.standard_normal((300, dim)) * np.exp(r.standard_normal((300, 1)))).astype(np.float32)
+    x[::30][:adv.shape[0]] = adv[: len(x[::30])]
+    w = (1 + 0.1 * r.standard_normal(dim)).astype(np.float32)
+    got, want = P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5)
+    for i in range(x.shape[0]):
+        assert same_bits(got[i], want[i]), i
+
+
 def test_sequential_order_closed_forms_on_device():
     from tests.test_oracle import order_cases, pv_order_case
     x_rms, y0, x_sm, p0 = order_cases()
