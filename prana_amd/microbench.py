@@ -341,37 +341,45 @@ def summarize(db, manifest_path):
     print("\n".join(out))
 
 
-def summarize_counters(db, cus=256):
+def summarize_counters(db, cus=256, xcds=8):
     """Per-kernel MFMA / VALU utilisation from a rocprofv3 --pmc run with
     SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_I8
-    SQ_ACTIVE_INST_VALU SQ_BUSY_CYCLES: MfmaUtil as rocprofv3 defines it
-    (busy cycles over GRBM active cycles x SIMDs), VALU busy (quad-cycles x 4
-    over active cycles x CUs), and int8 MFMA ops (MOPS x 512) per dispatch."""
+    SQ_ACTIVE_INST_VALU SQ_BUSY_CYCLES. rocprofv3 reports GRBM_GUI_ACTIVE
+    summed over the XCDs, so a dispatch's active cycles are that sum / xcds
+    (the implied clock, cycles over the dispatch's duration, is printed as a
+    check). MfmaUtil: busy cycles over active cycles x SIMDs; VALU busy per
+    SIMD: each VALU instruction (SQ_ACTIVE_INST_VALU counts one per
+    instruction) holds its SIMD four cycles; int8 MFMA ops = MOPS x 512."""
     import collections
     import re
     c = sqlite3.connect(db)
-    rows = c.execute("select dispatch_id, kernel_name, grid_size, counter_name, value from counters_collection").fetchall()
+    rows = c.execute("select dispatch_id, kernel_name, grid_size, counter_name, value, duration "
+                     "from counters_collection").fetchall()
     per = collections.defaultdict(lambda: collections.defaultdict(float))
-    names = {}
-    for did, kn, gs, cn, v in rows:
+    names, durs = {}, {}
+    for did, kn, gs, cn, v, dur in rows:
         per[did][cn] = max(per[did][cn], v) if cn == "GRBM_GUI_ACTIVE" else per[did][cn] + v
         kk = kn.replace("(anonymous namespace)::", "").replace("prana::", "")
         names[did] = (re.sub(r"^void ", "", kk.split("(")[0]), gs)
+        durs[did] = dur
     agg = collections.defaultdict(lambda: collections.defaultdict(list))
     for did, d in per.items():
         for cn, v in d.items():
             agg[names[did]][cn].append(v)
-    out = ["| kernel | grid | dispatches | MfmaUtil % | VALUBusy % | int8 MFMA ops / dispatch |", "|---|---:|---:|---:|---:|---:|"]
+        agg[names[did]]["_dur_ns"].append(durs[did])
+    out = ["| kernel | grid | dispatches | us | implied clock GHz | MfmaUtil % | VALU busy % per SIMD "
+           "| int8 MFMA ops / dispatch |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
     for (k, gs), d in sorted(agg.items()):
         if "gemm" not in k and "gemv" not in k:
             continue
         n = len(d["GRBM_GUI_ACTIVE"])
-        gui = sum(d["GRBM_GUI_ACTIVE"]) / n
+        cyc = sum(d["GRBM_GUI_ACTIVE"]) / n / xcds
+        dur = sum(d["_dur_ns"]) / n
         mfma = sum(d["SQ_VALU_MFMA_BUSY_CYCLES"]) / n
-        valu = 4 * sum(d["SQ_ACTIVE_INST_VALU"]) / n
+        valu = sum(d["SQ_ACTIVE_INST_VALU"]) / n
         mops = sum(d["SQ_INSTS_VALU_MFMA_MOPS_I8"]) / n * 512
-        out.append(f"| `{k}` | {int(gs)} | {n} | {100 * mfma / (gui * 4 * cus):.2f} | {100 * valu / cus / gui:.1f} "
-                   f"| {mops:.3e} |")
+        out.append(f"| `{k}` | {int(gs)} | {n} | {dur / 1e3:.1f} | {cyc / dur:.2f} | "
+                   f"{100 * mfma / (cyc * 4 * cus):.1f} | {100 * valu / cus / cyc:.1f} | {mops:.3e} |")
     print("\n".join(out))
 
 
