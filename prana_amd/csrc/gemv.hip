@@ -2884,7 +2884,9 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
       default: return launch_gemm_mfma<kKindQ4_0>(ms, os, n, q, sa, n_tok, s);
     }
   }
-  if (ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens) {
+  bool per_matrix = ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens;
+  for (int i = 0; i < n; i++) per_matrix = per_matrix || gemv_batch_skinny(ms[i], n_tok);
+  if (per_matrix) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
       if (rc) return rc;
@@ -2999,20 +3001,24 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
   return launch_quantize_acts(h, n_tok, gate.rows, hq, hsa, hsum, s);  // matmul.rs:105-127 on h
 }
 
+// Batches of block-32 kinds on the skinny matrix-core kernel: from 9 tokens
+// always, from 3 tokens for matrices of at least kSkinnyMinBlocks blocks.
+// Its cost hardly grows with the batch up to 16 tokens (one 16-token tile),
+// while the decode tiles and the chunk-major verify kernel pay per token:
+// on the 7B Q4_0 shapes at 5 tokens, down 25.3 against 33.8 us, the head
+// 26.2 against 39.6 us; at 9 tokens wo 8.8 against 14.6 us; at 2 tokens
+// and for Q|K|V or wo up to 8 tokens the decode tiles stay ahead.
+constexpr size_t kSkinnyMinBlocks = 1536 * 1024;
+bool gemv_batch_skinny(const DevMat& m, size_t n_tok) {
+  if (m.kind != kKindQ8F && m.kind != kKindQ8_0 && m.kind != kKindQ4_0) return false;
+  if (n_tok >= kGemvSkinnyMinTokens && n_tok <= kGemvSkinnyMaxTokens) return true;
+  return n_tok >= 3 && n_tok < kGemvSkinnyMinTokens && m.rows * (m.cols / 32) >= kSkinnyMinBlocks;
+}
+
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s) {
   if (n_tok == 0 || m.rows == 0) return kOk;
-  // batches of up to 16 tokens that the chunk-major multi-token kernel takes
-  // stay on the decode path when it beats the skinny matrix-core kernel:
-  // rows of more than 128 blocks, or few rows (the skinny kernel has the
-  // larger fixed cost, the chunk-major one the larger cost per row and token;
-  // on the 7B Q4_0 shapes they cross near 9 tokens x 8192 rows; for the 8-bit
-  // kinds the skinny kernel stays ahead from 9 tokens)
-  const int nb_m = static_cast<int>(m.cols / 32);
-  const bool km = n_tok <= kDecodeMaxTokens && km_chunk(nb_m, n_tok) > 0 &&
-                  (m.kind == kKindQ4_0 || n_tok <= static_cast<size_t>(kDecMaxTok)) &&
-                  (nb_m > 128 || m.rows * n_tok <= size_t{9} * 8192);
-  if (gemv_skinny(m.kind, n_tok) && !km) {
+  if (gemv_batch_skinny(m, n_tok)) {
     switch (m.kind) {
       case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
       case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);

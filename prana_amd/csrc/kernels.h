@@ -132,6 +132,9 @@ inline bool gemv_skinny(int kind, size_t n_tok) {
   return (kind == kKindQ8F || kind == kKindQ8_0 || kind == kKindQ4_0) && n_tok >= kGemvSkinnyMinTokens &&
          n_tok <= kGemvSkinnyMaxTokens;
 }
+// Whether a batch of n_tok tokens over m runs on the skinny matrix-core
+// kernel (block-32 kinds; see launch_gemv).
+bool gemv_batch_skinny(const DevMat& m, size_t n_tok);
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s);

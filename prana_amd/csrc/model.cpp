@@ -357,7 +357,8 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
 
 int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm) {
   const size_t H = c.hidden_dim;
-  const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens;
+  const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens &&
+                    !gemv_batch_skinny(gate.d, n);  // else two matrix-core launches and launch_act_mul
   PRANA_CHECK(!norm || (fuse && n == 1), "apply_gate_up: a fused rmsnorm takes one token of fusable matrices");
   if (fuse) {
     return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {

@@ -118,13 +118,14 @@ def test_matmul_skinny_block_split_ragged(ty, rows, cols, n_tok):
 
 @pytest.mark.parametrize("ty", [fx.Q8_0, fx.Q4_0])
 @pytest.mark.parametrize("rows,cols,n_tok", [(37, 2048, 10), (300, 4096, 12), (129, 7168, 8), (70, 14336, 3),
-                                             (70, 14336, 6), (4097, 4096, 9), (515, 14336, 16)])
+                                             (70, 14336, 6), (4097, 4096, 9), (515, 14336, 16), (4100, 14336, 2),
+                                             (4100, 14336, 3), (4100, 14336, 5), (12300, 4096, 7)])
 def test_matmul_verify_batch_chunked(ty, rows, cols, n_tok):
     # Widths of 2, 4, 7 or 14 chunks of 32 or 64 blocks: the chunk-major
     # multi-token kernel (activations and term rows staged one chunk at a
-    # time) takes rows of more than 128 blocks from 2 tokens and, for Q4_0,
-    # narrower rows from 9 tokens (16 tokens: two launches); Q8_0 takes the
-    # skinny matrix-core kernel from 9 tokens. Ragged last tiles.
+    # time) takes rows of more than 128 blocks at 2..8 tokens; from 9 tokens,
+    # and from 3 tokens for matrices of at least 1.5M blocks, the skinny
+    # matrix-core kernel takes the batch. Ragged last tiles.
     raw, g, o = _mat_pair(ty, rows, cols, 60 + n_tok + cols, real=True)
     a = rng(n_tok + 3).standard_normal((n_tok, cols)).astype(np.float32)
     assert same_bits(g.apply(a), o.apply(a))
