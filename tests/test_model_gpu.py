@@ -278,18 +278,19 @@ def test_block32_verify_batches_bitexact(ty):
 @pytest.mark.parametrize("ty", [P.Q4_0, P.Q8_0])
 def test_large_verify_batches_on_matrix_cores_bitexact(ty):
     # Verify batches of 3..8 tokens over matrices of at least 1.5M blocks take
-    # the skinny matrix-core kernel: here gate, up (12288 x 4096) and down
-    # (4096 x 12288) each as their own launch, SiLU and the quantization of h
-    # in launch_act_mul; the smaller Q|K|V and wo stay on the decode tiles.
-    cfg = M.config(4096, 12288, 1, 32, 8, 300, 32, head_dim=128)
+    # the skinny matrix-core kernel: here down (4096 x 12288); gate|up stays
+    # one fused launch, the smaller Q|K|V and wo stay on the decode tiles. At
+    # 9 tokens every projection takes it, gate and up as two launches with
+    # SiLU and the quantization of h in launch_act_mul.
+    cfg = M.config(4096, 12288, 1, 32, 8, 300, 48, head_dim=128)
     t = M.synth_tensors(cfg, lambda name, cols: ty, 13)
     g, o = pair(cfg, t)
-    gc, oc = g.cache(32), o.cache(32)
-    prompt = np.random.default_rng(13).integers(0, cfg["vocab_size"], 24).astype(np.uint32)
+    gc, oc = g.cache(48), o.cache(48)
+    prompt = np.random.default_rng(13).integers(0, cfg["vocab_size"], 40).astype(np.uint32)
     gc.prefill(prompt[:4])
     oc.prefill(prompt[:4])
     pos = 4
-    for n in (3, 5, 8):
+    for n in (3, 5, 8, 9):
         batch = [int(x) for x in prompt[pos:pos + n]]
         assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
         pos += n
