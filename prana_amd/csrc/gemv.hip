@@ -1891,9 +1891,18 @@ struct MmaJob {
   GemvOut o[3];
   int t0[3];  // first x-block of each matrix (t0[0] = 0)
   int n_mats;
+  // ACT launches (m[0] = gate, m[1] = up, H = rows % 64 == 0): x-block b
+  // holds rows 64b..64b+63 of both, and the epilogue forms h = act(g) * u
+  // (infer.rs:197-199) and its 32-row blocks quantized for the down
+  // projection (matmul.rs:105-127), as launch_act_mul does
+  int gelu;  // 0 silu, 1 gelu_tanh
+  float* h;  // optional f32 h [n_tok][H]
+  int8_t* hq;
+  float* hsa;
+  int* hsum;
 };
 
-template <int KIND>
+template <int KIND, bool ACT = false>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t* __restrict__ q,
                                                         const float* __restrict__ sa, int n_tok) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
@@ -1902,14 +1911,20 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t
   uint8_t* lds = reinterpret_cast<uint8_t*>(mma_smem);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
   const int bx = blockIdx.x;
-  const int mi = job.n_mats > 2 && bx >= job.t0[2] ? 2 : job.n_mats > 1 && bx >= job.t0[1] ? 1 : 0;  // uniform
+  const int mi = ACT ? 0 : job.n_mats > 2 && bx >= job.t0[2] ? 2 : job.n_mats > 1 && bx >= job.t0[1] ? 1 : 0;
   const DevMat m = mi == 0 ? job.m[0] : mi == 1 ? job.m[1] : job.m[2];
   const GemvOut o = mi == 0 ? job.o[0] : mi == 1 ? job.o[1] : job.o[2];
   const int K = static_cast<int>(m.cols), G = K / 32;
   const int R = static_cast<int>(m.rows);
-  const int row0 = (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * kMmaRows;
+  const int row0 = ACT ? bx * (kMmaRows / 2) : (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * kMmaRows;
   const int m0 = blockIdx.y * kMmaToks;
   const int n_chunks = (G + L::CB - 1) / L::CB;
+  // tile row lr (0..127): its matrix row, and (ACT) gate rows 0..63 / up rows 64..127
+  auto tile_row = [&](int lr) { return min(row0 + (ACT ? (lr & 63) : lr), R - 1); };
+  const uint8_t* const qs_up = ACT ? job.m[1].qs : m.qs;
+  const void* const sc_up = ACT ? job.m[1].sc : m.sc;
+  auto tile_qs = [&](int lr) { return ACT && lr >= 64 ? qs_up : m.qs; };
+  auto tile_sc = [&](int lr) { return ACT && lr >= 64 ? sc_up : m.sc; };
 
   auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
     MmaRegs<KIND> r;
@@ -1917,9 +1932,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t
 #pragma unroll
     for (int i = 0; i < L::WPL; i++) {
       const int p = tid + 256 * i;
-      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int rr = tile_row(p / L::WPR), pr = p % L::WPR;
       const int blk = min(cb0 + pr / (L::QB / 16), G - 1);
-      r.w[i] = *reinterpret_cast<const sk_i4*>(m.qs + (size_t)rr * G * L::QB + (size_t)blk * L::QB +
+      r.w[i] = *reinterpret_cast<const sk_i4*>(tile_qs(p / L::WPR) + (size_t)rr * G * L::QB + (size_t)blk * L::QB +
                                                (pr % (L::QB / 16)) * 16);
     }
 #pragma unroll
@@ -1932,9 +1947,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t
 #pragma unroll
     for (int i = 0; i < L::DPL; i++) {
       const int p = tid + 256 * i;
-      const size_t gi = (size_t)min(row0 + p / L::CB, R - 1) * G + min(cb0 + p % L::CB, G - 1);
-      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
-                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+      const size_t gi = (size_t)tile_row(p / L::CB) * G + min(cb0 + p % L::CB, G - 1);
+      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(tile_sc(p / L::CB))[gi]
+                                : reinterpret_cast<const uint16_t*>(tile_sc(p / L::CB))[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
@@ -2057,6 +2072,53 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t
     if (c + 4 < n_chunks) r1 = load(c + 4);
     __syncthreads();
   }
+  if constexpr (ACT) {
+    // waves 2 and 3 hold the up rows of waves 0 and 1's gate rows: the pair
+    // swaps half of its values through LDS (free: the last chunk's barrier is
+    // behind), so that wave w < 2 forms h for its values 0..7 and wave w + 2
+    // for values 8..15 (tokens 8g + 4h + e for value 4g + e); the 32 lanes of
+    // a half hold one 32-row block of h for each of those tokens
+    float* s_x = reinterpret_cast<float*>(lds);  // [4 waves][64 lanes][9]
+    const int pw = wave & 1, up_wave = wave >> 1;
+#pragma unroll
+    for (int v = 0; v < 8; v++) s_x[(wave * 64 + lane) * 9 + v] = acc[up_wave ? v : v + 8];
+    __syncthreads();
+    const int r = row0 + pw * 32 + (lane & 31);  // < H (H % 64 == 0)
+    const int H = R;
+    const float* other = s_x + (((up_wave ? pw : pw + 2) * 64) + lane) * 9;  // the partner wave's values
+    float hv[8];
+#pragma unroll
+    for (int v = 0; v < 8; v++) {
+      float g = up_wave ? other[v] : acc[v];
+      const float u = up_wave ? acc[v + 8] : other[v];
+      if (job.gelu) {
+        const float kS = 0.7978846f;  // norms.rs:36
+        const float x3 = g * g * g;
+        g = 0.5f * g * (1.0f + dev_tanhf(kS * (g + 0.044715f * x3)));
+      } else {
+        g = g * (1.0f / (1.0f + dev_expf(-g)));
+      }
+      hv[v] = g * u;
+    }
+    int qv[8], sm[8];
+    float sc[8];
+    quantize_lanes<8>(hv, qv, sc, sm);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int v = up_wave ? j + 8 : j;
+      const int t = m0 + 8 * (v / 4) + 4 * h + (v % 4);
+      if (t < n_tok) {
+        const size_t gi = (size_t)t * H + r;
+        job.hq[gi] = static_cast<int8_t>(qv[j]);
+        if (job.h) job.h[gi] = hv[j];
+        if ((lane & 31) == 0) {
+          job.hsa[gi >> 5] = sc[j];
+          job.hsum[gi >> 5] = sm[j];
+        }
+      }
+    }
+    return;
+  }
   const int n_row = row0 + wr_row;
   if (n_row < R) {
 #pragma unroll
@@ -2092,6 +2154,37 @@ int launch_gemm_mfma(const DevMat* ms, const GemvOut* os, int n_mats, const int8
   PRANA_CHECK(tiles >= 1 && tiles < (1u << 31), "gemm: row tiles out of range");
   dim3 grid(static_cast<unsigned>(tiles), (n_tok + kMmaToks - 1) / kMmaToks);
   hipLaunchKernelGGL(gemm_mfma_kernel<KIND>, grid, dim3(256), L::BYTES * 2, s, job, q, sa, (int)n_tok);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
+}
+
+// gate|up, the activation and the quantization of h in one launch (batches
+// beyond the skinny kernel's, block-32 kinds, H % 64 == 0).
+template <int KIND>
+int launch_gemm_mfma_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, size_t n_tok,
+                         int gelu, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s) {
+  using L = MmaLayout<KIND>;
+  static const bool attr_ok = [] {
+    return L::BYTES * 2 <= 65536 ||
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_mfma_kernel<KIND, true>), L::BYTES * 2);
+  }();
+  PRANA_CHECK(attr_ok, "gemm: LDS size not granted");
+  static_assert(4 * 64 * 9 * 4 <= L::BYTES * 2, "the gate/up exchange fits the staging LDS");
+  PRANA_CHECK(gate.kind == KIND && up.kind == KIND && gate.rows == up.rows && gate.cols == up.cols &&
+                  gate.rows % 64 == 0 && gate.cols % 32 == 0 && gate.cols <= (1u << 30) && gate.rows <= (1u << 30),
+              "gemm act: gate and up must share kind and shape, rows a multiple of 64");
+  PRANA_CHECK(hq && hsa && hsum, "gemm act: quantized h outputs required");
+  MmaJob job{};
+  job.m[0] = gate;
+  job.m[1] = up;
+  job.n_mats = 2;
+  job.gelu = gelu;
+  job.h = h;
+  job.hq = hq;
+  job.hsa = hsa;
+  job.hsum = hsum;
+  dim3 grid(static_cast<unsigned>(gate.rows / 64), (n_tok + kMmaToks - 1) / kMmaToks);
+  hipLaunchKernelGGL((gemm_mfma_kernel<KIND, true>), grid, dim3(256), L::BYTES * 2, s, job, q, sa, (int)n_tok);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
@@ -2999,6 +3092,22 @@ int launch_gemv_act(const DevMat& gate, const DevMat& up, int act, const int8_t*
   });
   if (rc || in_kernel) return rc;
   return launch_quantize_acts(h, n_tok, gate.rows, hq, hsa, hsum, s);  // matmul.rs:105-127 on h
+}
+
+bool gemm_act_fusable(const DevMat& gate, const DevMat& up, size_t n_tok) {
+  const int k = gate.kind;
+  return (k == kKindQ8F || k == kKindQ8_0 || k == kKindQ4_0) && up.kind == k && gate.rows == up.rows &&
+         gate.cols == up.cols && gate.rows % 64 == 0 && gate.cols % 32 == 0 && n_tok > kGemvSkinnyMaxTokens;
+}
+
+int launch_gemm_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, size_t n_tok, int gelu,
+                    float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s) {
+  PRANA_CHECK(gemm_act_fusable(gate, up, n_tok), "gemm act: these matrices and batch do not take the fused launch");
+  switch (gate.kind) {
+    case kKindQ8F: return launch_gemm_mfma_act<kKindQ8F>(gate, up, q, sa, n_tok, gelu, h, hq, hsa, hsum, s);
+    case kKindQ8_0: return launch_gemm_mfma_act<kKindQ8_0>(gate, up, q, sa, n_tok, gelu, h, hq, hsa, hsum, s);
+    default: return launch_gemm_mfma_act<kKindQ4_0>(gate, up, q, sa, n_tok, gelu, h, hq, hsa, hsum, s);
+  }
 }
 
 // Batches of block-32 kinds on the skinny matrix-core kernel: from 9 tokens

@@ -135,6 +135,13 @@ inline bool gemv_skinny(int kind, size_t n_tok) {
 // Whether a batch of n_tok tokens over m runs on the skinny matrix-core
 // kernel (block-32 kinds; see launch_gemv).
 bool gemv_batch_skinny(const DevMat& m, size_t n_tok);
+// Batches beyond the skinny kernel's (prefill): gate and up (block-32 kind,
+// H = rows % 64 == 0) on the matrix cores in one launch whose epilogue forms
+// h = act(g) * u (gelu: gelu_tanh, else silu) and quantizes it into
+// (hq, hsa, hsum), as launch_act_mul; h (optional) gets the f32 values.
+bool gemm_act_fusable(const DevMat& gate, const DevMat& up, size_t n_tok);
+int launch_gemm_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, size_t n_tok, int gelu,
+                    float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s);

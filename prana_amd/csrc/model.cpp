@@ -355,7 +355,7 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
   return kOk;
 }
 
-int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm) {
+int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm, bool dense_h) {
   const size_t H = c.hidden_dim;
   // from 9 tokens two skinny matrix-core launches and launch_act_mul (at 5
   // tokens the fused launch and the quantization of h tie with them on the 7B
@@ -368,6 +368,13 @@ int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s
       return launch_gemv_act(gate.d, up.d, c.act, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n,
                              ws.gate.as<float>(), ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s,
                              norm);
+    });
+  }
+  if (gemm_act_fusable(gate.d, up.d, n)) {  // prefill: gate|up, the activation and h's quantization in one launch
+    float* h = dense_h ? ws.gate.as<float>() : nullptr;
+    return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {
+      return launch_gemm_act(gate.d, up.d, ws.qa.as<int8_t>(), ws.sa.as<float>(), n, c.act, h, ws.hq.as<int8_t>(),
+                             ws.hsa.as<float>(), ws.hsum.as<int>(), s);
     });
   }
   GemvOut og{ws.gate.as<float>(), H, nullptr, 0};
@@ -623,7 +630,9 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     const NormIn nin_ffn{x, L.vec[kRmsFfn].as<float>(), c.norm_eps, ws.xch.as<unsigned>()};
     const bool ffn_fused = mode == 0 && n == 1 && gemv_norm_act_fusable(L.w[kW1]->d, L.w[kW3]->d);
     if (!ffn_fused && (rc = norm_quant(x, L.vec[kRmsFfn], n, s))) return rc;
-    if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s, ffn_fused ? &nin_ffn : nullptr))) return rc;
+    if ((rc = apply_gate_up(*L.w[kW1], *L.w[kW3], n, s, ffn_fused ? &nin_ffn : nullptr,
+                            L.w[kW2]->d.kind == kKindF32)))
+      return rc;
     if ((rc = apply(*L.w[kW2], n, ws.gate.as<float>(), ores, s, true))) return rc;
   }
   return kOk;

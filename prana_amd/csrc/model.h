@@ -131,7 +131,9 @@ struct Model {
   // quantization fused when both share a kind; h lands in ws.gate (f32) and
   // ws.hq/hsa/hsum (quantized).
   // norm: one token whose rmsnorm the launch computes (gemv_norm_act_fusable).
-  int apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm = nullptr);
+  // dense_h: the down projection reads the f32 h (a dense matrix), not only its quantized form
+  int apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm = nullptr,
+                    bool dense_h = true);
   template <class F>
   int timed(size_t bytes, size_t n, hipStream_t s, F&& launch);
   int norm_quant(const float* x, const DevBuf& w, size_t n, hipStream_t s);

@@ -296,6 +296,26 @@ def test_large_verify_batches_on_matrix_cores_bitexact(ty):
         pos += n
 
 
+@pytest.mark.parametrize("ty,act,dense_down", [(P.Q4_0, 0, False), (P.Q8_0, 1, False), (P.Q4_0, 0, True)])
+def test_prefill_gate_up_act_one_launch_bitexact(ty, act, dense_down):
+    # Prompts beyond the skinny kernel's batches (more than 64 tokens) run
+    # gate|up on the matrix cores in one launch that also forms h = act(g) * u
+    # (silu, or gelu_tanh) and quantizes it for down; with a dense f32 down
+    # projection it also writes the f32 h that down reads. Ragged token tiles
+    # (100 = 3 x 32 + 4), two 64-row tile rows per 32-row quantization block.
+    cfg = M.config(512, 1536, 2, 8, 2, 300, 160, head_dim=64, act=act)
+    t = M.synth_tensors(cfg, lambda name, cols: M.F32 if dense_down and "ffn_down" in name else ty, 17 + act)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(160), o.cache(160)
+    prompt = np.random.default_rng(17).integers(0, cfg["vocab_size"], 101).astype(np.uint32)
+    gc.prefill(prompt[:100])
+    oc.prefill(prompt[:100])
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(gc.read(layer, 0, 100), oc.read(layer, 0, 100)), layer
+        assert np.array_equal(gc.read(layer, 1, 100), oc.read(layer, 1, 100)), layer
+    assert same_bits(gc.forward(int(prompt[100]), 100), oc.forward(int(prompt[100]), 100))
+
+
 @pytest.mark.parametrize("dim", [512, 896])
 def test_mixed_format_qkv_one_launch_bitexact(dim):
     # The K-quant mixture stores v in another format than q and k: Q4_K with
