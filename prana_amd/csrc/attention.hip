@@ -1045,8 +1045,9 @@ int launch_wide(const float* q, const uint16_t* k, const uint16_t* v, size_t pos
 
 // ---------------------------------------------------------------- prefill blocks
 // Prefill attention over the f32 K/V of the window (attention.rs:236-284)
-// with one 256-lane workgroup per (head, block of kPbQ consecutive query
-// rows): each K row a lane fetches serves the block's kPbQ score chains (side
+// with one 256-lane workgroup per (head, pair of blocks of kPbQ consecutive
+// query rows, one from each end of the causal window, taken one after the
+// other): each K row a lane fetches serves the block's kPbQ score chains (side
 // by side), and each V element a lane fetches serves kPbQ*hd/256 P·V chains.
 // Row qq of the block attends keys 0..i0+qq; its softmax sum is the exact
 // left-to-right fold, one row after another.
@@ -1077,144 +1078,154 @@ __global__ __launch_bounds__(kPbNT) void attn_prefill_blk(const float* __restric
   const int scw = DYN ? scw_arg : kPbW;
   __shared__ float s_red[kPbQ][kPbNT / 64];
   const int h = blockIdx.x, tid = threadIdx.x;
-  const int i0 = blockIdx.y * kPbQ;
-  const int nk = min(i0 + kPbQ, seq);  // keys any row of the block attends
-  const int kvh = h / group;
-  const int kv_dim = (n_heads / group) * HD;
-  for (int e = tid; e < kPbQ * HD; e += kPbNT) {
-    const int qq = e / HD, d = e % HD;
-    s_q[qq][d] = i0 + qq < seq ? q[((size_t)(i0 + qq) * n_heads + h) * HD + d] : 0.0f;
-  }
-  __syncthreads();
-  // ---- scores: (fold_d q[d]*k_t[d] from -0.0) * (1/sqrt(hd)), lane per key row
-  const float scale = 1.0f / sqrtf(static_cast<float>(HD));
-  float mxl[kPbQ];
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) mxl[qq] = -INFINITY;
-  for (int t = tid; t < nk; t += kPbNT) {
-    const float4* kp = reinterpret_cast<const float4*>(k + (size_t)t * kv_dim + (size_t)kvh * HD);
-    float dot[kPbQ];
-#pragma unroll
-    for (int qq = 0; qq < kPbQ; qq++) dot[qq] = -0.0f;
-#pragma unroll 4
-    for (int c = 0; c < HD / 4; c++) {
-      const float4 kv = kp[c];
-#pragma unroll
+  // Workgroup y takes query blocks y and nqb-1-y (the causal window's short
+  // and long ends), so every workgroup has about the same keys to cover
+  const int nqb = (seq + kPbQ - 1) / kPbQ;
+  for (int pass = 0; pass < 2; pass++) {
+    const int qb = pass == 0 ? static_cast<int>(blockIdx.y) : nqb - 1 - static_cast<int>(blockIdx.y);
+    if (pass == 1) {
+      if (qb <= static_cast<int>(blockIdx.y)) break;  // uniform: an odd count's middle block, done once
+      __syncthreads();  // the first block's reads of the LDS rows are done
+    }
+    const int i0 = qb * kPbQ;
+    const int nk = min(i0 + kPbQ, seq);  // keys any row of the block attends
+    const int kvh = h / group;
+    const int kv_dim = (n_heads / group) * HD;
+    for (int e = tid; e < kPbQ * HD; e += kPbNT) {
+      const int qq = e / HD, d = e % HD;
+      s_q[qq][d] = i0 + qq < seq ? q[((size_t)(i0 + qq) * n_heads + h) * HD + d] : 0.0f;
+    }
+    __syncthreads();
+    // ---- scores: (fold_d q[d]*k_t[d] from -0.0) * (1/sqrt(hd)), lane per key row
+    const float scale = 1.0f / sqrtf(static_cast<float>(HD));
+    float mxl[kPbQ];
+  #pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) mxl[qq] = -INFINITY;
+    for (int t = tid; t < nk; t += kPbNT) {
+      const float4* kp = reinterpret_cast<const float4*>(k + (size_t)t * kv_dim + (size_t)kvh * HD);
+      float dot[kPbQ];
+  #pragma unroll
+      for (int qq = 0; qq < kPbQ; qq++) dot[qq] = -0.0f;
+  #pragma unroll 4
+      for (int c = 0; c < HD / 4; c++) {
+        const float4 kv = kp[c];
+  #pragma unroll
+        for (int qq = 0; qq < kPbQ; qq++) {
+          const float4 qv = reinterpret_cast<const float4*>(s_q[qq])[c];
+          dot[qq] += qv.x * kv.x;
+          dot[qq] += qv.y * kv.y;
+          dot[qq] += qv.z * kv.z;
+          dot[qq] += qv.w * kv.w;
+        }
+      }
+  #pragma unroll
       for (int qq = 0; qq < kPbQ; qq++) {
-        const float4 qv = reinterpret_cast<const float4*>(s_q[qq])[c];
-        dot[qq] += qv.x * kv.x;
-        dot[qq] += qv.y * kv.y;
-        dot[qq] += qv.z * kv.z;
-        dot[qq] += qv.w * kv.w;
+        if (t <= i0 + qq) {  // causal: row i0+qq attends keys 0..i0+qq
+          const float sv = dot[qq] * scale;
+          s_scd[(qq) * scw + exact::run_pad(t)] = sv;
+          mxl[qq] = fmaxf(mxl[qq], sv);
+        }
       }
     }
-#pragma unroll
+  #pragma unroll
     for (int qq = 0; qq < kPbQ; qq++) {
-      if (t <= i0 + qq) {  // causal: row i0+qq attends keys 0..i0+qq
-        const float sv = dot[qq] * scale;
-        s_scd[(qq) * scw + exact::run_pad(t)] = sv;
-        mxl[qq] = fmaxf(mxl[qq], sv);
+      const float m = wave_max_f32(mxl[qq]);
+      if ((tid & 63) == 0) s_red[qq][tid >> 6] = m;
+    }
+    __syncthreads();
+    float mx[kPbQ];
+  #pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) {
+      mx[qq] = -INFINITY;
+  #pragma unroll
+      for (int w = 0; w < kPbNT / 64; w++) mx[qq] = fmaxf(mx[qq], s_red[qq][w]);
+    }
+  #pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) {
+      const int n = i0 + qq + 1;
+      if (i0 + qq < seq)
+        for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = dev_expf(s_scd[(qq) * scw + exact::run_pad(t)] - mx[qq]);
+    }
+    __syncthreads();
+    // softmax sums in the reference's left-to-right order (norms.rs:53): each
+    // wave folds one row at a time, the waves' rows at once
+    __shared__ float s_inv[kPbQ];
+    static_assert(kPbQ % (kPbNT / 64) == 0, "whole rounds of rows");
+  #pragma unroll
+    for (int r = 0; r < kPbQ / (kPbNT / 64); r++) {
+      const int qq = r * (kPbNT / 64) + (tid >> 6);
+      if (i0 + qq < seq) {  // wave-uniform; the group barriers are the wave's own
+        const float sum =
+            exact::group_seq_sum_short<64, kPbNT / 64>([s_scd, scw, qq](int t) { return s_scd[(qq) * scw + exact::run_pad(t)]; }, i0 + qq + 1);
+        if ((tid & 63) == 0) s_inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
+      } else if ((tid & 63) == 0) {
+        s_inv[qq] = 0.0f;
       }
     }
-  }
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) {
-    const float m = wave_max_f32(mxl[qq]);
-    if ((tid & 63) == 0) s_red[qq][tid >> 6] = m;
-  }
-  __syncthreads();
-  float mx[kPbQ];
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) {
-    mx[qq] = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kPbNT / 64; w++) mx[qq] = fmaxf(mx[qq], s_red[qq][w]);
-  }
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) {
-    const int n = i0 + qq + 1;
-    if (i0 + qq < seq)
-      for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = dev_expf(s_scd[(qq) * scw + exact::run_pad(t)] - mx[qq]);
-  }
-  __syncthreads();
-  // softmax sums in the reference's left-to-right order (norms.rs:53): each
-  // wave folds one row at a time, the waves' rows at once
-  __shared__ float s_inv[kPbQ];
-  static_assert(kPbQ % (kPbNT / 64) == 0, "whole rounds of rows");
-#pragma unroll
-  for (int r = 0; r < kPbQ / (kPbNT / 64); r++) {
-    const int qq = r * (kPbNT / 64) + (tid >> 6);
-    if (i0 + qq < seq) {  // wave-uniform; the group barriers are the wave's own
-      const float sum =
-          exact::group_seq_sum_short<64, kPbNT / 64>([s_scd, scw, qq](int t) { return s_scd[(qq) * scw + exact::run_pad(t)]; }, i0 + qq + 1);
-      if ((tid & 63) == 0) s_inv[qq] = sum > 0.0f ? 1.0f / sum : 0.0f;
-    } else if ((tid & 63) == 0) {
-      s_inv[qq] = 0.0f;
+    __syncthreads();
+    float inv[kPbQ];
+  #pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) inv[qq] = s_inv[qq];
+  #pragma unroll
+    for (int qq = 0; qq < kPbQ; qq++) {
+      const int n = i0 + qq + 1;
+      if (i0 + qq < seq)
+        for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = s_scd[(qq) * scw + exact::run_pad(t)] * inv[qq];
     }
-  }
-  __syncthreads();
-  float inv[kPbQ];
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) inv[qq] = s_inv[qq];
-#pragma unroll
-  for (int qq = 0; qq < kPbQ; qq++) {
-    const int n = i0 + qq + 1;
-    if (i0 + qq < seq)
-      for (int t = tid; t < n; t += kPbNT) s_scd[(qq) * scw + exact::run_pad(t)] = s_scd[(qq) * scw + exact::run_pad(t)] * inv[qq];
-  }
-  __syncthreads();
-  // ---- P·V: lane (d, qg) folds rows qg, qg+QSTEP, ... of dim d over t from +0.0
-  const int d = tid % HD, qg = tid / HD;
-  const float* vcol = v + (size_t)kvh * HD + d;
-  float acc[QPL];
-#pragma unroll
-  for (int c = 0; c < QPL; c++) acc[c] = 0.0f;
-  // rows 0..i0 are attended by every query row of the block: no causal test
-  // there, so the probability and V reads of a batch issue together; only
-  // the last kPbQ - 1 keys need the per-row select
-  int t = 0;
-  for (; t + 8 <= i0 + 1; t += 8) {
-    float vt[8], pt[8][QPL];
-#pragma unroll
-    for (int u = 0; u < 8; u++) vt[u] = vcol[(size_t)(t + u) * kv_dim];
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-      for (int c = 0; c < QPL; c++) pt[u][c] = s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t + u)];
-#pragma unroll
-    for (int u = 0; u < 8; u++)
-#pragma unroll
-      for (int c = 0; c < QPL; c++) acc[c] = acc[c] + pt[u][c] * vt[u];
-  }
-  for (; t <= i0; t++) {
-    const float vt = vcol[(size_t)t * kv_dim];
-#pragma unroll
-    for (int c = 0; c < QPL; c++) acc[c] = acc[c] + s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t)] * vt;
-  }
-  for (; t < nk; t++) {
-    const float vt = vcol[(size_t)t * kv_dim];
-#pragma unroll
+    __syncthreads();
+    // ---- P·V: lane (d, qg) folds rows qg, qg+QSTEP, ... of dim d over t from +0.0
+    const int d = tid % HD, qg = tid / HD;
+    const float* vcol = v + (size_t)kvh * HD + d;
+    float acc[QPL];
+  #pragma unroll
+    for (int c = 0; c < QPL; c++) acc[c] = 0.0f;
+    // rows 0..i0 are attended by every query row of the block: no causal test
+    // there, so the probability and V reads of a batch issue together; only
+    // the last kPbQ - 1 keys need the per-row select
+    int t = 0;
+    for (; t + 8 <= i0 + 1; t += 8) {
+      float vt[8], pt[8][QPL];
+  #pragma unroll
+      for (int u = 0; u < 8; u++) vt[u] = vcol[(size_t)(t + u) * kv_dim];
+  #pragma unroll
+      for (int u = 0; u < 8; u++)
+  #pragma unroll
+        for (int c = 0; c < QPL; c++) pt[u][c] = s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t + u)];
+  #pragma unroll
+      for (int u = 0; u < 8; u++)
+  #pragma unroll
+        for (int c = 0; c < QPL; c++) acc[c] = acc[c] + pt[u][c] * vt[u];
+    }
+    for (; t <= i0; t++) {
+      const float vt = vcol[(size_t)t * kv_dim];
+  #pragma unroll
+      for (int c = 0; c < QPL; c++) acc[c] = acc[c] + s_scd[(qg + c * QSTEP) * scw + exact::run_pad(t)] * vt;
+    }
+    for (; t < nk; t++) {
+      const float vt = vcol[(size_t)t * kv_dim];
+  #pragma unroll
+      for (int c = 0; c < QPL; c++) {
+        const int qq = qg + c * QSTEP;
+        const float nv = acc[c] + s_scd[(qq) * scw + exact::run_pad(t)] * vt;
+        acc[c] = t <= i0 + qq ? nv : acc[c];
+      }
+    }
+  #pragma unroll
     for (int c = 0; c < QPL; c++) {
-      const int qq = qg + c * QSTEP;
-      const float nv = acc[c] + s_scd[(qq) * scw + exact::run_pad(t)] * vt;
-      acc[c] = t <= i0 + qq ? nv : acc[c];
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < QPL; c++) {
-    const int qq = qg + c * QSTEP, i = i0 + qq;
-    const bool live = i < seq;
-    const size_t gi = ((size_t)min(i, seq - 1) * n_heads + h) * HD + d;
-    if (live) out[gi] = acc[c];
-    if (qd) {  // 32-lane groups share qq (HD is a multiple of 32 here)
-      float qscale;
-      int qs;
-      const int qi = quantize_lane(live ? acc[c] : 0.0f, &qscale, &qs);
-      if (live) {
-        qd[gi] = static_cast<int8_t>(qi);
-        if ((gi & 31) == 0) {
-          qsa[gi >> 5] = qscale;
-          qsum[gi >> 5] = qs;
+      const int qq = qg + c * QSTEP, i = i0 + qq;
+      const bool live = i < seq;
+      const size_t gi = ((size_t)min(i, seq - 1) * n_heads + h) * HD + d;
+      if (live) out[gi] = acc[c];
+      if (qd) {  // 32-lane groups share qq (HD is a multiple of 32 here)
+        float qscale;
+        int qs;
+        const int qi = quantize_lane(live ? acc[c] : 0.0f, &qscale, &qs);
+        if (live) {
+          qd[gi] = static_cast<int8_t>(qi);
+          if ((gi & 31) == 0) {
+            qsa[gi >> 5] = qscale;
+            qsum[gi >> 5] = qs;
+          }
         }
       }
     }
@@ -1226,7 +1237,8 @@ int launch_prefill_blk(const float* q, const float* k, const float* v, size_t se
                        size_t n_kv_heads, float* out, const ActQuant* aq, bool* quantized, hipStream_t s) {
   const bool fuse_q = aq && aq->q;
   if (quantized) *quantized = fuse_q;
-  const dim3 grid(n_heads, (seq + kPbQ - 1) / kPbQ);
+  const size_t nqb = (seq + kPbQ - 1) / kPbQ;
+  const dim3 grid(n_heads, (nqb + 1) / 2);  // a pair of query blocks per workgroup
   int8_t* qd = fuse_q ? aq->q : nullptr;
   float* qsa = fuse_q ? aq->sa : nullptr;
   int* qsum = fuse_q ? aq->sums : nullptr;
