@@ -94,6 +94,10 @@ int prana_mat_info(prana_mat_t m, size_t *rows, size_t *cols, int *kind, size_t 
  * q[n_rows*k] i8, scales/sums[n_rows*k/32]. */
 int prana_quantize_acts(const float *x, size_t n_rows, size_t k, int8_t *q, float *scales, int32_t *sums,
                         prana_stream_t stream);
+/* quantize_q8 (matmul.rs:61-84): a dense f32 weight matrix w[rows*cols]
+ * (cols % 32 == 0) to Q8, q[rows*cols] i8 and scales[rows*cols/32] f32 (the
+ * parts prana_mat_create_q8 takes, host copies). */
+int prana_quantize_q8(const float *w, size_t rows, size_t cols, int8_t *q, float *scales, prana_stream_t stream);
 /* Linear::apply for n_tokens rows (checkpoint.rs:94-100): matmul_f32
  * (matmul.rs:150-157) / matmul_q8_f32 (162-178) / matmul_kquant_f32
  * (kquant.rs:323-333). x[n_tokens*cols] -> out[n_tokens*rows]. Quantizes the
@@ -113,7 +117,8 @@ int prana_matmul_block_sums(prana_mat_t w, const int8_t *q, const int32_t *sums,
  * scale when scale != 1 (infer.rs:155-159). out[n*cols]. */
 int prana_embed_rows(prana_mat_t table, const uint32_t *tokens, size_t n, float scale, float *out,
                      prana_stream_t stream);
-/* rmsnorm (norms.rs:9-23), rows x dim, dim <= 16320. */
+/* rmsnorm (norms.rs:9-23), rows x dim (rows wider than 16320 values read from
+ * global memory instead of LDS, slower; dim < 2^31 - 4096). */
 int prana_rmsnorm(const float *x, const float *w, size_t rows, size_t dim, float eps, float *out,
                   prana_stream_t stream);
 /* silu in place (norms.rs:27-31); gelu_tanh in place (norms.rs:35-41). */

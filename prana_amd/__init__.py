@@ -172,6 +172,16 @@ def quantize_acts(x):
     return q.to_host(), s.to_host(), m.to_host()
 
 
+def quantize_q8(w):
+    """quantize_q8 (matmul.rs:61-84) of a dense f32 matrix: (q, scales)."""
+    w = np.ascontiguousarray(np.atleast_2d(w), np.float32)
+    rows, cols = w.shape
+    dw = DeviceArray.from_host(w)
+    q, s = DeviceArray((rows, cols), np.int8), DeviceArray((rows, cols // 32), np.float32)
+    check(load().prana_quantize_q8(dw.ptr, rows, cols, q.ptr, s.ptr, None))
+    return q.to_host(), s.to_host()
+
+
 def rmsnorm(x, w, eps):
     x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
     rows, dim = x.shape

@@ -64,6 +64,7 @@ _SIGS = {
     "prana_mat_destroy": (c_int, [c_void_p]),
     "prana_mat_info": (c_int, [c_void_p, C.POINTER(c_size), C.POINTER(c_size), C.POINTER(c_int), C.POINTER(c_size)]),
     "prana_quantize_acts": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "prana_quantize_q8": (c_int, [c_void_p, c_size, c_size, c_void_p, c_void_p, c_void_p]),
     "prana_matmul": (c_int, [c_void_p, c_void_p, c_size, c_void_p, c_void_p]),
     "prana_matmul_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p]),
     "prana_matmul_block_sums": (c_int, [c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p]),

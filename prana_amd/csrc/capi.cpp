@@ -200,6 +200,16 @@ int prana_quantize_acts(const float* x, size_t n_rows, size_t k, int8_t* q, floa
   });
 }
 
+int prana_quantize_q8(const float* w, size_t rows, size_t cols, int8_t* q, float* scales, prana_stream_t stream) {
+  return guard([&] {
+    INIT_OR_RETURN();
+    PRANA_CHECK(w && q && scales, "quantize_q8: null argument");
+    PRANA_CHECK(cols % 32 == 0, "quantize_q8: cols must be a multiple of 32 (matmul.rs:63)");
+    // the same per-block arithmetic as quantize_acts (matmul.rs:67-80 and 108-121), without the sums
+    return launch_quantize_acts(w, rows, cols, q, scales, nullptr, pick_stream(stream));
+  });
+}
+
 int prana_matmul(prana_mat_t w, const float* x, size_t n_tokens, float* out, prana_stream_t stream) {
   return guard([&] {
     INIT_OR_RETURN();

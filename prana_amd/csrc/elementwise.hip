@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void quantize_acts_kernel(const float* __restr
     q[gid] = static_cast<int8_t>(qi);
     if ((threadIdx.x & 31) == 0) {
       sa[blk] = scale;
-      sums[blk] = sum;
+      if (sums) sums[blk] = sum;  // (quantize_q8 has none)
     }
   }
 }
@@ -200,11 +200,77 @@ __global__ __launch_bounds__(kNormNT) void rmsnorm_kernel(const float* __restric
   }
 }
 
+// Rows wider than kNormMaxDim (no limit in norms.rs:9-23): the same
+// arithmetic with the row read from global memory instead of LDS. The sum of
+// squares is the exact left-to-right fold (the predicted-binade scan up to
+// kPredHead + 1024 * kPredMaxPerLane terms, one lane's chain beyond that);
+// each lane reads an element before it writes it, so out may be x.
+__global__ __launch_bounds__(1024) void rmsnorm_wide_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            int dim, float eps, float* __restrict__ out,
+                                                            int8_t* __restrict__ q, float* __restrict__ sa,
+                                                            int* __restrict__ sums) {
+  constexpr int NT = 1024;
+  const float* row = x + (size_t)blockIdx.x * dim;
+  const int tid = threadIdx.x;
+  auto sq = [row](int i) {
+    const float v = row[i];
+    return v * v;
+  };
+  float ss;
+  if (dim <= exact::kPredHead + NT * exact::kPredMaxPerLane) {
+    ss = exact::block_seq_sum_short<NT>(sq, dim);
+  } else {
+    __shared__ float s_ss;
+    if (tid == 0) {
+      float a = -0.0f;
+      for (int i = 0; i < dim; i++) a += sq(i);
+      s_ss = a;
+    }
+    __syncthreads();
+    ss = s_ss;
+  }
+  const float mean_sq = ss / static_cast<float>(dim);
+  const float inv = 1.0f / sqrtf(mean_sq + eps);
+  // four elements per lane at a time; with q, dim % 32 == 0, so every 32-lane
+  // group is all live or all past the end and reduces together
+  for (int base = 0; base < dim; base += 4 * NT) {
+    float y[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int i = base + b * NT + tid;
+      y[b] = i < dim ? row[i] * inv * w[i] : 0.0f;
+      if (i < dim && out) out[(size_t)blockIdx.x * dim + i] = y[b];
+    }
+    if (q) {
+      float scale[4];
+      int qi[4], sum[4];
+      quantize_lanes<4>(y, qi, scale, sum);
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int i = base + b * NT + tid;
+        if (i < dim) {
+          const size_t gi = (size_t)blockIdx.x * dim + i;
+          q[gi] = static_cast<int8_t>(qi[b]);
+          if ((i & 31) == 0) {
+            sa[gi >> 5] = scale[b];
+            sums[gi >> 5] = sum[b];
+          }
+        }
+      }
+    }
+  }
+}
+
 int launch_rmsnorm(const float* x, const float* w, size_t rows, size_t dim, float eps, float* out, int8_t* q,
                    float* sa, int* sums, hipStream_t s) {
   if (rows == 0) return kOk;
   PRANA_CHECK(!q || dim % 32 == 0, "rmsnorm: fused quantize needs dim % 32 == 0");
-  PRANA_CHECK(dim >= 1 && dim <= static_cast<size_t>(kNormMaxDim), "rmsnorm: dim must be in 1..=16320");
+  PRANA_CHECK(dim >= 1 && dim <= static_cast<size_t>(INT32_MAX) - 4096, "rmsnorm: dim must be in 1..2^31-4097");
+  if (dim > static_cast<size_t>(kNormMaxDim)) {  // the row does not fit LDS: read it from global memory
+    hipLaunchKernelGGL(rmsnorm_wide_kernel, dim3(rows), dim3(1024), 0, s, x, w, (int)dim, eps, out, q, sa, sums);
+    PRANA_LAUNCH_CHECK();
+    return kOk;
+  }
   const size_t lds = (exact::run_pad(static_cast<int>(dim)) + dim) * 4;
   if (dim <= static_cast<size_t>(kNormSmallDim) || (rows > kNormBatchRows && dim <= 16 * 256))
     hipLaunchKernelGGL(rmsnorm_kernel<256>, dim3(rows), dim3(256), lds, s, x, w, (int)dim, eps, out, q, sa, sums);

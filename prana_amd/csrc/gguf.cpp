@@ -141,8 +141,8 @@ void dq_q6k(const uint8_t* b, float* y) {
 }
 
 // quantize_q8 (matmul.rs:61-84): per 32-block scale = amax/127 (1.0 for a
-// zero block), q = clamp(round(x * (1/scale)), -127, 127), rounding half away
-// from zero.
+// zero block; NaN elements do not count toward amax), q = clamp(round(x *
+// (1/scale)), -127, 127), rounding half away from zero, NaN to 0.
 void quantize_q8_host(size_t rows, size_t cols, const float* w, std::vector<int8_t>& q, std::vector<float>& sc) {
   const size_t G = cols / 32;
   q.resize(rows * cols);
@@ -155,8 +155,8 @@ void quantize_q8_host(size_t rows, size_t cols, const float* w, std::vector<int8
       const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
       const float inv = 1.0f / scale;
       for (int i = 0; i < 32; i++) {
-        const float v = std::fmin(std::fmax(std::round(x[i] * inv), -127.0f), 127.0f);
-        q[r * cols + g * 32 + i] = static_cast<int8_t>(v);
+        const float v = std::round(x[i] * inv);  // a NaN casts to 0 (Rust's saturating `as i8`)
+        q[r * cols + g * 32 + i] = v != v ? 0 : static_cast<int8_t>(v < -127.0f ? -127.0f : v > 127.0f ? 127.0f : v);
       }
       sc[r * G + g] = scale;
     }

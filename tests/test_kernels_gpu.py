@@ -236,7 +236,7 @@ def _adversarial_rows(dim, seed):
     return np.stack(rows)
 
 
-@pytest.mark.parametrize("dim", [32, 288, 512, 544, 1000, 3072, 4096, 4128, 14336, 16320])
+@pytest.mark.parametrize("dim", [32, 288, 512, 544, 1000, 3072, 4096, 4128, 14336, 16320, 16384, 20000])
 def test_rmsnorm_adversarial(dim):
     x = _adversarial_rows(dim, dim)
     w = np.ones(dim, np.float32)
@@ -287,6 +287,35 @@ def test_rmsnorm_batches_beyond_256_rows(dim):
     got, want = P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5)
     for i in range(x.shape[0]):
         assert same_bits(got[i], want[i]), i
+
+
+@pytest.mark.parametrize("dim", [16352, 16384, 49152, 70000])
+def test_rmsnorm_rows_wider_than_lds(dim):
+    # rows past 16320 values are read from global memory: the exact sum by
+    # the predicted-binade scan up to 32 + 1024 * 64 terms, one lane's chain
+    # beyond (70000); dense and scaled rows, bit-exact
+    r = rng(dim + 5)
+    x = np.stack([r.standard_normal(dim), r.standard_normal(dim) * np.exp(r.standard_normal(dim)),
+                  np.round(r.standard_normal(dim) * 8)]).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(dim)).astype(np.float32)
+    got, want = P.rmsnorm(x, w, 1e-5), O.rmsnorm(x, w, 1e-5)
+    for i in range(x.shape[0]):
+        assert same_bits(got[i], want[i]), i
+
+
+def test_quantize_q8_matches_the_oracle():
+    # quantize_q8 (matmul.rs:61-84): a zero block (scale 1), a tiny block, ties
+    # at .5 after the scaling, NaN (quantized to 0) and inf in a block
+    r = rng(61)
+    w = (r.standard_normal((37, 512)) * 3).astype(np.float32)
+    w[0, :32] = 0.0
+    w[1, 32:64] *= 1e-30
+    w[2, 64:96] = (np.arange(32) - 15.5).astype(np.float32) * (127.0 / 15.5)
+    w[3, 5] = np.nan
+    w[4, 40] = np.inf
+    q, s = P.quantize_q8(w)
+    qo, so = O.quantize_q8(w)
+    assert np.array_equal(q, qo) and same_bits(s, so)
 
 
 def test_sequential_order_closed_forms_on_device():
