@@ -31,6 +31,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# prana_gemv_profile_shapes entry of the decode attention launch (no GEMV streams 1 byte)
+ATTENTION_PROFILE_KEY = 1
 
 
 def log(msg):
@@ -142,8 +144,13 @@ def main():
              2 * q4(hid, d): ("gate|up + SiLU + FFN rmsnorm", cfg["n_layers"]),
              q4(d, hid): ("down", cfg["n_layers"]),
              q4(voc, d): ("LM head", 1)}
-    per = []
+    per, attn = [], None
     for b, n, sec in shapes:
+        if b == ATTENTION_PROFILE_KEY:  # the one-launch decode attention kernel, sampled in the same rotation
+            us = sec / max(n, 1) * 1e6
+            attn = {"launches": n, "avg_us": round(us, 3), "per_token": cfg["n_layers"],
+                    "us_per_token": round(us * cfg["n_layers"], 1)}
+            continue
         name, per_tok = names.get(b, (f"{b} bytes", 0))
         us = sec / max(n, 1) * 1e6
         gbs = b / (sec / n) / 1e9 if sec > 0 else 0.0
@@ -153,6 +160,18 @@ def main():
     dom = max(per, key=lambda r: r["us_per_token"]) if per else None
     for r in per:
         log(f"  {r['name']:<30} {r['avg_us']:8.2f} us  {r['gbs']:8.1f} GB/s  ({r['frac'] * 100:.1f} %)")
+    # A decode token split into sections: each projection's launches and the
+    # attention launches (the norms run inside the Q|K|V and gate|up launches).
+    # Dispatch-timestamp durations include each dispatch's start, which
+    # back-to-back launches overlap, so their sum can exceed the token time.
+    tok_us = dt_plain / K * 1e6
+    sections = {r["name"]: r["us_per_token"] for r in per if r["per_token"]}
+    if attn is not None:
+        sections["attention (score, softmax, PV, wo input quantization)"] = attn["us_per_token"]
+        log(f"  {'attention':<30} {attn['avg_us']:8.2f} us x {attn['per_token']} per token")
+    decode_sections = {"token_us": round(tok_us, 1), "sampled_us_per_token": sections,
+                       "sampled_sum_us": round(sum(sections.values()), 1)}
+    log(f"per-token sections (us, token {tok_us:.1f}): " + ", ".join(f"{k}: {v}" for k, v in sections.items()))
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "q4_0_gemv_7b_decode_traffic.json")
@@ -238,6 +257,8 @@ def main():
             "decode_weight_stream_gbs": round(stream_bytes * tok_s / 1e9, 2),
             "prefill_tok_s": round((npre - 1) / prefill_s, 2),
             "tok_s_without_events": round(K / dt_plain, 3),
+            "decode_sections": decode_sections,
+            "attention_launch": attn,
             "parity": match if match is not None else "not checked (--no-cpu)",
         },
         "roofline": {

@@ -260,8 +260,13 @@ int prana_gemv_profile_read(size_t *launches, double *seconds, double *bytes, in
 /* The same timed launches split by shape: one entry per distinct weight-byte
  * count streamed by a launch (which tells the projections apart), in
  * ascending byte order; up to cap entries are written and *n_out gets the
- * number of shapes. Cleared by prana_gemv_profile_read with reset set.
- * No counterpart in the reference (a measurement hook for the benchmark). */
+ * number of shapes. Entry 1 (bytes = 1) is the decode attention launch (the
+ * one-launch kernel, which also quantizes its output for wo), sampled in the
+ * same rotation and left out of prana_gemv_profile_read's GEMV totals; the
+ * norms of a decode step run inside the Q|K|V and gate|up launches. Cleared
+ * by prana_gemv_profile_read with reset set.
+ * No counterpart in the reference (a measurement hook for the benchmark; its
+ * PRANA_TIMING buckets, infer.rs:81-130, are these entries by projection). */
 int prana_gemv_profile_shapes(size_t cap, size_t *bytes, size_t *launches, double *seconds, size_t *n_out);
 
 typedef struct prana_gen_stats {

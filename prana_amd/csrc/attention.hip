@@ -11,6 +11,8 @@
 // slices and the heads of one KV group are placed on the same XCD) and then
 // folds its own dims; V rows of the slice stream through LDS in chunks that
 // are fetched with 16-byte loads one chunk ahead of the fold.
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 
 #include "common.h"
@@ -1408,9 +1410,18 @@ int launch_attn(const float* q, const void* k, const void* v, size_t pos0, const
   // fused quantization needs every workgroup's dims to be whole 32-blocks
   const bool fuse_q = aq && aq->q && (hd / ds) % 32 == 0;
   if (quantized) *quantized = fuse_q;
-  hipLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, q, k, v, (int)pos0, pos_dev,
-                     (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode,
-                     fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr, (int)kcap);
+  LaunchEvents& le = launch_events();
+  if (le.start) {  // a sampled decode launch: timestamps as part of the dispatch
+    hipExtLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, le.start, le.stop, 0, q, k, v,
+                          (int)pos0, pos_dev, (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch,
+                          (int)ctx_cap, mode, fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr,
+                          fuse_q ? aq->sums : nullptr, (int)kcap);
+    le = LaunchEvents{};
+  } else {
+    hipLaunchKernelGGL(attn_kernel<F16>, dim3(n_heads * ds, n_q), dim3(kNT), 0, s, q, k, v, (int)pos0, pos_dev,
+                       (int)n_heads, (int)(n_heads / n_kv_heads), (int)hd, ds, out, scratch, (int)ctx_cap, mode,
+                       fuse_q ? aq->q : nullptr, fuse_q ? aq->sa : nullptr, fuse_q ? aq->sums : nullptr, (int)kcap);
+  }
   PRANA_LAUNCH_CHECK();
   return kOk;
 }

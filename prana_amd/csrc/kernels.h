@@ -106,6 +106,9 @@ struct LaunchEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 LaunchEvents& launch_events();
+// The sampled launch profile's key of the one-launch decode attention kernel
+// (the GEMV launches are keyed by the weight bytes they stream).
+constexpr size_t kProfileAttentionKey = 1;
 
 // out[t*ldo + r] (mode): 0 = store, 1 = store + bias[r], 2 = out += result
 // (the residual add x += o of infer.rs:186-188, 201-203).

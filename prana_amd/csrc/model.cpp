@@ -407,9 +407,11 @@ int GemvProfile::collect() {
     PRANA_HIP(hipEventSynchronize(pool[r.ev + 1]));
     float ms = 0.0f;
     PRANA_HIP(hipEventElapsedTime(&ms, pool[r.ev], pool[r.ev + 1]));
-    launches += 1;
-    seconds += ms * 1e-3;
-    bytes += static_cast<double>(r.bytes);
+    if (r.bytes != kProfileAttentionKey) {  // the GEMV totals
+      launches += 1;
+      seconds += ms * 1e-3;
+      bytes += static_cast<double>(r.bytes);
+    }
     Shape& sh = shapes[r.bytes];
     sh.launches += 1;
     sh.seconds += ms * 1e-3;
@@ -599,9 +601,11 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
       if (!roped && (rc = launch_rope_kv(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), q_dim, kv_dim, hd,
                                          tab, c.rope_neox, kc, vc, cache.kcap, pos_dev, pos0, s)))
         return rc;
-      if ((rc = launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
-                                       ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, pos_dev, s, &aq,
-                                       &quantized, cache.kcap)))
+      if ((rc = timed(kProfileAttentionKey, 1, s, [&] {
+             return launch_attention_cache(ws.q.as<float>(), kc, vc, pos0, 1, c.n_heads, c.n_kv_heads, hd,
+                                           ws.attn.as<float>(), ws.scratch.as<float>(), cache.len, pos_dev, s, &aq,
+                                           &quantized, cache.kcap);
+           })))
         return rc;
     } else {
       if ((rc = launch_rope_kv_rows(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, q_dim, kv_dim, hd, tab,

@@ -415,7 +415,8 @@ def test_c4_speculative_equals_plain_greedy(c4, k):
 def test_gemv_profile_shapes_add_up():
     # prana_gemv_profile_shapes splits the sampled decode GEMV launches by the
     # weight bytes they stream; the split adds up to prana_gemv_profile_read's
-    # totals, and a reset clears it.
+    # totals, and a reset clears it. Entry 1 holds the decode attention
+    # launches (one per layer and step at this context), outside the totals.
     cfg = M.config(2048, 1024, 2, 32, 4, 500, 64, head_dim=64, rope_neox=1)
     g = P.Model(cfg, M.synth_tensors(cfg, lambda name, cols: M.Q4_0, 77))
     c = g.cache(32)
@@ -429,6 +430,9 @@ def test_gemv_profile_shapes_add_up():
     shapes = P.gemv_profile_shapes()
     n, sec, total_bytes = P.gemv_profile_read(reset=True)
     P.gemv_profile(False)
+    attn = [(k, t) for b, k, t in shapes if b == 1]
+    assert len(attn) == 1 and attn[0][0] == 4 * cfg["n_layers"] and attn[0][1] > 0
+    shapes = [r for r in shapes if r[0] != 1]
     assert n > 0 and sum(k for _, k, _ in shapes) == n
     assert sum(b * k for b, k, _ in shapes) == total_bytes
     assert abs(sum(t for _, _, t in shapes) - sec) <= 1e-9 * max(sec, 1.0)
