@@ -1874,11 +1874,18 @@ struct MmaLayout {
   static_assert(WP % 256 == 0 && AP % 256 == 0 && DPL * 256 == kMmaRows * CB, "whole pieces per lane");
 };
 
+// A block scale as loaded into a staging register: f32 bits for Q8F, else
+// the f16 bits. Held at their loaded width, so nothing touches the loaded
+// value before the register set is stored to LDS (a widening of a 16-bit
+// load there makes the compiler wait for every load in flight).
+template <int KIND>
+using ScaleReg = typename std::conditional<KIND == kKindQ8F, uint32_t, uint16_t>::type;
+
 template <int KIND>
 struct MmaRegs {
   using L = MmaLayout<KIND>;
   sk_i4 w[L::WPL], a[L::APL];
-  uint32_t d[L::DPL];
+  ScaleReg<KIND> d[L::DPL];
   float sa[L::SPL];
 };
 
@@ -1948,8 +1955,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MmaJob job, const int8_t
     for (int i = 0; i < L::DPL; i++) {
       const int p = tid + 256 * i;
       const size_t gi = (size_t)tile_row(p / L::CB) * G + min(cb0 + p % L::CB, G - 1);
-      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(tile_sc(p / L::CB))[gi]
-                                : reinterpret_cast<const uint16_t*>(tile_sc(p / L::CB))[gi];
+      if constexpr (KIND == kKindQ8F) r.d[i] = reinterpret_cast<const uint32_t*>(tile_sc(p / L::CB))[gi];
+      else r.d[i] = reinterpret_cast<const uint16_t*>(tile_sc(p / L::CB))[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
@@ -2228,16 +2235,25 @@ template <int KIND, int RW, int TT>
 struct SkRegs {
   using L = SkLayout<KIND, RW, TT>;
   sk_i4 w[L::WPL], a[L::APL];
-  uint32_t d[L::DPL];
+  ScaleReg<KIND> d[L::DPL];
   float sa[L::SPL];
   int sm[L::SPL];
 };
 
+// Up to three matrices of one block-32 kind and width over the same
+// activations (gate|up, Q|K|V) in one launch: workgroups t0[i].. take the row
+// tiles of matrix i, so two 14336-row matrices fill the chip with 64-row tiles
+// where each alone would leave CUs idle or need 32-row tiles.
+struct SkJob {
+  DevMat m[3];
+  GemvOut o[3];
+  int t0[3];  // first workgroup of matrix i (t0[0] = 0; unused entries INT32_MAX)
+};
+
 template <int KIND, int RW, int TT>
-__global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, const int8_t* __restrict__ q,
+__global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, const int8_t* __restrict__ q,
                                                                    const float* __restrict__ sa,
-                                                                   const int* __restrict__ sums, int n_tok,
-                                                                   GemvOut o) {
+                                                                   const int* __restrict__ sums, int n_tok) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
   using L = SkLayout<KIND, RW, TT>;
   extern __shared__ int4 sk_smem[];
@@ -2245,8 +2261,12 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rtile = wave % RW, ttile = wave / RW;
   const int j = lane & 15, kg = lane >> 4;
+  const int bx = static_cast<int>(blockIdx.x);
+  const int mi = (bx >= job.t0[1]) + (bx >= job.t0[2]);  // uniform
+  const DevMat m = mi == 0 ? job.m[0] : mi == 1 ? job.m[1] : job.m[2];
+  const GemvOut o = mi == 0 ? job.o[0] : mi == 1 ? job.o[1] : job.o[2];
   const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
-  const int row0 = static_cast<int>(blockIdx.x) * L::ROWS;
+  const int row0 = (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * L::ROWS;
   const int n_chunks = (G + kSkCB - 1) / kSkCB;
 
   auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
@@ -2271,8 +2291,8 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
     for (int i = 0; i < L::DPL; i++) {
       const int p = min(tid + L::NT * i, L::DP - 1);
       const size_t gi = (size_t)min(row0 + p / kSkCB, R - 1) * G + min(cb0 + p % kSkCB, G - 1);
-      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
-                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+      if constexpr (KIND == kKindQ8F) r.d[i] = reinterpret_cast<const uint32_t*>(m.sc)[gi];
+      else r.d[i] = reinterpret_cast<const uint16_t*>(m.sc)[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
@@ -2379,18 +2399,22 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(DevMat m, con
   }
 }
 
-// ---- one 16-row x 16-token tile per workgroup, blocks split over 4 waves
+// ---- one 16-row x 16-token tile per workgroup, blocks split over 8 waves
 // Below 8192 rows, 16-row workgroups of one wave per token tile leave most
 // SIMDs idle, and each wave walks its row tile's blocks alone. Here a
 // workgroup takes one 16-row x 16-token tile (grid: row tiles x token tiles;
 // a row tile's weights are read once per token tile, mostly from the caches
-// for matrices this small), and its 4 waves take
-// consecutive chunks of kSkCB blocks (wave w: chunk 4i + w), each staged in
+// for matrices this small), and its 8 waves take
+// consecutive chunks of kSkCB blocks (wave w: chunk 8i + w), each staged in
 // the wave's own LDS region and multiplied on the matrix cores as in
 // gemm_skinny_kernel; each block's term (d*sa)*float(isum) goes to LDS, and
-// lane (row, token) of the workgroup then adds the 4*kSkCB terms of its output
-// in block order: the same left-to-right fold as every other kernel.
-constexpr int kKsWaves = 4;
+// lane (row, token) of the first four waves then adds the 8*kSkCB terms of
+// its output in block order: the same left-to-right fold as every other
+// kernel. With one such workgroup per CU, the weight bytes in flight are
+// what bounds the stream (4 waves: 8 KB per CU, ~1.3 TB/s over the chip),
+// so the workgroup is as wide as the LDS allows. Tokens past n_tok load
+// nothing: their columns of the products are never stored.
+constexpr int kKsWaves = 8;
 
 template <int KIND>
 __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m, const int8_t* __restrict__ q,
@@ -2430,22 +2454,24 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
 #pragma unroll
     for (int i = 0; i < L::APL; i++) {
       const int p = min(lane + 64 * i, L::AP - 1);
-      const int t = min(tok0 + p / (2 * kSkCB), n_tok - 1), pr = p % (2 * kSkCB);
+      const int t = tok0 + p / (2 * kSkCB), pr = p % (2 * kSkCB);
       const int blk = min(cb0 + pr / 2, G - 1);
-      r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
+      r.a[i] = sk_i4{};
+      if (t < n_tok) r.a[i] = *reinterpret_cast<const sk_i4*>(q + (size_t)t * K + (size_t)blk * 32 + (pr & 1) * 16);
     }
 #pragma unroll
     for (int i = 0; i < L::DPL; i++) {
       const int p = min(lane + 64 * i, L::DP - 1);
       const size_t gi = (size_t)min(row0 + p / kSkCB, R - 1) * G + min(cb0 + p % kSkCB, G - 1);
-      r.d[i] = KIND == kKindQ8F ? reinterpret_cast<const uint32_t*>(m.sc)[gi]
-                                : reinterpret_cast<const uint16_t*>(m.sc)[gi];
+      if constexpr (KIND == kKindQ8F) r.d[i] = reinterpret_cast<const uint32_t*>(m.sc)[gi];
+      else r.d[i] = reinterpret_cast<const uint16_t*>(m.sc)[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
       const int p = min(lane + 64 * i, L::SP - 1);
-      const size_t gi = (size_t)min(tok0 + p / kSkCB, n_tok - 1) * G + min(cb0 + p % kSkCB, G - 1);
-      r.sa[i] = sa[gi];
+      const int t = tok0 + p / kSkCB;
+      r.sa[i] = 0.0f;
+      if (t < n_tok) r.sa[i] = sa[(size_t)t * G + min(cb0 + p % kSkCB, G - 1)];
     }
     return r;
   };
@@ -2500,7 +2526,8 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
     }
   };
 
-  const int fr = tid & 15, ft = tid >> 4;  // the output this lane folds: row fr, token ft
+  const int fr = tid & 15, ft = (tid >> 4) & 15;  // the output this lane folds: row fr, token ft
+  const bool folder = tid < 256;                  // (uniform per wave)
   const float* tf = terms + (ft + (ft >> 2)) * 16 + fr;
   float acc = 0.0f;
   // a chunk at or past n_chunks holds clamped (repeated) blocks, never folded
@@ -2512,7 +2539,8 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
     products();
     __syncthreads();  // terms visible
     const int nb = min(kKsWaves * kSkCB, G - c0 * kSkCB);  // uniform: live blocks of this group
-    if (nb == kKsWaves * kSkCB) {
+    if (!folder) {
+    } else if (nb == kKsWaves * kSkCB) {
       // whole group: every read issued before the adds
       float t[kKsWaves * kSkCB];
 #pragma unroll
@@ -2524,7 +2552,7 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
     }
   }
   const int n_row = row0 + fr;
-  if (n_row < R && tok0 + ft < n_tok) store_out(o, tok0 + ft, n_row, acc);
+  if (folder && n_row < R && tok0 + ft < n_tok) store_out(o, tok0 + ft, n_row, acc);
 }
 
 template <int KIND>
@@ -2532,6 +2560,7 @@ int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const in
                      const GemvOut& o, hipStream_t s) {
   using L = SkLayout<KIND, 1, 1>;
   constexpr int kBytes = kKsWaves * L::SM_OFF + kKsWaves * kSkCB * 20 * 16 * 4;
+  static_assert(kBytes <= 160 * 1024, "one workgroup's staging and terms fit a CU's LDS");
   static const bool attr_ok = [] {
     return kBytes <= 65536 ||
            set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND>), kBytes);
@@ -2544,41 +2573,73 @@ int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const in
 }
 
 template <int KIND, int RW, int TT>
-int launch_skinny_t(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
-                    const GemvOut& o, hipStream_t s) {
+int launch_skinny_t(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa,
+                    const int* sums, size_t n_tok, hipStream_t s) {
   using L = SkLayout<KIND, RW, TT>;
   static const bool attr_ok = [] {
     return L::BYTES * 2 <= 65536 ||
            set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_kernel<KIND, RW, TT>), L::BYTES * 2);
   }();
   PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
-  hipLaunchKernelGGL((gemm_skinny_kernel<KIND, RW, TT>), dim3((m.rows + L::ROWS - 1) / L::ROWS), dim3(L::NT),
-                     L::BYTES * 2, s, m, q, sa, sums, (int)n_tok, o);
+  SkJob job{};
+  size_t tiles = 0;
+  for (int i = 0; i < 3; i++) {
+    job.t0[i] = i < n_mats ? static_cast<int>(tiles) : INT32_MAX;
+    job.m[i] = ms[i < n_mats ? i : 0];
+    job.o[i] = os[i < n_mats ? i : 0];
+    if (i < n_mats) tiles += (ms[i].rows + L::ROWS - 1) / L::ROWS;
+  }
+  PRANA_CHECK(tiles <= static_cast<size_t>(INT32_MAX), "gemm_skinny: too many row tiles");
+  hipLaunchKernelGGL((gemm_skinny_kernel<KIND, RW, TT>), dim3(tiles), dim3(L::NT), L::BYTES * 2, s, job, q, sa,
+                     sums, (int)n_tok);
   PRANA_LAUNCH_CHECK();
   return kOk;
 }
 
 template <int KIND, int TT>
-int launch_skinny_tt(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
-                     const GemvOut& o, hipStream_t s) {
-  // rows per workgroup: grow while at least 256 workgroups remain (bigger
-  // tiles share each staged activation chunk among more rows); below 8192
-  // rows the block-split kernel takes the matrix instead
+int launch_skinny_tt(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa,
+                     const int* sums, size_t n_tok, hipStream_t s) {
+  // rows per workgroup: grow while at least 256 workgroups remain over all
+  // the matrices (bigger tiles share each staged activation chunk among more
+  // rows); where even 32-row tiles leave fewer, each matrix goes to the
+  // block-split kernel instead
+  auto tiles = [&](size_t rows_per_tile) {
+    size_t t = 0;
+    for (int i = 0; i < n_mats; i++) t += (ms[i].rows + rows_per_tile - 1) / rows_per_tile;
+    return t;
+  };
   int rw = 1;
-  while (rw < 4 && (m.rows + 32 * rw - 1) / (32 * rw) >= 256) rw *= 2;
-  if (rw == 1) return launch_skinny_ks<KIND>(m, q, sa, sums, n_tok, o, s);
-  if (rw == 2) return launch_skinny_t<KIND, 2, TT>(m, q, sa, sums, n_tok, o, s);
-  return launch_skinny_t<KIND, 4, TT>(m, q, sa, sums, n_tok, o, s);
+  while (rw < 4 && tiles(32 * rw) >= 256) rw *= 2;
+  if (rw == 1) {
+    for (int i = 0; i < n_mats; i++)
+      if (int rc = launch_skinny_ks<KIND>(ms[i], q, sa, sums, n_tok, os[i], s)) return rc;
+    return kOk;
+  }
+  if (rw == 2) return launch_skinny_t<KIND, 2, TT>(ms, os, n_mats, q, sa, sums, n_tok, s);
+  return launch_skinny_t<KIND, 4, TT>(ms, os, n_mats, q, sa, sums, n_tok, s);
 }
 
 template <int KIND>
-int launch_gemm_skinny(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
-                       const GemvOut& o, hipStream_t s) {
-  PRANA_CHECK(m.cols % 32 == 0 && m.cols <= (1u << 30) && m.rows <= (1u << 30) && n_tok >= 1 && n_tok <= 64,
-              "gemm_skinny: shape out of range");
-  if (n_tok <= 16) return launch_skinny_tt<KIND, 1>(m, q, sa, sums, n_tok, o, s);
-  if (n_tok <= 32) return launch_skinny_tt<KIND, 2>(m, q, sa, sums, n_tok, o, s);
-  return launch_skinny_tt<KIND, 4>(m, q, sa, sums, n_tok, o, s);
+int launch_gemm_skinny(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa,
+                       const int* sums, size_t n_tok, hipStream_t s) {
+  PRANA_CHECK(n_mats >= 1 && n_mats <= 3 && n_tok >= 1 && n_tok <= 64, "gemm_skinny: job out of range");
+  for (int i = 0; i < n_mats; i++)
+    PRANA_CHECK(ms[i].kind == KIND && ms[i].cols == ms[0].cols && ms[i].cols % 32 == 0 &&
+                    ms[i].cols <= (1u << 30) && ms[i].rows <= (1u << 30),
+                "gemm_skinny: shape out of range");
+  if (n_tok <= 16) return launch_skinny_tt<KIND, 1>(ms, os, n_mats, q, sa, sums, n_tok, s);
+  if (n_tok <= 32) return launch_skinny_tt<KIND, 2>(ms, os, n_mats, q, sa, sums, n_tok, s);
+  return launch_skinny_tt<KIND, 4>(ms, os, n_mats, q, sa, sums, n_tok, s);
+}
+
+int launch_gemm_skinny_any(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa,
+                           const int* sums, size_t n_tok, hipStream_t s) {
+  switch (ms[0].kind) {
+    case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(ms, os, n_mats, q, sa, sums, n_tok, s);
+    case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(ms, os, n_mats, q, sa, sums, n_tok, s);
+    case kKindQ4_0: return launch_gemm_skinny<kKindQ4_0>(ms, os, n_mats, q, sa, sums, n_tok, s);
+    default: return fail(kErrInvalid, "gemm_skinny: block-32 kinds only");
+  }
 }
 
 // ---- K-quant batches (Q4_K, Q6_K) on the 16x16x32 int8 matrix cores
@@ -2616,7 +2677,7 @@ template <int KIND, int RW, int TT>
 struct KqRegs {
   using L = KqLayout<KIND, RW, TT>;
   sk_i4 w[L::WPL], a[L::APL];
-  uint32_t d[L::DPL];
+  uint16_t d[L::DPL];  // Q6_K's f16 scale (0 for the other kinds)
   float sa[L::SPL];
   int sm[L::SPL];
 };
@@ -2665,7 +2726,7 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_kq_kernel(DevMat m, const i
     for (int i = 0; i < L::DPL; i++) {
       const int p = min(tid + L::NT * i, L::DP - 1);
       const size_t gi = (size_t)min(row0 + p / kKqCS, R - 1) * NB + min(sb0 + p % kKqCS, NB - 1);
-      r.d[i] = KIND == kKindQ6_K ? reinterpret_cast<const uint16_t*>(m.sc)[gi] : 0u;
+      r.d[i] = KIND == kKindQ6_K ? reinterpret_cast<const uint16_t*>(m.sc)[gi] : uint16_t{0};
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
@@ -2978,7 +3039,15 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
     }
   }
   bool per_matrix = ms[0].kind == kKindF32 || n_tok > kDecodeMaxTokens;
-  for (int i = 0; i < n; i++) per_matrix = per_matrix || gemv_batch_skinny(ms[i], n_tok);
+  bool skinny_all = one_kind, skinny_any = false;
+  for (int i = 0; i < n; i++) {
+    const bool sk = gemv_batch_skinny(ms[i], n_tok);
+    skinny_any = skinny_any || sk;
+    skinny_all = skinny_all && sk && ms[i].cols == ms[0].cols;
+  }
+  if (skinny_all && n_tok <= kDecodeMaxTokens)  // the matrices' row tiles in one skinny launch
+    return launch_gemm_skinny_any(ms, os, n, q, sa, sums, n_tok, s);
+  per_matrix = per_matrix || skinny_any;
   if (per_matrix) {
     for (int i = 0; i < n; i++) {
       int rc = launch_gemv(ms[i], nullptr, q, sa, sums, n_tok, os[i], s);
@@ -3114,9 +3183,10 @@ int launch_gemm_act(const DevMat& gate, const DevMat& up, const int8_t* q, const
 // always, from 3 tokens for matrices of at least kSkinnyMinBlocks blocks.
 // Its cost hardly grows with the batch up to 16 tokens (one 16-token tile),
 // while the decode tiles and the chunk-major verify kernel pay per token:
-// on the 7B Q4_0 shapes at 5 tokens, down 25.3 against 33.8 us, the head
-// 26.2 against 39.6 us; at 9 tokens wo 8.8 against 14.6 us; at 2 tokens
-// and for Q|K|V or wo up to 8 tokens the decode tiles stay ahead.
+// on the 7B Q4_0 shapes at 5 tokens, down 17.7 against 33.8 us, the head
+// 26.3 against 39.6 us, gate|up in one launch 25.7 against 40.1 us; at 9
+// tokens wo 6.6 against 14.6 us; at 2 tokens and for Q|K|V or wo up to 8
+// tokens the decode tiles stay ahead.
 constexpr size_t kSkinnyMinBlocks = 1536 * 1024;
 bool gemv_batch_skinny(const DevMat& m, size_t n_tok) {
   if (m.kind != kKindQ8F && m.kind != kKindQ8_0 && m.kind != kKindQ4_0) return false;
@@ -3129,9 +3199,9 @@ int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* s
   if (n_tok == 0 || m.rows == 0) return kOk;
   if (gemv_batch_skinny(m, n_tok)) {
     switch (m.kind) {
-      case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(m, q, sa, sums, n_tok, o, s);
-      case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(m, q, sa, sums, n_tok, o, s);
-      case kKindQ4_0: return launch_gemm_skinny<kKindQ4_0>(m, q, sa, sums, n_tok, o, s);
+      case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(&m, &o, 1, q, sa, sums, n_tok, s);
+      case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(&m, &o, 1, q, sa, sums, n_tok, s);
+      case kKindQ4_0: return launch_gemm_skinny<kKindQ4_0>(&m, &o, 1, q, sa, sums, n_tok, s);
     }
   }
   if (m.kind != kKindF32 && n_tok <= kDecodeMaxTokens) {

@@ -357,11 +357,12 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
 
 int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm, bool dense_h) {
   const size_t H = c.hidden_dim;
-  // from 9 tokens two skinny matrix-core launches and launch_act_mul (at 5
-  // tokens the fused launch and the quantization of h tie with them on the 7B
-  // gate|up: 40.1 + 5.1 against 2 x 20.6 + 4.7 us)
+  // where the skinny matrix-core kernel takes the batch (from 9 tokens, and
+  // from 3 for matrices as large as the 7B gate|up): both matrices' row tiles
+  // in one skinny launch, then launch_act_mul (at 5 tokens on the 7B gate|up
+  // the fused launch and the quantization of h take 40.1 + 5.1 us)
   const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens &&
-                    (n < kGemvSkinnyMinTokens || !gemv_batch_skinny(gate.d, n));
+                    !gemv_batch_skinny(gate.d, n);
   PRANA_CHECK(!norm || (fuse && n == 1), "apply_gate_up: a fused rmsnorm takes one token of fusable matrices");
   if (fuse) {
     return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {

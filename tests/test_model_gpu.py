@@ -278,10 +278,11 @@ def test_block32_verify_batches_bitexact(ty):
 @pytest.mark.parametrize("ty", [P.Q4_0, P.Q8_0])
 def test_large_verify_batches_on_matrix_cores_bitexact(ty):
     # Verify batches of 3..8 tokens over matrices of at least 1.5M blocks take
-    # the skinny matrix-core kernel: here down (4096 x 12288); gate|up stays
-    # one fused launch, the smaller Q|K|V and wo stay on the decode tiles. At
-    # 9 tokens every projection takes it, gate and up as two launches with
-    # SiLU and the quantization of h in launch_act_mul.
+    # the skinny matrix-core kernel: here down (4096 x 12288) and gate|up (both
+    # matrices' row tiles in one launch, then SiLU and the quantization of h
+    # in launch_act_mul); the smaller Q|K|V and wo stay on the decode tiles.
+    # At 9 tokens every projection takes it (Q|K|V and wo on the block-split
+    # form, too few row tiles for the one-launch form).
     cfg = M.config(4096, 12288, 1, 32, 8, 300, 48, head_dim=128)
     t = M.synth_tensors(cfg, lambda name, cols: ty, 13)
     g, o = pair(cfg, t)
@@ -293,6 +294,29 @@ def test_large_verify_batches_on_matrix_cores_bitexact(ty):
     for n in (3, 5, 8, 9):
         batch = [int(x) for x in prompt[pos:pos + n]]
         assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
+        pos += n
+
+
+@pytest.mark.parametrize("ty", [P.Q4_0, P.Q8_0])
+def test_verify_qkv_one_skinny_launch_bitexact(ty):
+    # Three matrices in one skinny launch: Q|K|V of 3 x 6144 rows (as many KV
+    # heads as query heads) fill the chip with 64-row tiles, so the launch
+    # deals workgroups 0..95 to Q, 96..191 to K and 192..287 to V. Batches of
+    # 9 and 16 tokens (one 16-token tile, a ragged and a full one).
+    cfg = M.config(6144, 1024, 1, 48, 48, 300, 40, head_dim=128)
+    t = M.synth_tensors(cfg, lambda name, cols: ty, 29)
+    g, o = pair(cfg, t)
+    gc, oc = g.cache(40), o.cache(40)
+    prompt = np.random.default_rng(29).integers(0, cfg["vocab_size"], 30).astype(np.uint32)
+    gc.prefill(prompt[:4])
+    oc.prefill(prompt[:4])
+    pos = 4
+    for n in (9, 16):
+        batch = [int(x) for x in prompt[pos:pos + n]]
+        assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
+        for layer in range(cfg["n_layers"]):
+            assert np.array_equal(gc.read(layer, 0, pos + n), oc.read(layer, 0, pos + n)), (n, layer)
+            assert np.array_equal(gc.read(layer, 1, pos + n), oc.read(layer, 1, pos + n)), (n, layer)
         pos += n
 
 
