@@ -1090,9 +1090,10 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
       if (folder) store_out(job.o[mi], fl_tok, r0 + fl_lr, acc);
       return;
     }
-    // q/k/v + bias, exchanged through LDS for the rotation pairs (n_tok == 1)
+    // q/k/v + bias, exchanged through LDS for the rotation pairs; token t of
+    // the batch sits at position pos + t
     __syncthreads();  // every fold read of the term buffers is done
-    float* xv = reinterpret_cast<float*>(sm8);
+    float* xv = reinterpret_cast<float*>(sm8) + fl_tok * ROWS;
     const GemvOut& o = job.o[mi];
     const size_t r = r0 + fl_lr;
     float val = 0.0f;
@@ -1103,10 +1104,11 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
     __syncthreads();
     if (folder) {
       const RopeKv& rk = job.rk;
-      const int pos = rk.pos_dev ? *rk.pos_dev : rk.pos;
+      const int pos = (rk.pos_dev ? *rk.pos_dev : rk.pos) + fl_tok;
       const size_t crow = (size_t)pos * rows_m + r;  // k and v have kv_dim = rows_m rows
+      float* out = o.out + (size_t)fl_tok * o.ldo;
       if (mi == 2) {
-        o.out[r] = val;
+        out[r] = val;
         rk.vc[crow] = f32_to_f16(val);
       } else {
         const int half = rk.hd / 2;
@@ -1125,7 +1127,7 @@ __device__ __forceinline__ void gemv_tile_body(const DecodeJob& job, const int8_
         float a = first ? val : xv[lp], b = first ? xv[lp] : val;
         rotate(a, b, rk.table[(size_t)pos * half + m]);
         const float y = first ? a : b;
-        o.out[r] = y;
+        out[r] = y;
         if (mi == 1) rk.kc[kcache_index(pos, r, rows_m, rk.kcap)] = f32_to_f16(y);
       }
     }
@@ -1577,6 +1579,7 @@ int launch_tile_u(const DecodeJob& job0, const TileGeom& g, const int8_t* q, con
     DecodeJob j = job;
     for (int i = 0; i < 3; i++)
       if (j.o[i].out) j.o[i].out += t0 * j.o[i].ldo;
+    j.rk.pos += static_cast<int>(t0);  // the group's first token (a batch's positions are on the host)
     if (ACT) {
       const size_t H = j.m[0].rows;
       if (j.h) j.h += t0 * H;
@@ -2244,17 +2247,28 @@ struct SkRegs {
 // activations (gate|up, Q|K|V) in one launch: workgroups t0[i].. take the row
 // tiles of matrix i, so two 14336-row matrices fill the chip with 64-row tiles
 // where each alone would leave CUs idle or need 32-row tiles.
+// Act form (gate|up): m[0] = gate, m[1] = up, equal shapes, rows % 32 == 0.
+// A workgroup stages 32 rows of each (its staged rows 0..31 are gate rows,
+// 32..63 the same up rows), so waves 0-1 fold gate and waves 2-3 up; the
+// epilogue forms h = act(g) * u (silu, or gelu_tanh) and quantizes each
+// token's 32-row block of h for down, as launch_act_mul does.
 struct SkJob {
   DevMat m[3];
   GemvOut o[3];
   int t0[3];  // first workgroup of matrix i (t0[0] = 0; unused entries INT32_MAX)
+  int gelu;   // act form: gelu_tanh instead of silu
+  float* h;   // act form: optional f32 h [n_tok][rows]
+  int8_t* hq;
+  float* hsa;
+  int* hsum;
 };
 
-template <int KIND, int RW, int TT>
+template <int KIND, int RW, int TT, bool ACT = false>
 __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, const int8_t* __restrict__ q,
                                                                    const float* __restrict__ sa,
                                                                    const int* __restrict__ sums, int n_tok) {
   static_assert(KIND == kKindQ4_0 || KIND == kKindQ8_0 || KIND == kKindQ8F, "block-32 kinds");
+  static_assert(!ACT || (RW == 4 && TT == 1), "the act form stages 32 rows of each matrix for one token tile");
   using L = SkLayout<KIND, RW, TT>;
   extern __shared__ int4 sk_smem[];
   uint8_t* lds = reinterpret_cast<uint8_t*>(sk_smem);
@@ -2262,11 +2276,15 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, co
   const int rtile = wave % RW, ttile = wave / RW;
   const int j = lane & 15, kg = lane >> 4;
   const int bx = static_cast<int>(blockIdx.x);
-  const int mi = (bx >= job.t0[1]) + (bx >= job.t0[2]);  // uniform
+  const int mi = ACT ? 0 : (bx >= job.t0[1]) + (bx >= job.t0[2]);  // uniform
   const DevMat m = mi == 0 ? job.m[0] : mi == 1 ? job.m[1] : job.m[2];
   const GemvOut o = mi == 0 ? job.o[0] : mi == 1 ? job.o[1] : job.o[2];
   const int K = static_cast<int>(m.cols), G = K / 32, R = static_cast<int>(m.rows);
-  const int row0 = (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * L::ROWS;
+  const int row0 = ACT ? bx * 32 : (bx - (mi == 0 ? 0 : mi == 1 ? job.t0[1] : job.t0[2])) * L::ROWS;
+  // staged row lr: its matrix row, and which matrix (the act form's rows 32..63 are up rows)
+  auto src_row = [&](int lr) { return min(row0 + (ACT ? (lr & 31) : lr), R - 1); };
+  auto src_qs = [&](int lr) { return ACT && lr >= 32 ? job.m[1].qs : m.qs; };
+  auto src_sc = [&](int lr) { return ACT && lr >= 32 ? job.m[1].sc : m.sc; };
   const int n_chunks = (G + kSkCB - 1) / kSkCB;
 
   auto load = [&](int c) __attribute__((always_inline)) {  // this lane's share of chunk c (clamped addresses)
@@ -2275,9 +2293,9 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, co
 #pragma unroll
     for (int i = 0; i < L::WPL; i++) {
       const int p = min(tid + L::NT * i, L::WP - 1);
-      const int rr = min(row0 + p / L::WPR, R - 1), pr = p % L::WPR;
+      const int lr = p / L::WPR, rr = src_row(lr), pr = p % L::WPR;
       const int blk = min(cb0 + pr / (L::QB / 16), G - 1);
-      const uint8_t* src = m.qs + (size_t)rr * G * L::QB + (size_t)blk * L::QB + (pr % (L::QB / 16)) * 16;
+      const uint8_t* src = src_qs(lr) + (size_t)rr * G * L::QB + (size_t)blk * L::QB + (pr % (L::QB / 16)) * 16;
       r.w[i] = *reinterpret_cast<const sk_i4*>(src);
     }
 #pragma unroll
@@ -2290,9 +2308,10 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, co
 #pragma unroll
     for (int i = 0; i < L::DPL; i++) {
       const int p = min(tid + L::NT * i, L::DP - 1);
-      const size_t gi = (size_t)min(row0 + p / kSkCB, R - 1) * G + min(cb0 + p % kSkCB, G - 1);
-      if constexpr (KIND == kKindQ8F) r.d[i] = reinterpret_cast<const uint32_t*>(m.sc)[gi];
-      else r.d[i] = reinterpret_cast<const uint16_t*>(m.sc)[gi];
+      const int lr = p / kSkCB;
+      const size_t gi = (size_t)src_row(lr) * G + min(cb0 + p % kSkCB, G - 1);
+      if constexpr (KIND == kKindQ8F) r.d[i] = reinterpret_cast<const uint32_t*>(src_sc(lr))[gi];
+      else r.d[i] = reinterpret_cast<const uint16_t*>(src_sc(lr))[gi];
     }
 #pragma unroll
     for (int i = 0; i < L::SPL; i++) {
@@ -2388,6 +2407,54 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, co
     if (c + 2 < n_chunks) store(r1, 0);
     if (c + 4 < n_chunks) r1 = load(c + 4);
     __syncthreads();
+  }
+  if constexpr (ACT) {
+    // the last chunk's barrier is behind: the staging buffers are free.
+    // s_x[t][row] holds the gate values, then h, of this workgroup's 32 rows.
+    constexpr int kXs = 33;  // padded row of 32 values per token
+    float* s_x = reinterpret_cast<float*>(lds);
+    const int lr = (rtile & 1) * 16 + j;  // row within the 32
+    if (rtile < 2) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) s_x[(4 * kg + v) * kXs + lr] = acc[v];
+    }
+    __syncthreads();
+    if (rtile >= 2) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        float g = s_x[(4 * kg + v) * kXs + lr];
+        if (job.gelu) {
+          const float kS = 0.7978846f;  // norms.rs:36
+          const float x3 = g * g * g;
+          g = 0.5f * g * (1.0f + dev_tanhf(kS * (g + 0.044715f * x3)));
+        } else {
+          g = g * (1.0f / (1.0f + dev_expf(-g)));
+        }
+        s_x[(4 * kg + v) * kXs + lr] = g * acc[v];
+      }
+    }
+    __syncthreads();
+    // half-wave g (tid / 32) takes tokens g and g + 8, one row per lane: one
+    // 32-row block of h per token for quantize_lanes
+    const int hr = tid & 31, tg = tid >> 5;
+    float hv[2] = {s_x[tg * kXs + hr], s_x[(tg + 8) * kXs + hr]};
+    int qv[2], sm[2];
+    float sc[2];
+    quantize_lanes<2>(hv, qv, sc, sm);
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int t = tg + 8 * b;
+      if (t < n_tok) {
+        const size_t gi = (size_t)t * R + row0 + hr;
+        job.hq[gi] = static_cast<int8_t>(qv[b]);
+        if (job.h) job.h[gi] = hv[b];
+        if (hr == 0) {
+          job.hsa[gi >> 5] = sc[b];
+          job.hsum[gi >> 5] = sm[b];
+        }
+      }
+    }
+    return;
   }
   const int n_row = row0 + rtile * 16 + j;
   if (n_row < R) {
@@ -2630,6 +2697,32 @@ int launch_gemm_skinny(const DevMat* ms, const GemvOut* os, int n_mats, const in
   if (n_tok <= 16) return launch_skinny_tt<KIND, 1>(ms, os, n_mats, q, sa, sums, n_tok, s);
   if (n_tok <= 32) return launch_skinny_tt<KIND, 2>(ms, os, n_mats, q, sa, sums, n_tok, s);
   return launch_skinny_tt<KIND, 4>(ms, os, n_mats, q, sa, sums, n_tok, s);
+}
+
+template <int KIND>
+int launch_skinny_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, const int* sums,
+                      size_t n_tok, int gelu, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s) {
+  using L = SkLayout<KIND, 4, 1>;
+  static const bool attr_ok = [] {
+    return L::BYTES * 2 <= 65536 ||
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_kernel<KIND, 4, 1, true>), L::BYTES * 2);
+  }();
+  PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
+  static_assert(16 * 33 * 4 <= 2 * L::BYTES, "the act epilogue's h rows fit the staging buffers");
+  SkJob job{};
+  job.m[0] = job.m[2] = gate;
+  job.m[1] = up;
+  job.t0[0] = 0;
+  job.t0[1] = job.t0[2] = INT32_MAX;
+  job.gelu = gelu;
+  job.h = h;
+  job.hq = hq;
+  job.hsa = hsa;
+  job.hsum = hsum;
+  hipLaunchKernelGGL((gemm_skinny_kernel<KIND, 4, 1, true>), dim3(gate.rows / 32), dim3(L::NT), L::BYTES * 2, s, job,
+                     q, sa, sums, (int)n_tok);
+  PRANA_LAUNCH_CHECK();
+  return kOk;
 }
 
 int launch_gemm_skinny_any(const DevMat* ms, const GemvOut* os, int n_mats, const int8_t* q, const float* sa,
@@ -2910,6 +3003,24 @@ int launch_isums_t(const DevMat& m, const int8_t* q, const int* sums, size_t n_t
 
 }  // namespace
 
+bool gemm_skinny_act_fusable(const DevMat& gate, const DevMat& up, size_t n_tok) {
+  const int k = gate.kind;
+  return (k == kKindQ8F || k == kKindQ8_0 || k == kKindQ4_0) && up.kind == k && gate.rows == up.rows &&
+         gate.cols == up.cols && gate.rows % 32 == 0 && gate.rows <= (1u << 30) && gate.cols % 32 == 0 &&
+         gate.cols <= (1u << 30) && n_tok >= 1 && n_tok <= 16 && gemv_batch_skinny(gate, n_tok);
+}
+
+int launch_gemm_skinny_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, const int* sums,
+                           size_t n_tok, int gelu, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s) {
+  PRANA_CHECK(gemm_skinny_act_fusable(gate, up, n_tok) && hq && hsa && hsum,
+              "gemm_skinny_act: gate and up must be equal block-32 matrices of rows % 32 == 0, 1..16 tokens");
+  switch (gate.kind) {
+    case kKindQ8F: return launch_skinny_act<kKindQ8F>(gate, up, q, sa, sums, n_tok, gelu, h, hq, hsa, hsum, s);
+    case kKindQ8_0: return launch_skinny_act<kKindQ8_0>(gate, up, q, sa, sums, n_tok, gelu, h, hq, hsa, hsum, s);
+    default: return launch_skinny_act<kKindQ4_0>(gate, up, q, sa, sums, n_tok, gelu, h, hq, hsa, hsum, s);
+  }
+}
+
 namespace {
 template <class F>
 int dispatch_kind(int kind, F&& f) {
@@ -3061,16 +3172,21 @@ int launch_gemv_multi(const DevMat* ms, const GemvOut* os, int n, const int8_t* 
     job.o[i] = os[i];
   }
   job.n_mats = n;
-  if (rk && n == 3 && n_tok == 1 && ms[1].rows == ms[2].rows && rk->hd > 0 && rk->hd % 2 == 0 &&
-      ms[0].rows % rk->hd == 0 && ms[1].rows % rk->hd == 0 && !os[0].residual && !os[1].residual &&
-      !os[2].residual) {
+  // (a batch's tokens go to positions pos..pos+n_tok-1, given on the host)
+  if (rk && n == 3 && (n_tok == 1 || (!rk->pos_dev && (rk->kcap == 0 || rk->pos + n_tok <= (size_t)rk->kcap))) &&
+      ms[1].rows == ms[2].rows && rk->hd > 0 && rk->hd % 2 == 0 && ms[0].rows % rk->hd == 0 &&
+      ms[1].rows % rk->hd == 0 && (rk->kcap == 0 || ms[1].rows % 8 == 0) && !os[0].residual && !os[1].residual && !os[2].residual) {
     // the tile must hold whole rotation pairs: even row counts (adjacent
     // pairs) or whole heads (NeoX pairs), in a single stage
+    // (batches that launch_decode_t gives the chunk-major kernel keep it and
+    // the separate RoPE launch)
     const bool ok = dispatch_kind(ms[0].kind, [&](auto k) {
       constexpr int KIND = decltype(k)::value;
       const TileGeom g = choose_geom<KIND>(ms[0].cols, false);
       const int nb = static_cast<int>(ms[0].cols / RegUnit<KIND>::kElems);
-      return static_cast<int>(g.sb >= nb && (rk->neox ? g.rt % rk->hd == 0 : g.rt % 2 == 0));
+      const bool km = RegUnit<KIND>::kElems == 32 && n_tok >= 2 &&
+                      (nb > 128 || n_tok > static_cast<size_t>(kDecMaxTok));
+      return static_cast<int>(!km && g.sb >= nb && (rk->neox ? g.rt % rk->hd == 0 : g.rt % 2 == 0));
     });
     if (ok) {
       job.rk = *rk;

@@ -143,6 +143,12 @@ bool gemv_batch_skinny(const DevMat& m, size_t n_tok);
 // h = act(g) * u (gelu: gelu_tanh, else silu) and quantizes it into
 // (hq, hsa, hsum), as launch_act_mul; h (optional) gets the f32 values.
 bool gemm_act_fusable(const DevMat& gate, const DevMat& up, size_t n_tok);
+// Verify batches (1..16 tokens) that the skinny matrix-core kernel takes:
+// gate|up, h = act(g) * u and h's quantization in one launch (equal
+// block-32 matrices, rows % 32 == 0); h (f32, [n_tok][rows]) is optional.
+bool gemm_skinny_act_fusable(const DevMat& gate, const DevMat& up, size_t n_tok);
+int launch_gemm_skinny_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, const int* sums,
+                           size_t n_tok, int gelu, float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
 int launch_gemm_act(const DevMat& gate, const DevMat& up, const int8_t* q, const float* sa, size_t n_tok, int gelu,
                     float* h, int8_t* hq, float* hsa, int* hsum, hipStream_t s);
 // Quantized kinds read (q, sa, sums) for n_tok rows; F32 reads x.

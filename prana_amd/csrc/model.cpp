@@ -358,9 +358,9 @@ int Model::apply_multi(const Mat* const* w, const GemvOut* o, int n_mats, size_t
 int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s, const NormIn* norm, bool dense_h) {
   const size_t H = c.hidden_dim;
   // where the skinny matrix-core kernel takes the batch (from 9 tokens, and
-  // from 3 for matrices as large as the 7B gate|up): both matrices' row tiles
-  // in one skinny launch, then launch_act_mul (at 5 tokens on the 7B gate|up
-  // the fused launch and the quantization of h take 40.1 + 5.1 us)
+  // from 3 for matrices as large as the 7B gate|up): one skinny launch that
+  // also forms and quantizes h (at 5 tokens on the 7B gate|up the fused
+  // decode-tile launch and the quantization of h take 40.1 + 5.1 us)
   const bool fuse = gate.d.kind != kKindF32 && gate.d.kind == up.d.kind && n <= kGemvDecodeMaxTokens &&
                     !gemv_batch_skinny(gate.d, n);
   PRANA_CHECK(!norm || (fuse && n == 1), "apply_gate_up: a fused rmsnorm takes one token of fusable matrices");
@@ -369,6 +369,13 @@ int Model::apply_gate_up(const Mat& gate, const Mat& up, size_t n, hipStream_t s
       return launch_gemv_act(gate.d, up.d, c.act, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n,
                              ws.gate.as<float>(), ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s,
                              norm);
+    });
+  }
+  if (gemm_skinny_act_fusable(gate.d, up.d, n)) {  // verify batches: the same, on the skinny kernel
+    float* h = dense_h ? ws.gate.as<float>() : nullptr;
+    return timed(gate.stream_bytes + up.stream_bytes, n, s, [&] {
+      return launch_gemm_skinny_act(gate.d, up.d, ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>(), n, c.act,
+                                    h, ws.hq.as<int8_t>(), ws.hsa.as<float>(), ws.hsum.as<int>(), s);
     });
   }
   if (gemm_act_fusable(gate.d, up.d, n)) {  // prefill: gate|up, the activation and h's quantization in one launch
@@ -587,13 +594,14 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
     GemvOut oq{ws.q.as<float>(), q_dim, L.has[kBq] ? L.vec[kBq].as<float>() : nullptr, 0};
     GemvOut ok{ws.k.as<float>(), kv_dim, L.has[kBk] ? L.vec[kBk].as<float>() : nullptr, 0};
     GemvOut ov{ws.v.as<float>(), kv_dim, L.has[kBv] ? L.vec[kBv].as<float>() : nullptr, 0};
-    bool roped = false;  // the decode Q|K|V launch also did RoPE and the cache rows
+    bool roped = false;  // the Q|K|V launch also did RoPE and the cache rows
     {
       const GemvOut o[3] = {oq, ok, ov};
-      const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), pos_dev, kc, vc,
-                      static_cast<int>(cache.kcap)};
-      if ((rc = apply_multi(wqkv, o, 3, n, ws.xb.as<float>(), s, mode == 0 ? &rk : nullptr, &roped,
-                            norm_fused ? &nin : nullptr)))
+      // decode reads its position from device memory; a batch's positions
+      // pos0..pos0+n-1 are known here
+      const RopeKv rk{tab, static_cast<int>(hd), c.rope_neox, static_cast<int>(pos0), mode == 0 ? pos_dev : nullptr,
+                      kc, vc, static_cast<int>(cache.kcap)};
+      if ((rc = apply_multi(wqkv, o, 3, n, ws.xb.as<float>(), s, &rk, &roped, norm_fused ? &nin : nullptr)))
         return rc;
     }
     const ActQuant aq{ws.qa.as<int8_t>(), ws.sa.as<float>(), ws.sums.as<int>()};
@@ -609,8 +617,8 @@ int Model::layers_pass(Cache& cache, size_t n, size_t pos0, int mode, hipStream_
            })))
         return rc;
     } else {
-      if ((rc = launch_rope_kv_rows(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, q_dim, kv_dim, hd, tab,
-                                    c.rope_neox, kc, vc, cache.kcap, pos0, s)))
+      if (!roped && (rc = launch_rope_kv_rows(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, q_dim, kv_dim,
+                                              hd, tab, c.rope_neox, kc, vc, cache.kcap, pos0, s)))
         return rc;
       if (mode == 1)
         rc = launch_attention_prefill(ws.q.as<float>(), ws.k.as<float>(), ws.v.as<float>(), n, c.n_heads,

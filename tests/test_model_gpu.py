@@ -275,16 +275,16 @@ def test_block32_verify_batches_bitexact(ty):
         assert same_bits(gc.forward_batch(batch, pos), oc.forward_batch(batch, pos)), n
 
 
-@pytest.mark.parametrize("ty", [P.Q4_0, P.Q8_0])
-def test_large_verify_batches_on_matrix_cores_bitexact(ty):
+@pytest.mark.parametrize("ty,act,dense_down", [(P.Q4_0, 0, False), (P.Q8_0, 0, False), (P.Q4_0, 1, True)])
+def test_large_verify_batches_on_matrix_cores_bitexact(ty, act, dense_down):
     # Verify batches of 3..8 tokens over matrices of at least 1.5M blocks take
-    # the skinny matrix-core kernel: here down (4096 x 12288) and gate|up (both
-    # matrices' row tiles in one launch, then SiLU and the quantization of h
-    # in launch_act_mul); the smaller Q|K|V and wo stay on the decode tiles.
-    # At 9 tokens every projection takes it (Q|K|V and wo on the block-split
-    # form, too few row tiles for the one-launch form).
-    cfg = M.config(4096, 12288, 1, 32, 8, 300, 48, head_dim=128)
-    t = M.synth_tensors(cfg, lambda name, cols: ty, 13)
+    # the skinny matrix-core kernel: here down (4096 x 12288) and gate|up (one
+    # launch that also forms h = act(g) * u, silu or gelu_tanh, quantizes it
+    # and, for a dense f32 down, writes the f32 h); the smaller Q|K|V and wo
+    # stay on the decode tiles. At 9 tokens every projection takes it (Q|K|V
+    # and wo on the block-split form, too few row tiles for the one-launch form).
+    cfg = M.config(4096, 12288, 1, 32, 8, 300, 48, head_dim=128, act=act)
+    t = M.synth_tensors(cfg, lambda name, cols: M.F32 if dense_down and "ffn_down" in name else ty, 13 + act)
     g, o = pair(cfg, t)
     gc, oc = g.cache(48), o.cache(48)
     prompt = np.random.default_rng(13).integers(0, cfg["vocab_size"], 40).astype(np.uint32)
