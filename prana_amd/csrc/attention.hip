@@ -287,14 +287,50 @@ __device__ __forceinline__ void one_head_body(const HeadJob& J, int vec_hd, cons
     for (int c = 0; c < n_chunks; c++) {
       const int t0 = c * ch, nr = min(ch, n - t0);
       if (folder) {
+        // groups of 32 rows in two register sets: the next group's reads are
+        // issued before this group's adds (the empty asm, consuming acc and
+        // ordering memory, keeps later reads from being hoisted further)
         const float* pr = L.prod + (c & 1) * kProdFloats + d * stride;
-        int i = 0;
+        const float4* p4 = reinterpret_cast<const float4*>(pr);
+        const int ng = nr / 32;
+        float4 x[8], y[8];
+        auto add8 = [&acc](const float4* z) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            acc += z[j].x;
+            acc += z[j].y;
+            acc += z[j].z;
+            acc += z[j].w;
+          }
+        };
+        if (ng > 0) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) x[j] = p4[j];
+        }
+        int g = 0;
+        for (; g + 1 < ng; g += 2) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) y[j] = p4[(g + 1) * 8 + j];
+          add8(x);
+          asm volatile("" ::"v"(acc) : "memory");
+          if (g + 2 < ng) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) x[j] = p4[(g + 2) * 8 + j];
+          }
+          add8(y);
+          asm volatile("" ::"v"(acc) : "memory");
+        }
+        if (g < ng) {
+          add8(x);
+          g++;
+        }
+        int i = 32 * g;
         for (; i + 4 <= nr; i += 4) {
-          const float4 x = *reinterpret_cast<const float4*>(pr + i);
-          acc += x.x;
-          acc += x.y;
-          acc += x.z;
-          acc += x.w;
+          const float4 z = p4[i / 4];
+          acc += z.x;
+          acc += z.y;
+          acc += z.z;
+          acc += z.w;
         }
         for (; i < nr; i++) acc += pr[i];
       }
