@@ -926,10 +926,11 @@ constexpr size_t kWideMinRows = 256;          // shorter windows stay on the one
 template <int HD>
 struct WideCfg {
   static constexpr int F = HD / 64;                 // fold waves
-  static constexpr int CH = HD == 128 ? 64 : 128;   // rows per PV chunk
+  static constexpr int CH = HD == 128 ? 128 : 256;  // rows per PV chunk
   static constexpr int PL = kWideNT - 64 * F;       // producer lanes
-  static constexpr int TASKS = CH / 4 * (HD / 2);   // (row quad, dim pair) per chunk
+  static constexpr int TASKS = CH / 4 * (HD / 8);   // (row quad, 8-dim piece) per chunk
   static constexpr int PER = (TASKS + PL - 1) / PL;
+  static constexpr int QS = HD + HD / 8;            // float4 words per row quad: a pad word after every 8 dims
   static constexpr int SC = exact::run_pad(kWideMax - 1) + 1;  // probability words
 };
 
@@ -944,7 +945,7 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   __shared__ __align__(16) float s_q[HD];
   __shared__ float s_red[kWideNT / 64];
   __shared__ __align__(16) float s_p[C::SC];
-  __shared__ __align__(16) float s_prod[2][C::CH * HD];
+  __shared__ __align__(16) float s_prod[2][C::CH / 4 * C::QS * 4];
   const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
   const int n = pos0 + i + 1;  // <= kWideMax rows
   const int kvh = h / group;
@@ -986,22 +987,26 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   __syncthreads();
 
   // ---- P·V: fold lanes (waves 0..F-1) own the head's dims; the others form
-  // the products of the next chunk as [row/4][dim][row%4]. Rows past n are
-  // zero products, which leave the fold (started from +0.0) unchanged.
+  // the products of the next chunk as [row/4][dim][row%4] (a pad word after
+  // every 8 dims, so that the producers' 16-byte stores of neighbouring
+  // pieces fall on different banks). A producer task is one row quad of one
+  // 8-dim piece: four 16-byte V loads (4-byte loads made the texture
+  // address unit the bound). Rows past n are zero products, which leave the
+  // fold (started from +0.0) unchanged.
   const bool folder = tid < 64 * C::F;
   const int pl = tid - 64 * C::F;
-  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(v + (size_t)kvh * HD);
-  const int kv_words = kv_stride / 2;
+  const uint16_t* vh = v + (size_t)kvh * HD;
   const int n_chunks = (n + C::CH - 1) / C::CH;
-  uint32_t vr[C::PER][4];
+  uint4 vr[C::PER][4];
   auto fetch = [&](int c) {
 #pragma unroll
     for (int kk = 0; kk < C::PER; kk++) {
       const int task = min(pl + C::PL * kk, C::TASKS - 1);
-      const int dp = task % (HD / 2), rq = task / (HD / 2);
+      const int pc = task % (HD / 8), rq = task / (HD / 8);
       const int t = c * C::CH + 4 * rq;
 #pragma unroll
-      for (int r = 0; r < 4; r++) vr[kk][r] = v32[(size_t)min(t + r, n - 1) * kv_words + dp];
+      for (int r = 0; r < 4; r++)
+        vr[kk][r] = *reinterpret_cast<const uint4*>(vh + (size_t)min(t + r, n - 1) * kv_stride + 8 * pc);
     }
   };
   auto produce = [&](int c, float* buf) {
@@ -1009,19 +1014,28 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
     for (int kk = 0; kk < C::PER; kk++) {
       const int task = pl + C::PL * kk;
       if (task >= C::TASKS) break;
-      const int dp = task % (HD / 2), rq = task / (HD / 2);
+      const int pc = task % (HD / 8), rq = task / (HD / 8);
       const int t = c * C::CH + 4 * rq;
-      float a[4], b[4];
+      float p[4];
+      bool live[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const bool live = t + r < n;
-        const float p = s_p[exact::run_pad(min(t + r, n - 1))];
-        a[r] = live ? p * f16_operand(static_cast<uint16_t>(vr[kk][r] & 0xffffu)) : 0.0f;
-        b[r] = live ? p * f16_operand(static_cast<uint16_t>(vr[kk][r] >> 16)) : 0.0f;
+        live[r] = t + r < n;
+        p[r] = s_p[exact::run_pad(min(t + r, n - 1))];
       }
-      float4* dst = reinterpret_cast<float4*>(buf) + rq * HD + 2 * dp;
-      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
-      dst[1] = make_float4(b[0], b[1], b[2], b[3]);
+      float4* dst = reinterpret_cast<float4*>(buf) + rq * C::QS + 9 * pc;
+#pragma unroll
+      for (int w = 0; w < 4; w++) {  // dims 8pc + 2w, 8pc + 2w + 1
+        float a[4], b[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t word = w == 0 ? vr[kk][r].x : w == 1 ? vr[kk][r].y : w == 2 ? vr[kk][r].z : vr[kk][r].w;
+          a[r] = live[r] ? p[r] * f16_operand(static_cast<uint16_t>(word & 0xffffu)) : 0.0f;
+          b[r] = live[r] ? p[r] * f16_operand(static_cast<uint16_t>(word >> 16)) : 0.0f;
+        }
+        dst[2 * w] = make_float4(a[0], a[1], a[2], a[3]);
+        dst[2 * w + 1] = make_float4(b[0], b[1], b[2], b[3]);
+      }
     }
   };
   float acc = 0.0f;
@@ -1033,12 +1047,12 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   __syncthreads();
   for (int c = 0; c < n_chunks; c++) {
     if (folder) {
-      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid;
+      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid + tid / 8;
 #pragma unroll
       for (int g = 0; g < C::CH / 32; g++) {
         float4 x[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; jj++) x[jj] = src[(g * 8 + jj) * HD];
+        for (int jj = 0; jj < 8; jj++) x[jj] = src[(g * 8 + jj) * C::QS];
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) {
           acc += x[jj].x;
