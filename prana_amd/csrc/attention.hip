@@ -945,6 +945,9 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   __shared__ __align__(16) float s_q[HD];
   __shared__ float s_red[kWideNT / 64];
   __shared__ __align__(16) float s_p[C::SC];
+  // windows of up to kPadSerialMax rows: the exponentials again, contiguous
+  // and zero-padded, for the one-lane fold on 16-byte loads
+  __shared__ __align__(16) float s_e[exact::lane_pad(exact::kPadSerialMax)];
   __shared__ __align__(16) float s_prod[2][C::CH / 4 * C::QS * 4];
   const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
   const int n = pos0 + i + 1;  // <= kWideMax rows
@@ -978,9 +981,14 @@ __global__ __launch_bounds__(kWideNT) void attn_wide_kernel(const float* __restr
   float e1 = 0.0f, e2 = 0.0f;
   if (t1 < n) s_p[exact::run_pad(t1)] = e1 = dev_expf(s_p[exact::run_pad(t1)] - mx);
   if (t2 < n) s_p[exact::run_pad(t2)] = e2 = dev_expf(s_p[exact::run_pad(t2)] - mx);
+  const bool short_row = n <= exact::kPadSerialMax;  // uniform
+  if (short_row && t1 < exact::lane_pad(n)) s_e[t1] = t1 < n ? e1 : 0.0f;  // lane_pad(896) < kWideNT
   __syncthreads();
-  // softmax sum in the reference's left-to-right order (norms.rs:53)
-  const float sum = exact::block_seq_sum_short<kWideNT>([](int t) { return s_p[exact::run_pad(t)]; }, n);
+  // softmax sum in the reference's left-to-right order (norms.rs:53): one
+  // lane's chain over the padded row when it is short (~4 ns a term, against
+  // the scan's fixed ~4.5 us), the exact scan otherwise
+  const float sum = short_row ? exact::block_seq_sum_nonneg<kWideNT, true>(s_e, n)
+                              : exact::block_seq_sum_short<kWideNT>([](int t) { return s_p[exact::run_pad(t)]; }, n);
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
   if (t1 < n) s_p[exact::run_pad(t1)] = e1 * inv;
   if (t2 < n) s_p[exact::run_pad(t2)] = e2 * inv;

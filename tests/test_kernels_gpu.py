@@ -553,8 +553,11 @@ def test_attention_decode_special_values(pos):
 
 @pytest.mark.parametrize("nh,nkv,hd,pos0,seq", [(32, 8, 128, 512, 9), (32, 8, 128, 3000, 8), (32, 8, 128, 2040, 9),
                                                  (14, 2, 64, 2046, 3), (32, 8, 128, 2040, 7), (32, 8, 128, 250, 9),
-                                                 (14, 2, 64, 700, 5)])
+                                                 (14, 2, 64, 700, 5), (14, 2, 64, 1500, 5), (32, 8, 128, 892, 5)])
 def test_attention_verify(nh, nkv, hd, pos0, seq):
+    # Verify rows over windows of 256..2047 rows take the wide kernel: its
+    # softmax sum is one lane's chain over a padded row up to 896 rows and the
+    # exact scan beyond (892 + 5: rows 893..897 straddle the switch).
     kc, vc = _cache(pos0 + seq, nkv, hd, 4)
     q = rng(5).standard_normal(seq * nh * hd).astype(np.float32)
     assert same_bits(P.attention_verify(q, kc, vc, pos0, seq, nh, nkv, hd),
