@@ -641,10 +641,13 @@ __global__ __launch_bounds__(kSmNT) void attn_split_softmax(float* __restrict__ 
 }
 
 // grid: (n_heads * HD/64, n_q). Folder lane d (wave 0) owns dim 64*slice + d;
-// producer lane (waves 1..4) tasks = (row quad, dim pair). Products of a
-// chunk of CH rows sit in LDS as [row/4][dim][row%4] so the folder reads four
-// rows of its dim with one 16-byte load. Rows past n are zero products, which
-// leave the fold (started from +0.0) unchanged.
+// a producer task (waves 1..8) is one row quad of one 8-dim piece: four
+// 16-byte V loads (with one 4-byte word per load, the producers' loads set
+// the pace: ~4x the load instructions). Products of a chunk of CH rows sit in
+// LDS as [row/4][dim][row%4], a pad word after every 8 dims so that
+// neighbouring pieces' 16-byte stores fall on different banks; the folder
+// reads four rows of its dim with one 16-byte load. Rows past n are zero
+// products, which leave the fold (started from +0.0) unchanged.
 template <int HD, int CH>
 __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__ prob, int sc_stride,
                                                        const uint16_t* __restrict__ v, int pos0,
@@ -653,12 +656,11 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
                                                        int8_t* __restrict__ qd, float* __restrict__ qsa,
                                                        int* __restrict__ qsum) {
   constexpr int NS = HD / 64;
-  constexpr int kTasks = CH / 4 * 32;  // (row quad, dim pair) per chunk
-  constexpr int kPer = kTasks / kPvProd;
-  constexpr int kQuadStep = kPvProd / 32;  // row quads between a lane's tasks
-  static_assert(kTasks % kPvProd == 0, "whole tasks per producer lane");
+  constexpr int kTasks = CH / 4 * 8;  // (row quad, 8-dim piece) per chunk
+  constexpr int kPer = (kTasks + kPvProd - 1) / kPvProd;
+  constexpr int QS = 64 + 8;          // float4 words per row quad: a pad word after every 8 dims
   static_assert(kSplitRows % CH == 0, "probability reads of the last chunk stay inside the scratch row");
-  __shared__ __align__(16) float s_prod[2][CH * 64];
+  __shared__ __align__(16) float s_prod[2][CH / 4 * QS * 4];
   const int lb = logical_block(n_heads * NS);
   const int h = lb / NS, slice = lb % NS, i = blockIdx.y;
   const int n = (pos_dev ? *pos_dev : pos0) + i + 1;
@@ -668,49 +670,45 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
   const int n_chunks = (n + CH - 1) / CH;
   const bool folder = tid < 64;
   const int pl = tid - 64;
-  const int dp = pl & 31, rq0 = pl >> 5;
-  // this lane's dim pair in row 0, and its probabilities
-  const uint32_t* vlane = reinterpret_cast<const uint32_t*>(v + (size_t)kvh * HD + slice * 64) + dp;
-  const float* plane = prob + ((size_t)i * n_heads + h) * sc_stride + 4 * rq0;
+  // this head's 64-dim slice of V, and its probability row
+  const uint16_t* vs = v + (size_t)kvh * HD + slice * 64;
+  const size_t kv_stride = 2 * (size_t)kv_words;  // a cache row in f16 values
+  const float* prow = prob + ((size_t)i * n_heads + h) * sc_stride;
 
-  uint32_t vr[kPer][4];
+  uint4 vr[kPer][4];
   float4 pr[kPer];
   auto fetch = [&](int c) {
-    const int tq = c * CH + 4 * rq0;  // first row of task 0
-    if (c * CH + CH <= n) {           // whole chunk: no clamping
 #pragma unroll
-      for (int k = 0; k < kPer; k++) {
-        const uint32_t* r0 = vlane + (size_t)(tq + 4 * kQuadStep * k) * kv_words;
-        pr[k] = *reinterpret_cast<const float4*>(plane + c * CH + 4 * kQuadStep * k);
+    for (int k = 0; k < kPer; k++) {
+      const int task = min(pl + kPvProd * k, kTasks - 1);
+      const int pc = task % 8, t = c * CH + 4 * (task / 8);
+      pr[k] = *reinterpret_cast<const float4*>(prow + t);  // t + 3 < sc_stride
 #pragma unroll
-        for (int r = 0; r < 4; r++) vr[k][r] = r0[(size_t)r * kv_words];
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < kPer; k++) {
-        const int t = tq + 4 * kQuadStep * k;
-        pr[k] = *reinterpret_cast<const float4*>(plane + c * CH + 4 * kQuadStep * k);  // t + 3 < sc_stride
-#pragma unroll
-        for (int r = 0; r < 4; r++) vr[k][r] = vlane[(size_t)min(t + r, n - 1) * kv_words];  // rows past n: unused
-      }
+      for (int r = 0; r < 4; r++)  // rows past n: clamped, unused
+        vr[k][r] = *reinterpret_cast<const uint4*>(vs + (size_t)min(t + r, n - 1) * kv_stride + 8 * pc);
     }
   };
   auto produce = [&](int c, float* buf) {
-    const int tq = c * CH + 4 * rq0;
 #pragma unroll
     for (int k = 0; k < kPer; k++) {
-      const int t = tq + 4 * kQuadStep * k;
+      const int task = pl + kPvProd * k;
+      if (task >= kTasks) break;
+      const int pc = task % 8, rq = task / 8, t = c * CH + 4 * rq;
       const float pv[4] = {pr[k].x, pr[k].y, pr[k].z, pr[k].w};
-      float a[4], b[4];
+      float4* dst = reinterpret_cast<float4*>(buf) + rq * QS + 9 * pc;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const bool live = t + r < n;
-        a[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(vr[k][r] & 0xffffu)) : 0.0f;
-        b[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(vr[k][r] >> 16)) : 0.0f;
+      for (int w = 0; w < 4; w++) {  // dims 8pc + 2w, 8pc + 2w + 1
+        float a[4], b[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t word = w == 0 ? vr[k][r].x : w == 1 ? vr[k][r].y : w == 2 ? vr[k][r].z : vr[k][r].w;
+          const bool live = t + r < n;
+          a[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(word & 0xffffu)) : 0.0f;
+          b[r] = live ? pv[r] * f16_operand(static_cast<uint16_t>(word >> 16)) : 0.0f;
+        }
+        dst[2 * w] = make_float4(a[0], a[1], a[2], a[3]);
+        dst[2 * w + 1] = make_float4(b[0], b[1], b[2], b[3]);
       }
-      float4* dst = reinterpret_cast<float4*>(buf) + (rq0 + kQuadStep * k) * 64 + 2 * dp;
-      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
-      dst[1] = make_float4(b[0], b[1], b[2], b[3]);
     }
   };
 
@@ -726,15 +724,15 @@ __global__ __launch_bounds__(kPvNT) void attn_split_pv(const float* __restrict__
       // groups of 8 row quads; the next group's reads are issued before this
       // group's adds, and the empty asm (consuming acc, ordering memory)
       // keeps later reads from being hoisted further
-      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid;
+      const float4* src = reinterpret_cast<const float4*>(s_prod[c & 1]) + tid + tid / 8;
       float4 x[8], y[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = src[j * 64];
+      for (int j = 0; j < 8; j++) x[j] = src[j * QS];
 #pragma unroll
       for (int g = 0; g < CH / 32; g++) {
         if (g + 1 < CH / 32) {
 #pragma unroll
-          for (int j = 0; j < 8; j++) y[j] = src[((g + 1) * 8 + j) * 64];
+          for (int j = 0; j < 8; j++) y[j] = src[((g + 1) * 8 + j) * QS];
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
