@@ -3310,10 +3310,20 @@ bool gemv_batch_skinny(const DevMat& m, size_t n_tok) {
   return n_tok >= 3 && n_tok < kGemvSkinnyMinTokens && m.rows * (m.cols / 32) >= kSkinnyMinBlocks;
 }
 
+// A single matrix of 512K+ blocks below 8192 rows (the block-split form of
+// the skinny kernel) also takes it at 3..8 tokens: the 7B wo at 5 tokens 6.7
+// against 7.7 us on the decode tiles. (Q|K|V, a multi-matrix launch with its
+// RoPE epilogue, stays on the tiles: as one matrix its 6144 rows took 12.6
+// against 9.7 us.)
+bool gemv_verify_block_split(const DevMat& m, size_t n_tok) {
+  return (m.kind == kKindQ8F || m.kind == kKindQ8_0 || m.kind == kKindQ4_0) && n_tok >= 3 && n_tok <= 8 &&
+         m.rows < 8192 && m.rows * (m.cols / 32) >= 512 * 1024;
+}
+
 int launch_gemv(const DevMat& m, const float* x, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
                 const GemvOut& o, hipStream_t s) {
   if (n_tok == 0 || m.rows == 0) return kOk;
-  if (gemv_batch_skinny(m, n_tok)) {
+  if (gemv_batch_skinny(m, n_tok) || gemv_verify_block_split(m, n_tok)) {
     switch (m.kind) {
       case kKindQ8F: return launch_gemm_skinny<kKindQ8F>(&m, &o, 1, q, sa, sums, n_tok, s);
       case kKindQ8_0: return launch_gemm_skinny<kKindQ8_0>(&m, &o, 1, q, sa, sums, n_tok, s);
