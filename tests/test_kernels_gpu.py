@@ -236,7 +236,7 @@ def _adversarial_rows(dim, seed):
     return np.stack(rows)
 
 
-@pytest.mark.parametrize("dim", [32, 288, 512, 544, 1000, 3072, 4096, 4128, 14336, 16320, 16384, 20000])
+@pytest.mark.parametrize("dim", [32, 288, 512, 544, 1000, 2080, 3072, 4096, 4128, 14336, 16320, 16384, 20000])
 def test_rmsnorm_adversarial(dim):
     x = _adversarial_rows(dim, dim)
     w = np.ones(dim, np.float32)
