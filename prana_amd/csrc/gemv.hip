@@ -2481,9 +2481,10 @@ __global__ __launch_bounds__(64 * RW * TT) void gemm_skinny_kernel(SkJob job, co
 // what bounds the stream (4 waves: 8 KB per CU, ~1.3 TB/s over the chip),
 // so the workgroup is as wide as the LDS allows. Tokens past n_tok load
 // nothing: their columns of the products are never stored.
-constexpr int kKsWaves = 8;
-
-template <int KIND>
+// A batch of more than one token tile has a workgroup per (row tile, token
+// tile): there two four-wave workgroups per CU (70 KB each) beat one of
+// eight (4096 x 14336 at 64 tokens: 73.0 against 82.7 us).
+template <int KIND, int kKsWaves>
 __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m, const int8_t* __restrict__ q,
                                                                       const float* __restrict__ sa,
                                                                       const int* __restrict__ sums, int n_tok,
@@ -2622,21 +2623,28 @@ __global__ __launch_bounds__(64 * kKsWaves) void gemm_skinny_ks_kernel(DevMat m,
   if (folder && n_row < R && tok0 + ft < n_tok) store_out(o, tok0 + ft, n_row, acc);
 }
 
-template <int KIND>
-int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
-                     const GemvOut& o, hipStream_t s) {
+template <int KIND, int W>
+int launch_skinny_ks_w(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                       const GemvOut& o, hipStream_t s) {
   using L = SkLayout<KIND, 1, 1>;
-  constexpr int kBytes = kKsWaves * L::SM_OFF + kKsWaves * kSkCB * 20 * 16 * 4;
+  constexpr int kBytes = W * L::SM_OFF + W * kSkCB * 20 * 16 * 4;
   static_assert(kBytes <= 160 * 1024, "one workgroup's staging and terms fit a CU's LDS");
   static const bool attr_ok = [] {
     return kBytes <= 65536 ||
-           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND>), kBytes);
+           set_max_dynamic_lds(reinterpret_cast<const void*>(gemm_skinny_ks_kernel<KIND, W>), kBytes);
   }();
   PRANA_CHECK(attr_ok, "gemm_skinny: LDS size not granted");
-  hipLaunchKernelGGL(gemm_skinny_ks_kernel<KIND>, dim3((m.rows + 15) / 16, (n_tok + 15) / 16), dim3(64 * kKsWaves),
+  hipLaunchKernelGGL((gemm_skinny_ks_kernel<KIND, W>), dim3((m.rows + 15) / 16, (n_tok + 15) / 16), dim3(64 * W),
                      kBytes, s, m, q, sa, sums, (int)n_tok, o);
   PRANA_LAUNCH_CHECK();
   return kOk;
+}
+
+template <int KIND>
+int launch_skinny_ks(const DevMat& m, const int8_t* q, const float* sa, const int* sums, size_t n_tok,
+                     const GemvOut& o, hipStream_t s) {
+  if (n_tok <= 16) return launch_skinny_ks_w<KIND, 8>(m, q, sa, sums, n_tok, o, s);
+  return launch_skinny_ks_w<KIND, 4>(m, q, sa, sums, n_tok, o, s);
 }
 
 template <int KIND, int RW, int TT>
